@@ -1,0 +1,363 @@
+"""LEAFDC02..07 decoder artifacts: writer for seeded synthetic models, and reader.
+
+The byte layout is Leaf's (writer: tools/export_decoder.py:22-25, 213-420;
+reader: engine/src/decoder.cpp:787-933).  It has to be identical, because the
+reference CPU decoder and this library's GPU decoder must load the very same
+file.  Weights are drawn from a seeded numpy generator instead of a Hugging
+Face snapshot: there is no network here, and the tests and benchmarks need
+models of exact architectural shape with random-init weights.
+
+Quantization follows export_decoder.quantize (tools/export_decoder.py:91-105):
+symmetric, ``s = max(absmax_group / limit, 1e-12)`` in float32,
+``q = clip(rint(w / s), -limit, limit)``; INT4 packs the even column in the low
+nibble.  Every payload starts on a 64-byte boundary relative to ``data_base``.
+"""
+from __future__ import annotations
+
+import dataclasses
+import struct
+from pathlib import Path
+from typing import Iterable
+
+import numpy as np
+
+HEADER = struct.Struct("<8sIIQ10Iff8If")        # export_decoder.py:23, read at decoder.cpp:795-808
+OPERATOR_METADATA = struct.Struct("<3I")        # export_decoder.py:24, read at decoder.cpp:823-838
+DESCRIPTOR = struct.Struct("<5I4Q")             # export_decoder.py:25, read at decoder.cpp:858-890
+NO_EOS = 0xFFFFFFFF
+
+NORM_RMS, NORM_LAYER = 0, 1
+ACT_SILU, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU = 0, 1, 2, 3
+POS_ROPE, POS_LEARNED, POS_NONE = 0, 1, 2
+
+LAYER_MATRICES = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                  "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+@dataclasses.dataclass
+class DecoderSpec:
+    """Header semantics plus storage policy of one decoder artifact."""
+    hidden: int
+    intermediate: int
+    heads: int
+    kv_heads: int
+    layers: int
+    vocab: int
+    max_positions: int
+    head_dim: int
+    eos: int = NO_EOS
+    sliding_window: int = 0
+    theta: float = 10000.0
+    epsilon: float = 1e-5
+    norm: int = NORM_RMS
+    activation: int = ACT_SILU
+    position: int = POS_ROPE
+    gated: int = 1
+    parallel_residual: int = 0
+    rotary_dim: int | None = None
+    position_offset: int = 0
+    final_norm: int = 1
+    embedding_scale: float = 1.0
+    eos_tokens: tuple[int, ...] = ()
+    qk_norm: int = 0
+    rope_frequencies: tuple[float, ...] = ()
+    # storage policy
+    bits: int = 32                  # 32, 8 or 4 for ".weight" matrices with rows > 1
+    group_size: int = 64            # INT4 group (min(group, cols))
+    int8_group_size: int = 0        # 0 = one scale per row
+    keep_fp32: frozenset = frozenset()
+    source_bf16: bool = False       # v6: matrices stored as original BF16 bits
+    tied: bool = False              # lm_head shares the embedding payload
+    attention_bias: bool = False    # q/k/v(/o) projection biases
+    o_bias: bool = False
+    mlp_bias: bool = False
+    norm_bias: bool = False         # LayerNorm beta tensors
+    # random init
+    std: float = 0.02
+    bias_std: float = 0.0
+    norm_jitter: float = 0.0        # 0 keeps gamma = 1 exactly
+
+    @property
+    def rotary(self) -> int:
+        """Rotated width per head: the whole head for RoPE unless set explicitly."""
+        if self.rotary_dim is not None:
+            return self.rotary_dim
+        return self.head_dim if self.position == POS_ROPE else 0
+
+    @property
+    def qwidth(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kvwidth(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    def header_values(self) -> tuple:
+        return (self.hidden, self.intermediate, self.heads, self.kv_heads, self.layers, self.vocab,
+                self.max_positions, self.eos, self.head_dim, self.sliding_window,
+                float(self.theta), float(self.epsilon),
+                self.norm, self.activation, self.position, self.gated, self.parallel_residual,
+                self.rotary, self.position_offset, self.final_norm, float(self.embedding_scale))
+
+
+def tensor_shapes(spec: DecoderSpec) -> dict[str, tuple[int, int]]:
+    """Canonical tensors (tools/decoder_plan.py:408-427) plus the spec's biases."""
+    h, f = spec.hidden, spec.intermediate
+    shapes = {"model.embed_tokens.weight": (spec.vocab, h), "lm_head.weight": (spec.vocab, h)}
+    if spec.final_norm:
+        shapes["model.norm.weight"] = (1, h)
+    if spec.position == POS_LEARNED:
+        shapes["model.position_embeddings.weight"] = (spec.max_positions + spec.position_offset, h)
+    for i in range(spec.layers):
+        p = f"model.layers.{i}."
+        shapes.update({p + "input_layernorm.weight": (1, h), p + "post_attention_layernorm.weight": (1, h),
+                       p + "self_attn.q_proj.weight": (spec.qwidth, h),
+                       p + "self_attn.k_proj.weight": (spec.kvwidth, h),
+                       p + "self_attn.v_proj.weight": (spec.kvwidth, h),
+                       p + "self_attn.o_proj.weight": (h, spec.qwidth),
+                       p + "mlp.up_proj.weight": (f, h), p + "mlp.down_proj.weight": (h, f)})
+        if spec.gated:
+            shapes[p + "mlp.gate_proj.weight"] = (f, h)
+        if spec.qk_norm:
+            shapes[p + "self_attn.q_norm.weight"] = (1, spec.head_dim)
+            shapes[p + "self_attn.k_norm.weight"] = (1, spec.head_dim)
+    biases = {}
+    if spec.norm_bias and spec.final_norm:
+        biases["model.norm.bias"] = (1, h)
+    for i in range(spec.layers):
+        p = f"model.layers.{i}."
+        if spec.norm_bias:
+            biases[p + "input_layernorm.bias"] = (1, h)
+            biases[p + "post_attention_layernorm.bias"] = (1, h)
+        roles = []
+        if spec.attention_bias:
+            roles += ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"]
+        if spec.o_bias:
+            roles.append("self_attn.o_proj")
+        if spec.mlp_bias:
+            roles += (["mlp.gate_proj"] if spec.gated else []) + ["mlp.up_proj", "mlp.down_proj"]
+        for role in roles:
+            biases[p + role + ".bias"] = (1, shapes[p + role + ".weight"][0])
+    shapes.update(biases)
+    return shapes
+
+
+def quantize(array: np.ndarray, bits: int, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric per-group quantization (tools/export_decoder.py:91-105)."""
+    rows, cols = array.shape
+    if cols % group:
+        raise ValueError(f"input width {cols} is not divisible by group size {group}")
+    grouped = array.reshape(rows, cols // group, group)
+    limit = (1 << (bits - 1)) - 1
+    scales = np.maximum(np.max(np.abs(grouped), axis=-1) / limit, 1e-12).astype("<f4")
+    values = np.clip(np.rint(grouped / scales[..., None]), -limit, limit).astype(np.int8).reshape(rows, cols)
+    if bits == 4:
+        nibbles = values.astype(np.uint8) & 15
+        values = nibbles[:, 0::2] | (nibbles[:, 1::2] << 4)
+    return np.ascontiguousarray(values), np.ascontiguousarray(scales)
+
+
+def round_to_bf16(array: np.ndarray) -> np.ndarray:
+    """Round float32 to BF16 bits (round-to-nearest-even), returned as uint16."""
+    bits = np.ascontiguousarray(array, dtype=np.float32).view(np.uint32)
+    rounded = bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))
+    return (rounded >> np.uint32(16)).astype("<u2")
+
+
+def _bf16_matrix(name: str, rows: int, layers: int) -> bool:
+    """Tensor roles v6 may store as BF16 (decoder.cpp:93-115)."""
+    if rows <= 1:
+        return False
+    if name in ("lm_head.weight", "model.embed_tokens.weight", "model.position_embeddings.weight"):
+        return True
+    if not name.startswith("model.layers."):
+        return False
+    rest = name[len("model.layers."):]
+    index, _, role = rest.partition(".")
+    return index.isdigit() and int(index) < layers and role.removesuffix(".weight") in LAYER_MATRICES \
+        and role.endswith(".weight")
+
+
+def _precision(spec: DecoderSpec, name: str, rows: int) -> int:
+    # export_decoder.py:312-314
+    if spec.source_bf16 and _bf16_matrix(name, rows, spec.layers) and name not in spec.keep_fp32:
+        return 16
+    if name.endswith(".weight") and rows > 1 and name not in spec.keep_fp32:
+        return spec.bits
+    return 32
+
+
+def _version(spec: DecoderSpec) -> tuple[int, bytes]:
+    eos_list = list(spec.eos_tokens)
+    if spec.eos != NO_EOS and not eos_list:
+        eos_list = [spec.eos]
+    version = 4 if len(eos_list) > 1 else 3 if spec.sliding_window else 2
+    meta = struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list) if version == 4 else b""
+    storage = 0
+    if spec.source_bf16:
+        version = storage = 6
+        meta = struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list)
+    if spec.qk_norm or spec.rope_frequencies:
+        ext = OPERATOR_METADATA.pack(storage, spec.qk_norm, len(spec.rope_frequencies))
+        version = 7
+        meta = (ext + struct.pack(f"<{len(spec.rope_frequencies)}f", *spec.rope_frequencies)
+                + struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list))
+    return version, meta
+
+
+class _Init:
+    """Seeded per-tensor generator: the same (seed, name) always yields the same data."""
+
+    def __init__(self, spec: DecoderSpec, seed: int):
+        self.spec, self.seed = spec, seed
+
+    def __call__(self, name: str, rows: int, cols: int) -> np.ndarray:
+        spec = self.spec
+        digest = np.frombuffer(name.encode(), dtype=np.uint8).astype(np.uint64)
+        key = int((digest * (np.arange(digest.size, dtype=np.uint64) + 1)).sum() % (1 << 31))
+        rng = np.random.Generator(np.random.PCG64([self.seed, key, len(name)]))
+        if name.endswith("norm.weight"):
+            out = np.ones((rows, cols), np.float32)
+            if spec.norm_jitter:
+                out += rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(spec.norm_jitter)
+            return out
+        if name.endswith(".bias"):
+            if not spec.bias_std:
+                return np.zeros((rows, cols), np.float32)
+            return rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(spec.bias_std)
+        out = rng.standard_normal((rows, cols), dtype=np.float32)
+        out *= np.float32(spec.std)
+        return out
+
+
+def write_artifact(path: str | Path, spec: DecoderSpec, seed: int = 0) -> dict:
+    """Write a seeded random-init decoder artifact; returns a small report."""
+    path = Path(path)
+    version, meta = _version(spec)
+    shapes = tensor_shapes(spec)
+    init = _Init(spec, seed)
+    descriptors, shared, offset = [], {}, 0
+    for name, (rows, cols) in shapes.items():
+        precision = _precision(spec, name, rows)
+        group = (spec.int8_group_size or cols) if precision == 8 else \
+            min(spec.group_size, cols) if precision == 4 else 0
+        if precision == 8 and cols % group:
+            raise ValueError(f"INT8 group {group} must divide {cols}")
+        if precision == 4 and (cols % group or group % 2):
+            raise ValueError(f"INT4 group {group} must divide even width {cols}")
+        source = "model.embed_tokens.weight" if (spec.tied and name == "lm_head.weight") else name
+        identity = (source, rows, cols, precision, group)
+        if identity in shared:
+            descriptors.append((name, rows, cols, precision, group, *shared[identity], None))
+            continue
+        size = rows * cols * precision // 8
+        offset = (offset + 63) & ~63
+        data_offset = offset
+        offset += size
+        scales = rows * (cols // group) if precision in (4, 8) else 0
+        offset = (offset + 63) & ~63
+        scale_offset = offset
+        offset += scales * 4
+        shared[identity] = (data_offset, size, scale_offset, scales)
+        descriptors.append((name, rows, cols, precision, group, data_offset, size, scale_offset, scales, source))
+    metadata = HEADER.size + len(meta) + sum(4 + len(d[0].encode()) + DESCRIPTOR.size for d in descriptors)
+    base = (metadata + 63) & ~63
+    magic = f"LEAFDC0{version}".encode()
+    tmp = path.with_suffix(path.suffix + ".partial")
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with tmp.open("wb") as out:
+        out.write(HEADER.pack(magic, version, len(descriptors), base, *spec.header_values()))
+        out.write(meta)
+        for name, rows, cols, precision, group, start, size, scale_start, scales, _ in descriptors:
+            encoded = name.encode()
+            out.write(struct.pack("<I", len(encoded)) + encoded)
+            out.write(DESCRIPTOR.pack(2, rows, cols, precision, group, start, size, scale_start, scales))
+        end = base + offset
+        for name, rows, cols, precision, group, start, size, scale_start, scales, source in descriptors:
+            if source is None:
+                continue
+            array = init(source, rows, cols)
+            if precision == 32:
+                payload, scale_array = array.astype("<f4", copy=False), None
+            elif precision == 16:
+                payload, scale_array = round_to_bf16(array), None
+            else:
+                payload, scale_array = quantize(array, precision, group)
+            out.seek(base + start)
+            out.write(payload.tobytes())
+            if scales:
+                out.seek(base + scale_start)
+                out.write(scale_array.tobytes())
+        out.truncate(max(end, out.tell()))
+    tmp.replace(path)
+    return {"version": version, "tensor_count": len(descriptors), "bytes": path.stat().st_size,
+            "data_base": base}
+
+
+@dataclasses.dataclass
+class TensorInfo:
+    name: str
+    rows: int
+    cols: int
+    bits: int
+    group: int
+    offset: int
+    size: int
+    scale_offset: int
+    scale_count: int
+
+
+def read_tensor_table(path: str | Path) -> tuple[dict, dict[str, TensorInfo], int]:
+    """Parse the header and tensor table (no validation beyond structure)."""
+    blob = Path(path).read_bytes()[:1 << 24]
+    fields = HEADER.unpack_from(blob)
+    magic, version, count, base = fields[:4]
+    keys = ("hidden", "intermediate", "heads", "kv_heads", "layers", "vocab", "max_positions", "eos",
+            "head_dim", "sliding_window", "theta", "epsilon", "norm", "activation", "position", "gated",
+            "parallel_residual", "rotary_dim", "position_offset", "final_norm", "embedding_scale")
+    header = dict(zip(keys, fields[4:]))
+    header["version"] = version
+    pos = HEADER.size
+    if version == 7:
+        storage, qk, nfreq = OPERATOR_METADATA.unpack_from(blob, pos)
+        pos += 12
+        header.update(storage=storage, qk_norm=qk,
+                      rope_frequencies=list(struct.unpack_from(f"<{nfreq}f", blob, pos)))
+        pos += 4 * nfreq
+    if version >= 4:
+        (n,) = struct.unpack_from("<I", blob, pos)
+        header["eos_tokens"] = list(struct.unpack_from(f"<{n}I", blob, pos + 4))
+        pos += 4 + 4 * n
+    tensors = {}
+    for _ in range(count):
+        (length,) = struct.unpack_from("<I", blob, pos)
+        name = blob[pos + 4:pos + 4 + length].decode()
+        pos += 4 + length
+        rank, rows, cols, bits, group, off, size, soff, scount = DESCRIPTOR.unpack_from(blob, pos)
+        pos += DESCRIPTOR.size
+        tensors[name] = TensorInfo(name, rows, cols, bits, group, off, size, soff, scount)
+    return header, tensors, base
+
+
+def load_tensor(path: str | Path, name: str) -> tuple[np.ndarray, np.ndarray | None, TensorInfo]:
+    """Raw payload and scales of one tensor (memory-mapped)."""
+    _, tensors, base = read_tensor_table(path)
+    info = tensors[name]
+    raw = np.memmap(path, dtype=np.uint8, mode="r", offset=base + info.offset, shape=(info.size,))
+    dtype = {32: "<f4", 16: "<u2", 8: np.int8, 4: np.uint8}[info.bits]
+    data = np.asarray(raw).view(dtype)
+    data = data.reshape(info.rows, -1)
+    scales = None
+    if info.scale_count:
+        scales = np.asarray(np.memmap(path, dtype="<f4", mode="r", offset=base + info.scale_offset,
+                                      shape=(info.scale_count,))).reshape(info.rows, -1)
+    return data, scales, info
+
+
+def write_tokens(path: str | Path, requests: Iterable[Iterable[int]]) -> None:
+    """tokens.bin request file: u32 count, then {u32 len, u32 ids[len]} (main_decoder.cpp:196-210)."""
+    requests = [list(r) for r in requests]
+    with Path(path).open("wb") as out:
+        out.write(struct.pack("<I", len(requests)))
+        for ids in requests:
+            out.write(struct.pack(f"<I{len(ids)}I", len(ids), *ids))
