@@ -1,0 +1,98 @@
+// Device-side helpers shared by the decoder kernels (gfx950, wave64).
+//
+// The library is compiled with -ffp-contract=off: every fused multiply-add in
+// these kernels is spelled with fmaf(), so operation order is explicit wherever
+// results must match Leaf's CPU arithmetic bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace leafhip {
+
+constexpr int kWave = 64;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming load (non-temporal: weights are read once per forward).
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    const v4u v = __builtin_nontemporal_load(static_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Butterfly reductions across the 64 lanes of a wave; every lane gets the result.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Block-wide reductions for blockDim.x a multiple of 64 (<= 1024).
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, T* scratch, Op op, T (*wave_op)(T)) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    v = wave_op(v);
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    T r = scratch[0];
+    for (int w = 1; w < waves; ++w) r = op(r, scratch[w]);
+    return r;
+}
+
+// Symmetric int8 activation quantization of one value (decoder.cpp:618-627):
+// round half to even of x * multiplier, saturated to +-127.
+__device__ __forceinline__ int quantize_one(float x, float multiplier) {
+    float r = __builtin_rintf(x * multiplier);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+// Signed nibble (low nibble = even column) -> int.
+__device__ __forceinline__ int nibble(uint32_t byte, int high) {
+    int v = (byte >> (high * 4)) & 15;
+    return v >= 8 ? v - 16 : v;
+}
+
+// Four signed int8 packed in a 32-bit word, from eight signed nibbles'
+// low (even columns) or high (odd columns) halves of four bytes: used to widen
+// INT4 weights to the int8 lanes of v_dot4_i32_i8.
+__device__ __forceinline__ int widen_nibbles_lo(uint32_t w) {   // nibbles 0,2,4,6 -> bytes 0..3? (see callers)
+    uint32_t n = w & 0x0F0F0F0Fu;                                // low nibble of each byte
+    uint32_t s = (n & 0x08080808u) * 0x1Eu;                      // 0x08 -> 0xF0 sign extension
+    return (int)(n | s);
+}
+__device__ __forceinline__ int widen_nibbles_hi(uint32_t w) {
+    uint32_t n = (w >> 4) & 0x0F0F0F0Fu;
+    uint32_t s = (n & 0x08080808u) * 0x1Eu;
+    return (int)(n | s);
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace leafhip

@@ -1,0 +1,109 @@
+// Host-visible launch interface of the decoder kernels (gfx950).
+//
+// Each launcher validates nothing: callers (the C ABI and the decoder) check
+// shapes first.  All pointers are device pointers; `stream` is a hipStream_t.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace leafhip {
+
+// One weight matrix [rows, cols] as stored in a LEAFDC artifact (decoder.cpp:236-251):
+// bits 32 = f32, 16 = BF16 bits, 8 = int8, 4 = two signed nibbles per byte
+// (low nibble = even column); scales[row * (cols / group) + col / group] for 8/4.
+struct WeightView {
+    const void* data = nullptr;
+    const float* scales = nullptr;
+    const float* bias = nullptr;    // null adds 0.0f, as the CPU path does without a bias
+    int rows = 0, cols = 0, bits = 32, group = 0;
+};
+
+// Optional normalization applied to the input rows of a linear (decoder.cpp:706-727).
+struct NormView {
+    const float* gamma = nullptr;
+    const float* beta = nullptr;
+    float epsilon = 0.0f;
+    int kind = -1;                  // -1 none, 0 RMS, 1 LayerNorm
+    int accurate = 0;               // RMS square sum in double (accurate_fp32.h:6-13)
+};
+
+enum Epilogue : int {
+    kStore = 0,     // y = acc + bias
+    kAccumulate = 1 // y = y + (acc + bias)      (residual add, decoder.cpp:1390)
+};
+
+// Token-major activations use row stride == width unless stated.
+void launch_embedding(const WeightView& table, const WeightView* positions, const uint32_t* ids, int tokens,
+                      int position_base, float scale, float* hidden, hipStream_t stream);
+void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream);
+void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream);
+void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y,
+                          hipStream_t stream);
+
+// y[t, row] for t < tokens.  integer_activations selects W8A8/W4A8 (bits 8/4):
+// then either x (f32, quantized per token inside the kernel) or xq/xs (given).
+// acc_out, when not null, receives the exact int32 group accumulators
+// [tokens][rows][cols/group] (integer path only).
+struct LinearCall {
+    WeightView w;
+    const float* x = nullptr;
+    const int8_t* xq = nullptr;
+    const float* xs = nullptr;
+    NormView norm;                  // applied to x first (integer path, tokens == 1 only)
+    int tokens = 1;
+    bool integer_activations = false;
+    float* y = nullptr;
+    int epilogue = kStore;
+    int32_t* acc_out = nullptr;
+    int8_t* xq_scratch = nullptr;   // [tokens, cols] when the GEMM path quantizes
+    float* xs_scratch = nullptr;    // [tokens]
+    float* norm_scratch = nullptr;  // [tokens, cols] when `norm` cannot be fused into the kernel
+    int force_path = 0;             // 0 auto, 1 GEMV, 2 generic, 3 GEMM
+};
+// Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
+// the call cannot run (missing scratch for the GEMM quantization).
+int launch_linear(const LinearCall& call, hipStream_t stream);
+
+// RoPE + head-major reorder + KV append for `tokens` new tokens at `position`.
+// qkv is [tokens, qwidth + 2 * kvwidth]; q_heads gets [heads, tokens, dim];
+// key/value caches are [kv_heads, capacity, dim].
+struct RopeKvCall {
+    const float* qkv = nullptr;
+    int ld = 0;                     // row stride of qkv
+    int q_offset = 0, k_offset = 0, v_offset = 0;
+    int tokens = 0, heads = 0, kv_heads = 0, dim = 0, rotary = 0;
+    int position = 0;
+    const float* cosines = nullptr; // [positions, rotary/2] tables built on the host
+    const float* sines = nullptr;
+    float* q_heads = nullptr;
+    float* keys = nullptr;
+    float* values = nullptr;
+    int capacity = 0;
+};
+void launch_rope_kv(const RopeKvCall& call, hipStream_t stream);
+
+// Causal (optionally sliding-window) GQA attention of `tokens` queries at
+// positions [position, position+tokens) over keys [0, position+tokens).
+struct AttentionCall {
+    const float* q_heads = nullptr; // [heads, tokens, dim]
+    const float* keys = nullptr;    // [kv_heads, capacity, dim]
+    const float* values = nullptr;
+    float* out = nullptr;           // [tokens, heads * dim]
+    int heads = 0, kv_heads = 0, tokens = 0, position = 0, dim = 0, capacity = 0, window = 0;
+    float scale = 1.0f;             // applied twice: (q.k * scale) * scale (decoder.cpp:1348)
+    float* partial = nullptr;       // split-K scratch (decode); may be null
+    int partial_capacity = 0;       // floats available in partial
+};
+void launch_attention(const AttentionCall& call, hipStream_t stream);
+
+// act = up * activate(gate) for gated MLPs, act = activate(up) otherwise.
+// gate_up holds [tokens, 2 * width] = [gate | up] when gated, [tokens, width] otherwise.
+void launch_activation(const float* gate_up, int tokens, int width, int gated, int activation, float* act,
+                       hipStream_t stream);
+// hidden = hidden + (a + (b ? b : 0))   (decoder.cpp:1434)
+void launch_residual(float* hidden, const float* a, const float* b, int count, hipStream_t stream);
+// index of the first maximum of each row (std::max_element, main_decoder.cpp:102)
+void launch_argmax(const float* logits, int rows, int width, uint32_t* out, hipStream_t stream);
+
+}  // namespace leafhip

@@ -1,0 +1,995 @@
+// Decoder kernels for MI355X (gfx950, CDNA4, wave64).
+//
+// Layout conventions (all device-resident, row-major):
+//   weights   [rows, cols] in their artifact storage (f32 / BF16 bits / int8 /
+//             signed nibbles), rows 16-byte aligned so a lane streams one
+//             128-bit chunk per load;
+//   hidden    [tokens, width] f32;
+//   KV cache  [kv_heads, capacity, dim] f32 per layer.
+// Decode GEMVs are HBM-bound: a wave owns whole rows, lanes stride over
+// 128-bit chunks of them (coalesced 1 KiB per wave load), and the dot product
+// is reduced across the wave with butterfly shuffles.  Prefill linears run on
+// MFMA (int8 for W8A8, f32 otherwise).
+#include "device_common.h"
+#include "kernels.h"
+
+#include <math.h>
+
+namespace leafhip {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float weight_value(const WeightView& w, int row, int col) {
+    const size_t index = (size_t)row * w.cols + col;
+    if (w.bits == 32) return ((const float*)w.data)[index];
+    if (w.bits == 16) return bf16_to_f32(((const uint16_t*)w.data)[index]);
+    int q;
+    if (w.bits == 8) q = ((const int8_t*)w.data)[index];
+    else q = nibble(((const uint8_t*)w.data)[index / 2], (int)(index & 1));
+    return (float)q * w.scales[(size_t)row * (w.cols / w.group) + col / w.group];
+}
+
+__device__ __forceinline__ float bias_at(const WeightView& w, int row) {
+    return w.bias ? w.bias[row] : 0.0f;
+}
+
+__device__ __forceinline__ int weight_int(const WeightView& w, int row, int col) {
+    const size_t index = (size_t)row * w.cols + col;
+    if (w.bits == 8) return ((const int8_t*)w.data)[index];
+    return nibble(((const uint8_t*)w.data)[index / 2], (int)(index & 1));
+}
+
+// ------------------------------------------------------------ embedding ---
+__global__ void embedding_kernel(WeightView table, WeightView positions, int use_positions, const uint32_t* ids,
+                                 int position_base, float scale, float* hidden) {
+    const int t = blockIdx.x;
+    const int id = (int)ids[t];
+    const int h = table.cols;
+    for (int c = threadIdx.x; c < h; c += blockDim.x) {
+        float v = weight_value(table, id, c) * scale;
+        if (use_positions) v = v + weight_value(positions, position_base + t, c);
+        hidden[(size_t)t * h + c] = v;
+    }
+}
+
+// ----------------------------------------------------------------- norm ---
+// Per-row statistics of a normalization over `width` values (decoder.cpp:706-727).
+// The sums are tree reductions (the CPU path sums left to right).
+struct NormStats { float mean, scale; };
+
+__device__ NormStats block_norm_stats(const float* in, int width, const NormView& norm, float* scratch) {
+    float mean = 0.0f;
+    if (norm.kind == 1) {
+        float s = 0.0f;
+        for (int c = threadIdx.x; c < width; c += blockDim.x) s += in[c];
+        s = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
+        mean = s / (float)width;
+    }
+    float square;
+    if (norm.kind == 0 && norm.accurate) {
+        double s = 0.0;
+        for (int c = threadIdx.x; c < width; c += blockDim.x) { const float v = in[c] * in[c]; s += (double)v; }
+        __shared__ double dscratch[16];
+        s = block_reduce<double>(s, dscratch, [](double a, double b) { return a + b; }, wave_sum_f64);
+        square = (float)s;
+    } else {
+        float s = 0.0f;
+        for (int c = threadIdx.x; c < width; c += blockDim.x) { const float v = in[c] - mean; s += v * v; }
+        square = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
+    }
+    NormStats st;
+    st.mean = mean;
+    st.scale = 1.0f / sqrtf(square / (float)width + norm.epsilon);
+    return st;
+}
+
+__device__ __forceinline__ float apply_norm(float x, int c, const NormStats& st, const NormView& norm) {
+    return (x - st.mean) * st.scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+}
+
+__global__ __launch_bounds__(kBlock) void norm_kernel(const float* x, int width, NormView norm, float* y) {
+    __shared__ float scratch[16];
+    const float* in = x + (size_t)blockIdx.x * width;
+    float* out = y + (size_t)blockIdx.x * width;
+    const NormStats st = block_norm_stats(in, width, norm, scratch);
+    for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = apply_norm(in[c], c, st, norm);
+}
+
+// ------------------------------------------------------------- quantize ---
+// Per-token symmetric int8 quantization (decoder.cpp:1028-1043).
+__global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, int width, int8_t* q, float* scales) {
+    __shared__ float scratch[16];
+    const float* in = x + (size_t)blockIdx.x * width;
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) m = fmaxf(m, fabsf(in[c]));
+    m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    const float s = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / s;
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = (int8_t)quantize_one(in[c], multiplier);
+}
+
+__global__ void scale_columns_kernel(const float* x, int width, size_t count, const float* factors, float* y) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = x[i] * factors[i % width];
+}
+
+// --------------------------------------------------------- GEMV helpers ---
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
+}
+// Even / odd columns of eight consecutive int8 values held in two words, so a
+// word of INT4 weights widened with widen_nibbles_lo/hi lines up with them.
+__device__ __forceinline__ uint32_t even_bytes(uint32_t w0, uint32_t w1) {
+    return (w0 & 0x000000FFu) | ((w0 >> 8) & 0x0000FF00u) | ((w1 << 16) & 0x00FF0000u) | ((w1 << 8) & 0xFF000000u);
+}
+__device__ __forceinline__ uint32_t odd_bytes(uint32_t w0, uint32_t w1) {
+    return ((w0 >> 8) & 0x000000FFu) | ((w0 >> 16) & 0x0000FF00u) | ((w1 << 8) & 0x00FF0000u) | (w1 & 0xFF000000u);
+}
+
+// Exact W8A8 epilogue for one group per row: ((float)acc * s_x) * s_w, then
+// + bias (decoder.cpp:568, 1229).  Separate roundings, as in the CPU path.
+__device__ __forceinline__ float int_epilogue(int acc, float sx, float sw) {
+    const float term = (float)acc * sx;
+    return term * sw;
+}
+
+__device__ __forceinline__ void store_out(float* y, size_t index, float value, float bias, int epilogue) {
+    const float v = value + bias;
+    if (epilogue == kAccumulate) y[index] = y[index] + v;
+    else y[index] = v;
+}
+
+// Integer dot of one 16-byte weight chunk with the matching activation words.
+template <int BITS>
+__device__ __forceinline__ int chunk_dot(const uint4 wv, const uint32_t* xw, int acc) {
+    if constexpr (BITS == 8) {
+        acc = dot4((int)wv.x, (int)xw[0], acc);
+        acc = dot4((int)wv.y, (int)xw[1], acc);
+        acc = dot4((int)wv.z, (int)xw[2], acc);
+        acc = dot4((int)wv.w, (int)xw[3], acc);
+    } else {
+        const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc = dot4(widen_nibbles_lo(words[k]), (int)xw[2 * k], acc);
+            acc = dot4(widen_nibbles_hi(words[k]), (int)xw[2 * k + 1], acc);
+        }
+    }
+    return acc;
+}
+
+// ------------------------------------------ W8A8/W4A8 decode GEMV (fused) ---
+// One token.  Every wave normalizes (optionally) and quantizes the whole input
+// row itself from L2-resident activations (each lane its own chunks), so no
+// separate quantization launch or grid-wide barrier is needed.  Weight loads
+// are issued first and overlap the prologue.  One group per row.
+template <int BITS, int RPW, int MAXJ>
+__global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, const float* __restrict__ x, NormView norm,
+                                                               float* __restrict__ y, int epilogue,
+                                                               int32_t* __restrict__ acc_out) {
+    constexpr int E = BITS == 8 ? 16 : 32;          // weight values per 16-byte chunk
+    constexpr int XW = E / 4;                       // activation words per chunk
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, nch = K / E;
+    const int row_first = (blockIdx.x * (kBlock / kWave) + wave) * RPW;
+    if (row_first >= w.rows) return;
+
+    uint4 wv[RPW][MAXJ];
+    const uint8_t* base = (const uint8_t*)w.data;
+    const size_t row_bytes = (size_t)K * BITS / 8;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = min(row_first + r, w.rows - 1);
+        const uint4* rp = (const uint4*)(base + (size_t)row * row_bytes);
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + kWave * j;
+            wv[r][j] = c < nch ? load_stream16(rp + c) : make_uint4(0, 0, 0, 0);
+        }
+    }
+
+    // Prologue: normalization statistics over the row (wave-wide).
+    float mean = 0.0f, nscale = 1.0f;
+    if (norm.kind >= 0) {
+        if (norm.kind == 1) {
+            float s = 0.0f;
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + kWave * j;
+                if (c < nch)
+                    for (int e = 0; e < E; ++e) s += x[c * E + e];
+            }
+            mean = wave_sum_f32(s) / (float)K;
+        }
+        float sq;
+        if (norm.kind == 0 && norm.accurate) {
+            double s = 0.0;
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + kWave * j;
+                if (c < nch)
+                    for (int e = 0; e < E; ++e) { const float v = x[c * E + e] * x[c * E + e]; s += (double)v; }
+            }
+            sq = (float)wave_sum_f64(s);
+        } else {
+            float s = 0.0f;
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + kWave * j;
+                if (c < nch)
+                    for (int e = 0; e < E; ++e) { const float v = x[c * E + e] - mean; s += v * v; }
+            }
+            sq = wave_sum_f32(s);
+        }
+        nscale = 1.0f / sqrtf(sq / (float)K + norm.epsilon);
+    }
+    auto input = [&](int col) -> float {
+        const float v = x[col];
+        if (norm.kind < 0) return v;
+        return (v - mean) * nscale * norm.gamma[col] + (norm.beta ? norm.beta[col] : 0.0f);
+    };
+    float amax = 0.0f;
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + kWave * j;
+        if (c < nch)
+            for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(input(c * E + e)));
+    }
+    amax = wave_max_f32(amax);
+    const float sx = fmaxf(amax / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+    uint32_t xq[MAXJ][XW];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + kWave * j;
+#pragma unroll
+        for (int k = 0; k < E / 8; ++k) {
+            int q[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = c < nch ? quantize_one(input(c * E + 8 * k + e), multiplier) : 0;
+            if constexpr (BITS == 8) {
+                xq[j][2 * k] = pack4(q[0], q[1], q[2], q[3]);
+                xq[j][2 * k + 1] = pack4(q[4], q[5], q[6], q[7]);
+            } else {
+                xq[j][2 * k] = pack4(q[0], q[2], q[4], q[6]);
+                xq[j][2 * k + 1] = pack4(q[1], q[3], q[5], q[7]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        int acc = 0;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) acc = chunk_dot<BITS>(wv[r][j], xq[j], acc);
+        acc = wave_sum_i32(acc);
+        const int row = row_first + r;
+        if (lane == 0 && row < w.rows) {
+            if (acc_out) acc_out[row] = acc;
+            store_out(y, row, int_epilogue(acc, sx, w.scales[row]), bias_at(w, row), epilogue);
+        }
+    }
+}
+
+// --------------------------------------- W8A8/W4A8 GEMV, given int8 input ---
+// Up to four tokens with activations already quantized (xq [T, K], xs [T]).
+template <int BITS, int T, int RPW>
+__global__ __launch_bounds__(kBlock) void gemv_int_kernel(WeightView w, const int8_t* __restrict__ xq,
+                                                         const float* __restrict__ xs, float* __restrict__ y,
+                                                         int epilogue, int32_t* __restrict__ acc_out) {
+    constexpr int E = BITS == 8 ? 16 : 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, nch = K / E;
+    const int row_first = (blockIdx.x * (kBlock / kWave) + wave) * RPW;
+    if (row_first >= w.rows) return;
+    const uint8_t* base = (const uint8_t*)w.data;
+    const size_t row_bytes = (size_t)K * BITS / 8;
+    int acc[RPW][T];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[r][t] = 0;
+    for (int c = lane; c < nch; c += kWave) {
+        uint32_t xw[T][E / 4];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint4* xp = (const uint4*)(xq + (size_t)t * K + (size_t)c * E);
+            if constexpr (BITS == 8) {
+                const uint4 v = xp[0];
+                xw[t][0] = v.x; xw[t][1] = v.y; xw[t][2] = v.z; xw[t][3] = v.w;
+            } else {
+                const uint4 a = xp[0], b = xp[1];
+                const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    xw[t][2 * k] = even_bytes(words[2 * k], words[2 * k + 1]);
+                    xw[t][2 * k + 1] = odd_bytes(words[2 * k], words[2 * k + 1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = min(row_first + r, w.rows - 1);
+            const uint4 wv = load_stream16((const uint4*)(base + (size_t)row * row_bytes) + c);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[r][t] = chunk_dot<BITS>(wv, xw[t], acc[r][t]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row_first + r;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int a = wave_sum_i32(acc[r][t]);
+            if (lane == 0 && row < w.rows) {
+                if (acc_out) acc_out[(size_t)t * w.rows + row] = a;
+                store_out(y, (size_t)t * w.rows + row, int_epilogue(a, xs[t], w.scales[row]), bias_at(w, row), epilogue);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------ FP decode GEMV family ---
+// FP32, BF16-source and weight-only INT8 / INT4 (W8A32, W4A32) for up to four
+// tokens.  Quantized weights accumulate q * x per scale group and apply the
+// group scale once per group, as the CPU kernels do; the summation order is
+// the wave's, not the CPU's, so results agree to rounding.
+template <int BITS, int T, int RPW>
+__global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const float* __restrict__ x,
+                                                        float* __restrict__ y, int epilogue) {
+    constexpr int E = 128 / BITS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, nch = K / E;
+    const int row_first = (blockIdx.x * (kBlock / kWave) + wave) * RPW;
+    if (row_first >= w.rows) return;
+    const uint8_t* base = (const uint8_t*)w.data;
+    const size_t row_bytes = (size_t)K * BITS / 8;
+    const int groups = (BITS == 8 || BITS == 4) ? K / w.group : 1;
+    // Values of one chunk that share a scale: the whole chunk, or group-sized pieces.
+    const int piece = (BITS == 8 || BITS == 4) ? min(E, w.group) : E;
+    float acc[RPW][T];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[r][t] = 0.0f;
+    for (int c = lane; c < nch; c += kWave) {
+        float xv[T][E];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float4* xp = (const float4*)(x + (size_t)t * K + (size_t)c * E);
+#pragma unroll
+            for (int k = 0; k < E / 4; ++k) {
+                const float4 v = xp[k];
+                xv[t][4 * k] = v.x; xv[t][4 * k + 1] = v.y; xv[t][4 * k + 2] = v.z; xv[t][4 * k + 3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = min(row_first + r, w.rows - 1);
+            const uint4 wv = load_stream16((const uint4*)(base + (size_t)row * row_bytes) + c);
+            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+            float wf[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (BITS == 32) wf[e] = __uint_as_float(words[e]);
+                else if constexpr (BITS == 16) wf[e] = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
+                else if constexpr (BITS == 8) wf[e] = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
+                else wf[e] = (float)nibble((words[e / 8] >> (8 * ((e / 2) & 3))) & 0xFFu, e & 1);
+            }
+            if constexpr (BITS == 32 || BITS == 16) {
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int e = 0; e < E; ++e) acc[r][t] = fmaf(wf[e], xv[t][e], acc[r][t]);
+            } else {
+                for (int p0 = 0; p0 < E; p0 += piece) {
+                    const float s = w.scales[(size_t)row * groups + (c * E + p0) / w.group];
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        float part = 0.0f;
+                        for (int e = p0; e < p0 + piece; ++e) part = fmaf(wf[e], xv[t][e], part);
+                        acc[r][t] = fmaf(part, s, acc[r][t]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row_first + r;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float a = wave_sum_f32(acc[r][t]);
+            if (lane == 0 && row < w.rows) store_out(y, (size_t)t * w.rows + row, a, bias_at(w, row), epilogue);
+        }
+    }
+}
+
+// ------------------------------------------------------ generic linear ---
+// Any shape and storage: one thread per (token, row), sequential over columns.
+// Integer activations reproduce the CPU epilogue exactly, groups in order
+// with the fused accumulate of quant_dot_avx (decoder.cpp:568).
+__global__ __launch_bounds__(kBlock) void linear_generic_kernel(WeightView w, const float* x, const int8_t* xq,
+                                                               const float* xs, int tokens, int integer,
+                                                               float* y, int epilogue, int32_t* acc_out) {
+    const size_t index = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (index >= (size_t)tokens * w.rows) return;
+    const int t = (int)(index / w.rows), row = (int)(index % w.rows);
+    const int K = w.cols;
+    float result = 0.0f;
+    if (integer) {
+        const int groups = K / w.group;
+        for (int g = 0; g < groups; ++g) {
+            int acc = 0;
+            for (int c = g * w.group; c < (g + 1) * w.group; ++c) acc += weight_int(w, row, c) * (int)xq[(size_t)t * K + c];
+            if (acc_out) acc_out[((size_t)t * w.rows + row) * groups + g] = acc;
+            result = fmaf((float)acc * xs[t], w.scales[(size_t)row * groups + g], result);
+        }
+    } else {
+        for (int c = 0; c < K; ++c) result = fmaf(weight_value(w, row, c), x[(size_t)t * K + c], result);
+    }
+    store_out(y, (size_t)t * w.rows + row, result, bias_at(w, row), epilogue);
+}
+
+// ------------------------------------------------ W8A8 prefill: int8 MFMA ---
+// Y[t, n] = sum_k Xq[t, k] W[n, k] with v_mfma_i32_16x16x64_i8.  A 64x64 block
+// tile, four waves of 32x32 (2x2 MFMA tiles).  Lane l feeds row/column (l & 15)
+// with 16 consecutive K bytes at offset 16 * (l >> 4) of each 64-wide K step,
+// for both operands, so the exact integer sum does not depend on how the
+// hardware orders K inside the instruction.  Accumulators are exact; the
+// epilogue is the CPU path's per group: res = fma((float)acc * s_x, s_w, res).
+__global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const int8_t* __restrict__ xq,
+                                                          const float* __restrict__ xs, int tokens,
+                                                          float* __restrict__ y, int epilogue,
+                                                          int32_t* __restrict__ acc_out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, N = w.rows;
+    const int tile_m = blockIdx.y * 64 + (wave >> 1) * 32;   // tokens
+    const int tile_n = blockIdx.x * 64 + (wave & 1) * 32;    // weight rows
+    const int li = lane & 15, lk = (lane >> 4) * 16;
+    const int groups = K / w.group;
+    const int steps_per_group = w.group / 64;
+    v4i acc[2][2];
+    float res[2][2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            acc[a][b] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) res[a][b][i] = 0.0f;
+        }
+    const int8_t* wbase = (const int8_t*)w.data;
+    const int steps = K / 64;
+    for (int s = 0; s < steps; ++s) {
+        const int k = s * 64 + lk;
+        v4i av[2], bv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int t = tile_m + a * 16 + li;
+            av[a] = t < tokens ? *(const v4i*)(xq + (size_t)t * K + k) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = tile_n + b * 16 + li;
+            bv[b] = n < N ? __builtin_nontemporal_load((const v4i*)(wbase + (size_t)n * K + k)) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[a], bv[b], acc[a][b], 0, 0, 0);
+        if ((s + 1) % steps_per_group == 0) {
+            const int g = (s + 1) / steps_per_group - 1;
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int n = tile_n + b * 16 + li;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = tile_m + a * 16 + (lane >> 4) * 4 + i;
+                        if (t < tokens && n < N) {
+                            if (acc_out) acc_out[((size_t)t * N + n) * groups + g] = acc[a][b][i];
+                            res[a][b][i] = fmaf((float)acc[a][b][i] * xs[t], w.scales[(size_t)n * groups + g],
+                                                res[a][b][i]);
+                        }
+                    }
+                    acc[a][b] = v4i{0, 0, 0, 0};
+                }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = tile_n + b * 16 + li;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = tile_m + a * 16 + (lane >> 4) * 4 + i;
+                if (t < tokens && n < N) store_out(y, (size_t)t * N + n, res[a][b][i], bias_at(w, n), epilogue);
+            }
+        }
+}
+
+// ------------------------------------------------ FP prefill: f32 MFMA ---
+// Y[t, n] = sum_k X[t, k] W[n, k] with v_mfma_f32_16x16x4_f32; weights of any
+// storage are widened (BF16) or dequantized (INT8 / INT4) as they are loaded.
+// Each lane loads four consecutive K values of its row and column and feeds
+// them to four MFMAs, so operand K positions always agree between A and B.
+template <int BITS>
+__device__ __forceinline__ float4 load_w4(const WeightView& w, int n, int k) {
+    // four consecutive values W[n, k..k+3], k a multiple of 4
+    if constexpr (BITS == 32) {
+        return *(const float4*)((const float*)w.data + (size_t)n * w.cols + k);
+    } else if constexpr (BITS == 16) {
+        const uint2 v = *(const uint2*)((const uint16_t*)w.data + (size_t)n * w.cols + k);
+        return make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFFu),
+                           bf16_to_f32(v.y >> 16));
+    } else {
+        float f[4];
+        const int groups = w.cols / w.group;
+        if constexpr (BITS == 8) {
+            const uint32_t v = *(const uint32_t*)((const int8_t*)w.data + (size_t)n * w.cols + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = (float)(int)(int8_t)((v >> (8 * e)) & 0xFFu);
+        } else {
+            const uint16_t v = *(const uint16_t*)((const uint8_t*)w.data + ((size_t)n * w.cols + k) / 2);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = (float)nibble((v >> (8 * (e / 2))) & 0xFFu, e & 1);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = f[e] * w.scales[(size_t)n * groups + (k + e) / w.group];
+        return make_float4(f[0], f[1], f[2], f[3]);
+    }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void gemm_f32_kernel(WeightView w, const float* __restrict__ x, int tokens,
+                                                         float* __restrict__ y, int epilogue) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, N = w.rows;
+    const int tile_m = blockIdx.y * 64 + (wave >> 1) * 32;
+    const int tile_n = blockIdx.x * 64 + (wave & 1) * 32;
+    const int li = lane & 15, lk = (lane >> 4) * 4;
+    v4f acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        const int k = k0 + lk;
+        float4 av[2], bv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int t = tile_m + a * 16 + li;
+            av[a] = (t < tokens && k < K) ? *(const float4*)(x + (size_t)t * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = tile_n + b * 16 + li;
+            bv[b] = (n < N && k < K) ? load_w4<BITS>(w, n, k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].x, bv[b].x, acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].y, bv[b].y, acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].z, bv[b].z, acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].w, bv[b].w, acc[a][b], 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int n = tile_n + b * 16 + li;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = tile_m + a * 16 + (lane >> 4) * 4 + i;
+                if (t < tokens && n < N) store_out(y, (size_t)t * N + n, acc[a][b][i], bias_at(w, n), epilogue);
+            }
+        }
+}
+
+// --------------------------------------------------------- RoPE + KV ---
+// rotary() + KV append (decoder.cpp:1259-1281, 1332-1343): head-major reorder,
+// rotate-half of the first `rotary` values with host-built cos/sin tables,
+// a*c - b*s and b*c + a*s rounded separately as on the CPU.
+__global__ void rope_kv_kernel(RopeKvCall p) {
+    const int t = blockIdx.y;
+    const int total_heads = p.heads + 2 * p.kv_heads;
+    const int item = blockIdx.x * blockDim.x + threadIdx.x;   // over total_heads * dim
+    if (item >= total_heads * p.dim) return;
+    const int hh = item / p.dim, i = item % p.dim;
+    const int half = p.rotary / 2;
+    const float* row = p.qkv + (size_t)t * p.ld;
+    const int pos = p.position + t;
+    float* dst;
+    const float* src;
+    if (hh < p.heads) {
+        src = row + p.q_offset + hh * p.dim;
+        dst = p.q_heads + ((size_t)hh * p.tokens + t) * p.dim;
+    } else if (hh < p.heads + p.kv_heads) {
+        const int kh = hh - p.heads;
+        src = row + p.k_offset + kh * p.dim;
+        dst = p.keys + ((size_t)kh * p.capacity + pos) * p.dim;
+    } else {
+        const int vh = hh - p.heads - p.kv_heads;
+        dst = p.values + ((size_t)vh * p.capacity + pos) * p.dim;
+        dst[i] = row[p.v_offset + vh * p.dim + i];
+        return;
+    }
+    if (i < half) {
+        const float c = p.cosines[(size_t)pos * half + i], s = p.sines[(size_t)pos * half + i];
+        const float a = src[i], b = src[i + half];
+        dst[i] = a * c - b * s;
+        dst[i + half] = b * c + a * s;
+    } else if (i >= p.rotary) {
+        dst[i] = src[i];
+    }
+}
+
+// ------------------------------------------------------------ attention ---
+// Online-softmax GQA attention (kv head = h / (heads / kv_heads), by index;
+// transformer.cpp:94-146).  Scores use the CPU's sequential dot order and
+// (dot * scale) * scale; the softmax is rescaled per key block, so results
+// agree with the CPU's max / exp / sum / divide to rounding.
+// Grid: (heads, tokens, splits).  With splits > 1 (decode) each block writes
+// (max, sum, o[dim]) for its key range to `partial`, merged by attention_merge.
+constexpr int kKeysPerPass = 256;
+
+__global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int keys_per_split) {
+    __shared__ float q_s[256];
+    __shared__ float scores[kKeysPerPass];
+    __shared__ float o_s[4][256];
+    __shared__ float red[16];
+    const int h = blockIdx.x, t = blockIdx.y, split = blockIdx.z;
+    const int kvh = h / (p.heads / p.kv_heads);
+    const int dim = p.dim;
+    const int qpos = p.position + t;
+    int begin = 0;
+    const int end = qpos + 1;
+    if (p.window && end > p.window) begin = end - p.window;
+    const int s_begin = max(begin, split * keys_per_split);
+    const int s_end = min(end, (split + 1) * keys_per_split);
+    for (int d = threadIdx.x; d < dim; d += blockDim.x) q_s[d] = p.q_heads[((size_t)h * p.tokens + t) * dim + d];
+    __syncthreads();
+    const float* K = p.keys + (size_t)kvh * p.capacity * dim;
+    const float* V = p.values + (size_t)kvh * p.capacity * dim;
+    float m = -INFINITY, l = 0.0f;
+    // thread owns output dims d = tid % 64 (+64, ...) for key lane kl = tid / 64
+    const int dl = threadIdx.x & 63, kl = threadIdx.x >> 6;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};   // dims dl, dl+64, dl+128, dl+192
+    for (int k0 = s_begin; k0 < s_end; k0 += kKeysPerPass) {
+        const int n = min(kKeysPerPass, s_end - k0);
+        float local_max = -INFINITY;
+        if (threadIdx.x < n) {
+            const float* krow = K + (size_t)(k0 + threadIdx.x) * dim;
+            float sum = 0.0f;
+            for (int d = 0; d < dim; ++d) sum = sum + q_s[d] * krow[d];
+            const float sc = sum * p.scale * p.scale;
+            scores[threadIdx.x] = sc;
+            local_max = sc;
+        }
+        const float block_max = block_reduce<float>(local_max, red, [](float a, float b) { return fmaxf(a, b); },
+                                                    wave_max_f32);
+        const float m_new = fmaxf(m, block_max);
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+        __syncthreads();
+        float e = 0.0f;
+        if (threadIdx.x < n) {
+            e = expf(scores[threadIdx.x] - m_new);
+            scores[threadIdx.x] = e;
+        }
+        const float block_sum = block_reduce<float>(e, red, [](float a, float b) { return a + b; }, wave_sum_f32);
+        __syncthreads();
+        l = l * alpha + block_sum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] *= alpha;
+        for (int kk = kl; kk < n; kk += 4) {
+            const float pk = scores[kk];
+            const float* vrow = V + (size_t)(k0 + kk) * dim;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = dl + 64 * j;
+                if (d < dim) o[j] = fmaf(pk, vrow[d], o[j]);
+            }
+        }
+        m = m_new;
+        __syncthreads();
+    }
+    // combine the four key lanes
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = dl + 64 * j;
+        if (d < dim) o_s[kl][d] = o[j];
+    }
+    __syncthreads();
+    if (gridDim.z == 1) {
+        float* out = p.out + ((size_t)t * p.heads + h) * dim;
+        for (int d = threadIdx.x; d < dim; d += blockDim.x) {
+            const float v = (o_s[0][d] + o_s[1][d]) + (o_s[2][d] + o_s[3][d]);
+            out[d] = l > 0.0f ? v / l : 0.0f;
+        }
+    } else {
+        float* part = p.partial + (((size_t)t * p.heads + h) * gridDim.z + split) * (dim + 2);
+        if (threadIdx.x == 0) { part[0] = m; part[1] = l; }
+        for (int d = threadIdx.x; d < dim; d += blockDim.x)
+            part[2 + d] = (o_s[0][d] + o_s[1][d]) + (o_s[2][d] + o_s[3][d]);
+    }
+}
+
+__global__ void attention_merge_kernel(AttentionCall p, int splits) {
+    const int h = blockIdx.x, t = blockIdx.y;
+    const float* part = p.partial + ((size_t)t * p.heads + h) * splits * (p.dim + 2);
+    float m = -INFINITY;
+    for (int s = 0; s < splits; ++s) m = fmaxf(m, part[s * (p.dim + 2)]);
+    float l = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float ms = part[s * (p.dim + 2)];
+        if (ms != -INFINITY) l += part[s * (p.dim + 2) + 1] * expf(ms - m);
+    }
+    float* out = p.out + ((size_t)t * p.heads + h) * p.dim;
+    for (int d = threadIdx.x; d < p.dim; d += blockDim.x) {
+        float v = 0.0f;
+        for (int s = 0; s < splits; ++s) {
+            const float ms = part[s * (p.dim + 2)];
+            if (ms != -INFINITY) v = fmaf(part[s * (p.dim + 2) + 2 + d], expf(ms - m), v);
+        }
+        out[d] = l > 0.0f ? v / l : 0.0f;
+    }
+}
+
+// ----------------------------------------------------- small elementwise ---
+__device__ __forceinline__ float activate(int activation, float x) {
+    // Decoder::Impl::activate (decoder.cpp:982-987)
+    if (activation == 0) return x / (1.0f + expf(-x));
+    if (activation == 1) return 0.5f * x * (1.0f + erff(x * 0.7071067811865475f));
+    if (activation == 2) return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+    return x < 0.0f ? 0.0f : x;
+}
+
+__global__ void activation_kernel(const float* gate_up, int tokens, int width, int gated, int activation, float* act) {
+    const size_t count = (size_t)tokens * width;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / width, j = i % width;
+        if (gated) {
+            const float g = gate_up[t * 2 * width + j], u = gate_up[t * 2 * width + width + j];
+            act[i] = u * activate(activation, g);
+        } else {
+            act[i] = activate(activation, gate_up[i]);
+        }
+    }
+}
+
+__global__ void residual_kernel(float* hidden, const float* a, const float* b, int count) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+        hidden[i] = hidden[i] + (a[i] + (b ? b[i] : 0.0f));
+}
+
+__global__ __launch_bounds__(kBlock) void argmax_kernel(const float* logits, int width, uint32_t* out) {
+    __shared__ float bv[kBlock / kWave];
+    __shared__ int bi[kBlock / kWave];
+    const float* row = logits + (size_t)blockIdx.x * width;
+    float best = -INFINITY;
+    int index = width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        const float v = row[c];
+        if (v > best || index == width) { best = v; index = c; }
+    }
+    // ties resolve to the lowest index (std::max_element keeps the first maximum)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, kWave);
+        const int oi = __shfl_xor(index, o, kWave);
+        if (ov > best || (ov == best && oi < index)) { best = ov; index = oi; }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { bv[wave] = best; bi[wave] = index; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w2 = 1; w2 < (int)(blockDim.x >> 6); ++w2)
+            if (bv[w2] > best || (bv[w2] == best && bi[w2] < index)) { best = bv[w2]; index = bi[w2]; }
+        out[blockIdx.x] = (uint32_t)index;
+    }
+}
+
+int ceil_div(size_t a, size_t b) { return (int)((a + b - 1) / b); }
+
+template <int BITS>
+void launch_fused_int(const LinearCall& c, hipStream_t stream) {
+    constexpr int E = BITS == 8 ? 16 : 32;
+    const int nch = c.w.cols / E;
+    const int jn = (nch + kWave - 1) / kWave;
+    constexpr int RPW = 2;
+    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
+    if (jn <= 1) gemv_int_fused_kernel<BITS, RPW, 1><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, c.epilogue, c.acc_out);
+    else if (jn <= 2) gemv_int_fused_kernel<BITS, RPW, 2><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, c.epilogue, c.acc_out);
+    else if (jn <= 4) gemv_int_fused_kernel<BITS, RPW, 4><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, c.epilogue, c.acc_out);
+    else gemv_int_fused_kernel<BITS, RPW, 6><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, c.epilogue, c.acc_out);
+}
+
+template <int BITS, int T>
+void launch_gemv_int_t(const LinearCall& c, const int8_t* xq, const float* xs, hipStream_t stream) {
+    constexpr int RPW = 2;
+    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
+    gemv_int_kernel<BITS, T, RPW><<<grid, kBlock, 0, stream>>>(c.w, xq, xs, c.y, c.epilogue, c.acc_out);
+}
+
+template <int BITS>
+void launch_gemv_int(const LinearCall& c, const int8_t* xq, const float* xs, hipStream_t stream) {
+    switch (c.tokens) {
+    case 1: launch_gemv_int_t<BITS, 1>(c, xq, xs, stream); break;
+    case 2: launch_gemv_int_t<BITS, 2>(c, xq, xs, stream); break;
+    case 3: launch_gemv_int_t<BITS, 3>(c, xq, xs, stream); break;
+    default: launch_gemv_int_t<BITS, 4>(c, xq, xs, stream); break;
+    }
+}
+
+template <int BITS, int T>
+void launch_gemv_fp_t(const LinearCall& c, hipStream_t stream) {
+    constexpr int RPW = 2;
+    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
+    gemv_fp_kernel<BITS, T, RPW><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.y, c.epilogue);
+}
+
+template <int BITS>
+void launch_gemv_fp(const LinearCall& c, hipStream_t stream) {
+    switch (c.tokens) {
+    case 1: launch_gemv_fp_t<BITS, 1>(c, stream); break;
+    case 2: launch_gemv_fp_t<BITS, 2>(c, stream); break;
+    case 3: launch_gemv_fp_t<BITS, 3>(c, stream); break;
+    default: launch_gemv_fp_t<BITS, 4>(c, stream); break;
+    }
+}
+
+}  // namespace
+
+// --------------------------------------------------------------- launchers ---
+void launch_embedding(const WeightView& table, const WeightView* positions, const uint32_t* ids, int tokens,
+                      int position_base, float scale, float* hidden, hipStream_t stream) {
+    WeightView none;
+    embedding_kernel<<<tokens, kBlock, 0, stream>>>(table, positions ? *positions : none, positions != nullptr, ids,
+                                                    position_base, scale, hidden);
+}
+
+void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream) {
+    norm_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, y);
+}
+
+void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {
+    quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, q, scales);
+}
+
+void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y, hipStream_t stream) {
+    const size_t count = (size_t)rows * width;
+    scale_columns_kernel<<<std::min(ceil_div(count, kBlock), 4096), kBlock, 0, stream>>>(x, width, count, factors, y);
+}
+
+int launch_linear(const LinearCall& call, hipStream_t stream) {
+    LinearCall c = call;
+    const WeightView& w = c.w;
+    if (c.norm.kind >= 0) {
+        // Only the single-token integer GEMV normalizes inside the kernel;
+        // everywhere else the rows are normalized first into norm_scratch.
+        const int E8 = w.bits == 8 ? 16 : 32;
+        const bool fusable = c.integer_activations && c.tokens == 1 && c.x && !c.xq && w.group == w.cols &&
+                             w.cols % E8 == 0 && w.cols <= 6 * 64 * E8 && (c.force_path == 0 || c.force_path == 1);
+        if (!fusable) {
+            if (!c.norm_scratch || !c.x) return -1;
+            launch_norm(c.x, c.tokens, w.cols, c.norm, c.norm_scratch, stream);
+            c.x = c.norm_scratch;
+            c.norm = NormView();
+        }
+    }
+    const int K = w.cols;
+    const bool quantized = w.bits == 8 || w.bits == 4;
+    const int E = 128 / w.bits;
+    // 128-bit loads need 16-byte aligned rows and inputs; anything else runs generic.
+    auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool chunked = K % E == 0 && aligned(w.data) && (!c.x || aligned(c.x)) && (!c.xq || aligned(c.xq));
+    if (c.integer_activations) {
+        const bool per_row = w.group == K;
+        const bool fast = per_row && chunked;
+        int path = c.force_path;
+        if (!path) path = (fast && c.tokens <= 4) ? 1 : (w.bits == 8 && c.tokens > 4 && K % 64 == 0 && w.group % 64 == 0) ? 3 : 2;
+        if (path == 1 && !(fast && c.tokens <= 4)) path = 2;
+        if (path == 3 && !(w.bits == 8 && K % 64 == 0 && w.group % 64 == 0 && aligned(w.data))) path = 2;
+        const int E8 = w.bits == 8 ? 16 : 32;
+        if (path == 1 && c.tokens == 1 && c.x && !c.xq && K <= 6 * 64 * E8) {
+            if (w.bits == 8) launch_fused_int<8>(c, stream); else launch_fused_int<4>(c, stream);
+            return 1;
+        }
+        const int8_t* xq = c.xq;
+        const float* xs = c.xs;
+        if (!xq) {
+            if (!c.xq_scratch || !c.xs_scratch || !c.x) return -1;
+            const float* src = c.x;
+            if (c.norm.kind >= 0) return -1;   // callers normalize beforehand on this path
+            launch_quantize(src, c.tokens, K, c.xq_scratch, c.xs_scratch, stream);
+            xq = c.xq_scratch;
+            xs = c.xs_scratch;
+        }
+        if (path == 1) {
+            if (w.bits == 8) launch_gemv_int<8>(c, xq, xs, stream); else launch_gemv_int<4>(c, xq, xs, stream);
+            return 1;
+        }
+        if (path == 3) {
+            dim3 grid(ceil_div(w.rows, 64), ceil_div(c.tokens, 64));
+            gemm_int8_kernel<<<grid, kBlock, 0, stream>>>(w, xq, xs, c.tokens, c.y, c.epilogue, c.acc_out);
+            return 3;
+        }
+        linear_generic_kernel<<<ceil_div((size_t)c.tokens * w.rows, kBlock), kBlock, 0, stream>>>(
+            w, nullptr, xq, xs, c.tokens, 1, c.y, c.epilogue, c.acc_out);
+        return 2;
+    }
+    if (c.norm.kind >= 0) return -1;
+    const bool group_ok = !quantized || (w.group % E == 0) || (E % w.group == 0);
+    int path = c.force_path;
+    if (!path) path = (chunked && group_ok && c.tokens <= 4) ? 1 : (c.tokens > 4 && K % 4 == 0 && (!quantized || w.group % 4 == 0)) ? 3 : 2;
+    if (path == 1 && !(chunked && group_ok && c.tokens <= 4)) path = 2;
+    if (path == 3 && !(K % 4 == 0 && (!quantized || w.group % 4 == 0) && aligned(w.data) && aligned(c.x))) path = 2;
+    if (path == 1) {
+        switch (w.bits) {
+        case 32: launch_gemv_fp<32>(c, stream); break;
+        case 16: launch_gemv_fp<16>(c, stream); break;
+        case 8: launch_gemv_fp<8>(c, stream); break;
+        default: launch_gemv_fp<4>(c, stream); break;
+        }
+        return 1;
+    }
+    if (path == 3) {
+        dim3 grid(ceil_div(w.rows, 64), ceil_div(c.tokens, 64));
+        switch (w.bits) {
+        case 32: gemm_f32_kernel<32><<<grid, kBlock, 0, stream>>>(w, c.x, c.tokens, c.y, c.epilogue); break;
+        case 16: gemm_f32_kernel<16><<<grid, kBlock, 0, stream>>>(w, c.x, c.tokens, c.y, c.epilogue); break;
+        case 8: gemm_f32_kernel<8><<<grid, kBlock, 0, stream>>>(w, c.x, c.tokens, c.y, c.epilogue); break;
+        default: gemm_f32_kernel<4><<<grid, kBlock, 0, stream>>>(w, c.x, c.tokens, c.y, c.epilogue); break;
+        }
+        return 3;
+    }
+    linear_generic_kernel<<<ceil_div((size_t)c.tokens * w.rows, kBlock), kBlock, 0, stream>>>(
+        w, c.x, nullptr, nullptr, c.tokens, 0, c.y, c.epilogue, nullptr);
+    return 2;
+}
+
+void launch_rope_kv(const RopeKvCall& call, hipStream_t stream) {
+    const int items = (call.heads + 2 * call.kv_heads) * call.dim;
+    dim3 grid(ceil_div(items, kBlock), call.tokens);
+    rope_kv_kernel<<<grid, kBlock, 0, stream>>>(call);
+}
+
+void launch_attention(const AttentionCall& call, hipStream_t stream) {
+    const int total = call.position + call.tokens;
+    int splits = 1, per_split = total;
+    if (call.tokens == 1 && call.partial) {
+        per_split = 256;
+        splits = (total + per_split - 1) / per_split;
+        while (splits > 1 && (size_t)splits * call.heads * (call.dim + 2) > (size_t)call.partial_capacity) {
+            per_split *= 2;
+            splits = (total + per_split - 1) / per_split;
+        }
+        if (splits == 1) per_split = total;
+    }
+    dim3 grid(call.heads, call.tokens, splits);
+    attention_kernel<<<grid, kBlock, 0, stream>>>(call, per_split);
+    if (splits > 1) attention_merge_kernel<<<dim3(call.heads, call.tokens), 64, 0, stream>>>(call, splits);
+}
+
+void launch_activation(const float* gate_up, int tokens, int width, int gated, int activation, float* act,
+                       hipStream_t stream) {
+    const size_t count = (size_t)tokens * width;
+    activation_kernel<<<std::min(ceil_div(count, kBlock), 8192), kBlock, 0, stream>>>(gate_up, tokens, width, gated,
+                                                                                    activation, act);
+}
+
+void launch_residual(float* hidden, const float* a, const float* b, int count, hipStream_t stream) {
+    residual_kernel<<<std::min(ceil_div(count, kBlock), 8192), kBlock, 0, stream>>>(hidden, a, b, count);
+}
+
+void launch_argmax(const float* logits, int rows, int width, uint32_t* out, hipStream_t stream) {
+    argmax_kernel<<<rows, kBlock, 0, stream>>>(logits, width, out);
+}
+
+}  // namespace leafhip

@@ -1,0 +1,142 @@
+// Host runtime of the MI355X decoder: artifact validation, device memory plan,
+// decoding sessions.  Internal to libleafhip; the public surface is include/leafhip.h.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/leafhip.h"
+#include "kernels.h"
+
+namespace leafhip {
+
+// An error carrying the C ABI status code.
+struct Error : std::runtime_error {
+    lh_status code;
+    Error(lh_status c, const std::string& message) : std::runtime_error(message), code(c) {}
+};
+
+// Reference-style check (decoder.cpp:86-88): "Leaf decoder: <message>".
+inline void check(bool ok, const std::string& message, lh_status code = LH_ERROR_ARTIFACT) {
+    if (!ok) throw Error(code, "Leaf decoder: " + message);
+}
+void hip_check(hipError_t status, const char* what);
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t n) { allocate(n); }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer() { release(); }
+    void allocate(size_t n);
+    void release();
+    template <typename T> T* as() const { return static_cast<T*>(ptr); }
+};
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    ~Context();
+};
+
+// One tensor of the artifact's table (decoder.cpp:858-904).
+struct TensorRecord {
+    std::string name;
+    uint32_t rows = 0, cols = 0, bits = 0, group = 0;
+    const uint8_t* data = nullptr;
+    const float* scales = nullptr;
+    uint64_t size = 0, scale_count = 0;
+};
+
+// Header semantics (Appendix A layout; decoder.cpp:795-857).
+struct Config {
+    uint32_t version = 0, hidden = 0, intermediate = 0, heads = 0, kv_heads = 0, layers = 0, vocab = 0;
+    uint32_t max_positions = 0, eos = 0, head_dim = 0, sliding_window = 0;
+    float theta = 0, epsilon = 0, embedding_scale = 1;
+    uint32_t norm_kind = 0, activation = 0, position_kind = 0, gated = 0, parallel = 0, rotary_dim = 0;
+    uint32_t position_offset = 0, final_norm = 0, qk_norm = 0;
+    std::vector<float> rope_frequencies;
+    std::vector<uint32_t> eos_tokens;
+    uint32_t qwidth() const { return heads * head_dim; }
+    uint32_t kvwidth() const { return kv_heads * head_dim; }
+};
+
+// A linear layer on the device: possibly several artifact matrices stacked
+// along rows (q|k|v, gate|up) so one launch streams them all.
+struct Linear {
+    WeightView view;
+    const float* input_scale = nullptr;   // SmoothQuant factors (decoder.cpp:1008-1019), device
+    bool present = false;
+};
+
+struct Layer {
+    NormView input_norm, post_norm;
+    Linear qkv;                 // [q | k | v] when stackable, else q only
+    Linear k, v;                // used when q, k, v could not be stacked
+    bool stacked_qkv = false;
+    Linear o, gate_up, up, down;
+    bool stacked_gate_up = false;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+};
+
+class Model {
+public:
+    static std::unique_ptr<Model> load(Context& context, const uint8_t* data, size_t size, uint32_t activation_bits,
+                                       uint32_t fp32_math);
+    Context& context;
+    Config config;
+    uint32_t activation_bits = 32;
+    bool accurate = false;
+    uint64_t artifact_bytes = 0;
+    uint32_t source_bf16_tensors = 0, quantized_tensors = 0;
+    DeviceBuffer weights;
+    std::vector<Layer> layers;
+    WeightView embedding, positions;
+    Linear head;
+    NormView final_norm;
+    bool has_positions = false;
+
+    explicit Model(Context& c) : context(c) {}
+    bool integer_linear(const Linear& l) const {
+        return activation_bits == 8 && (l.view.bits == 8 || l.view.bits == 4);
+    }
+};
+
+class Session {
+public:
+    Session(Model& model, uint32_t max_context, uint32_t max_prefill);
+    void reset() { length = 0; }
+    size_t cache_tokens() const { return length; }
+    // Decoder::forward_into (decoder.cpp:1282-1444)
+    void forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t capacity,
+                 uint32_t* argmax);
+    Model& model;
+    size_t length = 0;
+    uint32_t capacity = 0;
+    uint32_t planned = 0;
+    const float* logits_device = nullptr;
+    size_t logits_count = 0;
+
+private:
+    void plan(uint32_t tokens, bool all_logits);
+    void run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue, const NormView* fuse_norm);
+    hipStream_t stream() const { return model.context.stream; }
+    DeviceBuffer kv_, rope_cos_, rope_sin_;
+    DeviceBuffer hidden_, normed_, qkv_, q_heads_, attn_, attn_proj_, gate_up_, act_, proj_, logits_, xq_, xs_;
+    DeviceBuffer ids_, argmax_, partial_, scaled_;
+    uint32_t logits_rows_ = 0;
+    uint32_t* host_ids_ = nullptr;   // pinned staging for token ids
+    uint32_t* host_argmax_ = nullptr;
+public:
+    ~Session();
+};
+
+}  // namespace leafhip

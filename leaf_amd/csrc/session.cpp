@@ -1,0 +1,272 @@
+// Decoding session: device KV cache, workspaces and RoPE tables planned once,
+// and the forward pass of Decoder::Impl::forward_into (decoder.cpp:1282-1444).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+
+#include "runtime.h"
+
+namespace leafhip {
+
+namespace {
+template <typename T>
+void grow(DeviceBuffer& b, size_t count) {
+    if (b.bytes < count * sizeof(T)) b.allocate(count * sizeof(T));
+}
+}  // namespace
+
+Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m) {
+    const Config& c = m.config;
+    capacity = max_context ? std::min(max_context, c.max_positions) : c.max_positions;
+    check(capacity > 0, "session capacity must be positive", LH_ERROR_INVALID_ARGUMENT);
+    // KV cache for the whole context, [layers][k|v][kv_heads][capacity][dim].
+    kv_.allocate(size_t(c.layers) * 2 * c.kv_heads * capacity * c.head_dim * sizeof(float));
+    // RoPE tables for every position the cache can hold, from the same float
+    // expressions and libm calls as prepare_rotary_tables (decoder.cpp:1247-1256),
+    // so they equal the CPU's tables bit for bit.
+    if (c.position_kind == 0) {
+        const size_t half = c.rotary_dim / 2;
+        std::vector<float> cosines(size_t(capacity) * half), sines(cosines.size());
+        for (size_t pos = 0; pos < capacity; ++pos)
+            for (size_t i = 0; i < half; ++i) {
+                const float angle = static_cast<float>(pos) * c.rope_frequencies[i];
+                cosines[pos * half + i] = std::cos(angle);
+                sines[pos * half + i] = std::sin(angle);
+            }
+        rope_cos_.allocate(cosines.size() * sizeof(float));
+        rope_sin_.allocate(sines.size() * sizeof(float));
+        hip_check(hipMemcpy(rope_cos_.ptr, cosines.data(), cosines.size() * 4, hipMemcpyHostToDevice), "rope upload");
+        hip_check(hipMemcpy(rope_sin_.ptr, sines.data(), sines.size() * 4, hipMemcpyHostToDevice), "rope upload");
+    }
+    // Split-K decode attention scratch: (max, sum, out[dim]) per head per 256 keys.
+    const size_t splits = (capacity + 255) / 256;
+    partial_.allocate(splits * c.heads * (c.head_dim + 2) * sizeof(float));
+    grow<uint32_t>(argmax_, 1);
+    hip_check(hipHostMalloc((void**)&host_argmax_, sizeof(uint32_t)), "hipHostMalloc");
+    plan(max_prefill ? max_prefill : 512, false);
+}
+
+Session::~Session() {
+    if (host_ids_) (void)hipHostFree(host_ids_);
+    if (host_argmax_) (void)hipHostFree(host_argmax_);
+}
+
+// Workspaces for `tokens` rows; kept at their high-water mark like the CPU
+// runtime's vectors (decoder.cpp:755-765), so steady-state decode allocates nothing.
+void Session::plan(uint32_t tokens, bool all_logits) {
+    const Config& c = model.config;
+    if (tokens > planned) {
+        const size_t P = tokens;
+        const size_t qkv_width = size_t(c.qwidth()) + 2 * c.kvwidth();
+        const size_t widest = std::max<size_t>({c.hidden, c.qwidth(), c.intermediate});
+        grow<float>(hidden_, P * c.hidden);
+        grow<float>(normed_, P * c.hidden);
+        grow<float>(qkv_, P * qkv_width);
+        grow<float>(q_heads_, P * c.qwidth());
+        grow<float>(attn_, P * c.qwidth());
+        grow<float>(attn_proj_, P * c.hidden);
+        grow<float>(gate_up_, P * 2 * c.intermediate);
+        grow<float>(act_, P * c.intermediate);
+        grow<float>(proj_, P * c.hidden);
+        grow<int8_t>(xq_, P * widest);
+        grow<float>(xs_, P);
+        grow<float>(scaled_, P * widest);
+        grow<uint32_t>(ids_, P);
+        if (host_ids_) (void)hipHostFree(host_ids_);
+        hip_check(hipHostMalloc((void**)&host_ids_, P * sizeof(uint32_t)), "hipHostMalloc");
+        planned = tokens;
+    }
+    const uint32_t rows = all_logits ? tokens : 1;
+    if (rows > logits_rows_) {
+        logits_.allocate(size_t(rows) * c.vocab * sizeof(float));
+        logits_rows_ = rows;
+    }
+}
+
+void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue,
+                         const NormView* fuse_norm) {
+    LinearCall call;
+    call.w = l.view;
+    call.tokens = tokens;
+    call.y = y;
+    call.epilogue = epilogue;
+    call.integer_activations = model.integer_linear(l);
+    call.xq_scratch = xq_.as<int8_t>();
+    call.xs_scratch = xs_.as<float>();
+    call.norm_scratch = normed_.as<float>();
+    if (l.input_scale) {
+        // SmoothQuant input factors (decoder.cpp:1008-1019) before quantization.
+        launch_scale_columns(x, tokens, l.view.cols, l.input_scale, scaled_.as<float>(), stream());
+        x = scaled_.as<float>();
+    }
+    call.x = x;
+    if (fuse_norm) call.norm = *fuse_norm;
+    const int path = launch_linear(call, stream());
+    check(path > 0, "linear launch rejected", LH_ERROR_UNSUPPORTED);
+}
+
+void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t host_capacity,
+                      uint32_t* argmax) {
+    const Config& c = model.config;
+    // Input validation before any mutation (decoder.cpp:1286-1289).
+    check(count > 0, "input tokens are empty", LH_ERROR_INVALID_ARGUMENT);
+    const size_t position = length;
+    check(position <= c.max_positions && count <= c.max_positions - position, "context length exceeds artifact limit",
+          LH_ERROR_STATE);
+    for (size_t i = 0; i < count; ++i) check(ids[i] < c.vocab, "token id exceeds vocabulary", LH_ERROR_INVALID_ARGUMENT);
+    check(position + count <= capacity, "context length exceeds session capacity", LH_ERROR_STATE);
+    check(count <= uint32_t(std::numeric_limits<int32_t>::max()), "too many tokens", LH_ERROR_INVALID_ARGUMENT);
+    const size_t out_rows = all_logits ? count : 1;
+    check(!host_logits || host_capacity >= out_rows * c.vocab, "logits buffer too small", LH_ERROR_INVALID_ARGUMENT);
+    const int M = int(count);
+    plan(uint32_t(count), all_logits);
+    hipStream_t s = stream();
+    std::memcpy(host_ids_, ids, count * sizeof(uint32_t));
+    hip_check(hipMemcpyAsync(ids_.ptr, host_ids_, count * sizeof(uint32_t), hipMemcpyHostToDevice, s), "ids upload");
+
+    const int h = int(c.hidden), dim = int(c.head_dim);
+    const int qw = int(c.qwidth()), kvw = int(c.kvwidth());
+    const int qkv_width = qw + 2 * kvw;
+    float* hidden = hidden_.as<float>();
+    float* normed = normed_.as<float>();
+    launch_embedding(model.embedding, model.has_positions ? &model.positions : nullptr, ids_.as<uint32_t>(), M,
+                     int(position + c.position_offset), c.embedding_scale, hidden, s);
+    const float scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(c.head_dim)));
+    const size_t plane = size_t(c.kv_heads) * capacity * dim;
+
+    for (uint32_t layer = 0; layer < c.layers; ++layer) {
+        const Layer& L = model.layers[layer];
+        const bool last = layer + 1 == c.layers;
+        // ---- attention block
+        float* qkv = qkv_.as<float>();
+        const bool fuse_in = M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv && !L.qkv.input_scale;
+        if (fuse_in) {
+            run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
+        } else {
+            launch_norm(hidden, M, h, L.input_norm, normed, s);
+            if (L.stacked_qkv) {
+                run_linear(L.qkv, normed, M, qkv, kStore, nullptr);
+            } else {
+                // separate projections into a [M, q|k|v] staging layout
+                float* q = q_heads_.as<float>();   // reuse as [M, qw] staging
+                float* k = attn_.as<float>();      // [M, kvw]
+                float* v = attn_proj_.as<float>(); // [M, kvw]
+                run_linear(L.qkv, normed, M, q, kStore, nullptr);
+                run_linear(L.k, normed, M, k, kStore, nullptr);
+                run_linear(L.v, normed, M, v, kStore, nullptr);
+                for (int t = 0; t < M; ++t) {
+                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width, q + size_t(t) * qw, qw * 4,
+                                             hipMemcpyDeviceToDevice, s), "qkv staging");
+                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width + qw, k + size_t(t) * kvw, kvw * 4,
+                                             hipMemcpyDeviceToDevice, s), "qkv staging");
+                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width + qw + kvw, v + size_t(t) * kvw, kvw * 4,
+                                             hipMemcpyDeviceToDevice, s), "qkv staging");
+                }
+            }
+        }
+        if (c.qk_norm) {
+            // Q/K RMSNorm over each head's dim values (decoder.cpp:1327-1331).
+            NormView qn{L.q_norm, nullptr, c.epsilon, 0, model.accurate ? 1 : 0};
+            NormView kn{L.k_norm, nullptr, c.epsilon, 0, model.accurate ? 1 : 0};
+            for (int t = 0; t < M; ++t) {
+                float* row = qkv + size_t(t) * qkv_width;
+                launch_norm(row, int(c.heads), dim, qn, row, s);
+                launch_norm(row + qw, int(c.kv_heads), dim, kn, row + qw, s);
+            }
+        }
+        float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
+        float* values = keys + plane;
+        RopeKvCall rk;
+        rk.qkv = qkv; rk.ld = qkv_width; rk.q_offset = 0; rk.k_offset = qw; rk.v_offset = qw + kvw;
+        rk.tokens = M; rk.heads = int(c.heads); rk.kv_heads = int(c.kv_heads); rk.dim = dim;
+        rk.rotary = c.position_kind == 0 ? int(c.rotary_dim) : 0;
+        rk.position = int(position);
+        rk.cosines = rope_cos_.as<float>(); rk.sines = rope_sin_.as<float>();
+        rk.q_heads = q_heads_.as<float>(); rk.keys = keys; rk.values = values; rk.capacity = int(capacity);
+        launch_rope_kv(rk, s);
+
+        // After the last layer's KV append only the final row reaches the
+        // head (decoder.cpp:1375-1387 trims the MLP the same way; here the
+        // attention output, projections and MLP of earlier rows are skipped too:
+        // rows are independent, so the last row's values do not change).
+        const bool trim = last && !all_logits && M > 1;
+        const int rows = trim ? 1 : M;
+        const int first_row = trim ? M - 1 : 0;
+        AttentionCall at;
+        at.q_heads = q_heads_.as<float>(); at.keys = keys; at.values = values; at.out = attn_.as<float>();
+        at.heads = int(c.heads); at.kv_heads = int(c.kv_heads); at.tokens = M; at.position = int(position);
+        at.dim = dim; at.capacity = int(capacity); at.window = int(c.sliding_window); at.scale = scale;
+        at.partial = partial_.as<float>(); at.partial_capacity = int(partial_.bytes / sizeof(float));
+        launch_attention(at, s);
+        const float* attn_rows = attn_.as<float>() + size_t(first_row) * qw;
+        float* hid = hidden + size_t(first_row) * h;
+        float* attn_proj = attn_proj_.as<float>();
+        if (!c.parallel) {
+            run_linear(L.o, attn_rows, rows, hid, kAccumulate, nullptr);       // hidden += o(attn) + b
+        } else {
+            run_linear(L.o, attn_rows, rows, attn_proj, kStore, nullptr);
+        }
+        // ---- MLP block
+        float* gate_up = gate_up_.as<float>();
+        float* act = act_.as<float>();
+        const int f = int(c.intermediate);
+        if (c.gated) {
+            const bool fuse_post = rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up &&
+                                   !L.gate_up.input_scale;
+            if (fuse_post) {
+                run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm);
+            } else {
+                launch_norm(hid, rows, h, L.post_norm, normed, s);
+                if (L.stacked_gate_up) {
+                    run_linear(L.gate_up, normed, rows, gate_up, kStore, nullptr);
+                } else {
+                    float* g = proj_.as<float>();
+                    run_linear(L.gate_up, normed, rows, act, kStore, nullptr);   // gate -> act (staging)
+                    run_linear(L.up, normed, rows, g, kStore, nullptr);          // up -> proj (staging)
+                    for (int t = 0; t < rows; ++t) {
+                        hip_check(hipMemcpyAsync(gate_up + size_t(t) * 2 * f, act + size_t(t) * f, f * 4,
+                                                 hipMemcpyDeviceToDevice, s), "gate staging");
+                        hip_check(hipMemcpyAsync(gate_up + size_t(t) * 2 * f + f, g + size_t(t) * f, f * 4,
+                                                 hipMemcpyDeviceToDevice, s), "up staging");
+                    }
+                }
+            }
+            launch_activation(gate_up, rows, f, 1, int(c.activation), act, s);
+        } else {
+            launch_norm(hid, rows, h, L.post_norm, normed, s);
+            run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
+            launch_activation(gate_up, rows, f, 0, int(c.activation), act, s);
+        }
+        if (!c.parallel) {
+            run_linear(L.down, act, rows, hid, kAccumulate, nullptr);         // hidden += down(act) + b
+        } else {
+            float* proj = proj_.as<float>();
+            run_linear(L.down, act, rows, proj, kStore, nullptr);
+            launch_residual(hid, proj, attn_proj, rows * h, s);              // hidden += proj + attn_proj
+        }
+        if (trim) hidden = hid;   // the final norm and head see only the last row
+    }
+    const int head_rows = all_logits ? M : 1;
+    // `hidden` now points at the rows the head reads: all rows, or the last one.
+    const float* head_in = hidden;
+    const float* x = head_in;
+    if (c.final_norm) {
+        launch_norm(head_in, head_rows, h, model.final_norm, normed, s);
+        x = normed;
+    }
+    float* logits = logits_.as<float>();
+    run_linear(model.head, x, head_rows, logits, kStore, nullptr);
+    launch_argmax(logits + size_t(head_rows - 1) * c.vocab, 1, int(c.vocab), argmax_.as<uint32_t>(), s);
+    hip_check(hipMemcpyAsync(host_argmax_, argmax_.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s), "argmax copy");
+    if (host_logits)
+        hip_check(hipMemcpyAsync(host_logits, logits, size_t(head_rows) * c.vocab * sizeof(float),
+                                 hipMemcpyDeviceToHost, s), "logits copy");
+    hip_check(hipStreamSynchronize(s), "forward");
+    if (argmax) *argmax = *host_argmax_;
+    logits_device = logits;
+    logits_count = size_t(head_rows) * c.vocab;
+    length = position + count;
+}
+
+}  // namespace leafhip

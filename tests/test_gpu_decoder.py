@@ -1,0 +1,113 @@
+"""Whole decoder on the GPU against the oracle and the reference's golden outputs.
+
+Reduced models of every family (GPT-2 FP32, TinyLlama W8A8, Qwen INT4, SmolLM2
+BF16-accurate) keep the operator topology and storage policy of the full-size
+workloads.  Logits must agree within LOGIT_TOLERANCE (max-abs error relative
+to the largest |logit|) and greedy tokens must be identical.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+# max |gpu - cpu| / max |cpu| over the logits of a forward
+LOGIT_TOLERANCE = 1e-3
+
+
+def rel_error(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def runtime():
+    from leaf_amd import runtime
+    runtime.library()
+    return runtime
+
+
+@pytest.mark.parametrize("family", ["gpt2", "tinyllama", "qwen", "smollm2"])
+def test_chunked_logits_and_greedy_tokens_match_reference(runtime, oracle, golden_decoders, artifacts, family):
+    arrays, meta = golden_decoders
+    m = meta[family]
+    prompt = arrays[f"{family}_prompt"]
+    dec = runtime.Decoder(artifacts[family], m["activation_bits"], m["fp32_math"])
+    rows = []
+    for pos in range(0, len(prompt), m["chunk"]):
+        rows.append(dec.forward(prompt[pos:pos + m["chunk"]], all_logits=True))
+    logits = np.concatenate(rows)
+    assert dec.cache_tokens() == len(prompt)
+    ref_rows = arrays[f"{family}_logits_rows"]
+    err = rel_error(logits[m["rows"]], ref_rows)
+    print(f"{family}: chunked all-logits relative error {err:.2e}")
+    assert err <= LOGIT_TOLERANCE
+    # every row against the oracle (same arithmetic as the reference)
+    od = oracle.decoder(artifacts[family], m["activation_bits"], m["fp32_math"] == "accurate")
+    full = np.concatenate([od.forward(prompt[p:p + m["chunk"]], all_logits=True)
+                           for p in range(0, len(prompt), m["chunk"])])
+    assert rel_error(logits, full) <= LOGIT_TOLERANCE
+    dec.reset()
+    assert dec.cache_tokens() == 0
+    tokens, prefill_ms, decode_ms = dec.generate(prompt, 10)
+    assert tokens == arrays[f"{family}_tokens"].tolist()
+    dec.close()
+
+
+@pytest.mark.parametrize("family", ["gpt2", "tinyllama", "qwen", "smollm2"])
+def test_decode_steps_match_oracle_token_by_token(runtime, oracle, artifacts, family):
+    from leaf_amd import models
+    bits, math = models.RUN_POLICY[family]
+    dec = runtime.Decoder(artifacts[family], bits, math)
+    od = oracle.decoder(artifacts[family], bits, math == "accurate")
+    rng = np.random.default_rng(77)
+    prompt = rng.integers(0, dec.vocabulary_size, 33).astype(np.uint32)   # >= 32: final-layer trim on the CPU
+    a, b = dec.forward(prompt), od.forward(prompt)
+    assert rel_error(a, b) <= LOGIT_TOLERANCE
+    worst = 0.0
+    for step in range(24):
+        tok = int(np.argmax(b))
+        assert dec.last_argmax.value == int(np.argmax(a))
+        assert int(np.argmax(a)) == tok, f"greedy token differs at step {step}"
+        a, b = dec.forward([tok]), od.forward([tok])
+        worst = max(worst, rel_error(a, b))
+    print(f"{family}: worst decode-step relative logit error {worst:.2e}")
+    assert worst <= LOGIT_TOLERANCE
+    dec.close()
+
+
+def test_invalid_inputs_leave_the_session_untouched(runtime, artifacts):
+    dec = runtime.Decoder(artifacts["tinyllama"], 8, "fast", max_context=64)
+    first = dec.forward([1, 2, 3])
+    with pytest.raises(runtime.LeafError, match="input tokens are empty"):
+        dec.forward([])
+    with pytest.raises(runtime.LeafError, match="token id exceeds vocabulary"):
+        dec.forward([dec.vocabulary_size])
+    with pytest.raises(runtime.LeafError, match="exceeds"):
+        dec.forward(np.zeros(62, np.uint32))
+    assert dec.cache_tokens() == 3
+    dec.reset()
+    again = dec.forward([1, 2, 3])
+    assert np.array_equal(first.view(np.uint32), again.view(np.uint32)), "reset must reproduce the same logits"
+    buf = np.empty(dec.vocabulary_size, np.float32)
+    dec.reset()
+    arg = dec.forward_into([1, 2, 3], buf)
+    assert np.array_equal(buf, first) and arg == int(np.argmax(first))
+    dec.close()
+
+
+def test_rejects_corrupt_artifacts(runtime, tmp_path, artifacts):
+    blob = bytearray(artifacts["gpt2"].read_bytes())
+    bad = tmp_path / "bad.leaf"
+    bad.write_bytes(b"NOTLEAF!" + blob[8:])
+    with pytest.raises(runtime.LeafError, match="unsupported artifact magic"):
+        runtime.Decoder(bad)
+    bad.write_bytes(blob[:60])
+    with pytest.raises(runtime.LeafError, match="truncated artifact metadata"):
+        runtime.Decoder(bad)
+    with pytest.raises(runtime.LeafError, match="activation bits must be 8 or 32"):
+        runtime.Decoder(artifacts["gpt2"], activation_bits=16)
+    with pytest.raises(runtime.LeafError, match="accurate FP32 math requires"):
+        runtime.Decoder(artifacts["tinyllama"], 8, "accurate")
+    with pytest.raises(runtime.LeafError, match="source BF16 storage requires FP32 activations"):
+        runtime.Decoder(artifacts["smollm2"], 8)

@@ -1,0 +1,248 @@
+"""GPU kernels through the C ABI against the oracle, on the same seeded inputs.
+
+Integer work (activation quantization, int32 accumulators, the W8A8 / W4A8
+epilogue) must be bit-exact.  Floating-point paths are checked against the
+oracle and an FP64 restatement with the stated tolerances.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from leaf_amd.artifact import quantize, round_to_bf16  # noqa: E402
+from leaf_amd.models import W8A8_LINEAR_SHAPES  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from leaf_amd import runtime
+    runtime.library()
+    return runtime
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def activations(rng, M, K):
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[rng.random((M, K)) < 0.001] *= np.float32(20)
+    return x
+
+
+def run_int_linear(rt, w, s, b, x, bits, group, acc=True):
+    M, K = x.shape
+    N = w.shape[0]
+    dw = rt.DeviceWeight(w, bits, K, s, group, b)
+    dx = rt.DeviceArray.of(x)
+    dy = rt.DeviceArray((M, N), np.float32)
+    dacc = rt.DeviceArray((M, N, K // group), np.int32) if acc else None
+    rt.linear(dw, dx, M, 8, dy, dacc)
+    return dy.numpy(), (dacc.numpy() if acc else None)
+
+
+def test_quantize_rows_bit_exact(rt, oracle):
+    rng = np.random.default_rng(1)
+    for M, K in ((1, 2048), (7, 5632), (3, 100)):
+        x = activations(rng, M, K)
+        dx = rt.DeviceArray.of(x)
+        q, s = rt.DeviceArray((M, K), np.int8), rt.DeviceArray((M,), np.float32)
+        rt.quantize_rows(dx, M, K, q, s)
+        oq, os_ = oracle.quantize_rows(x)
+        assert np.array_equal(q.numpy(), oq) and bits_equal(s.numpy(), os_)
+
+
+@pytest.mark.parametrize("K,N", sorted(set(W8A8_LINEAR_SHAPES)))
+def test_w8a8_decode_gemv_bit_exact_at_tinyllama_shapes(rt, oracle, K, N):
+    rng = np.random.default_rng(K * 7 + N)
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, 8, K)
+    x = activations(rng, 1, K)
+    y, acc = run_int_linear(rt, wq, ws, None, x, 8, K)
+    q, qs = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(8, N, K, K, wq, q)), "int32 accumulators differ"
+    assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, None, x)), "dequantized outputs differ"
+
+
+@pytest.mark.parametrize("M", [2, 4, 16, 128])
+def test_w8a8_multi_token_bit_exact(rt, oracle, M):
+    rng = np.random.default_rng(M)
+    K, N = 2048, 256
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, 8, K)
+    b = rng.standard_normal(N, dtype=np.float32)
+    x = activations(rng, M, K)
+    y, acc = run_int_linear(rt, wq, ws, b, x, 8, K)
+    q, _ = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(8, N, K, K, wq, q))
+    assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, b, x))
+
+
+def test_w8a8_prefill_gemm_512_tokens_bit_exact(rt, oracle):
+    rng = np.random.default_rng(512)
+    M, K, N = 512, 2048, 320
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, 8, K)
+    x = activations(rng, M, K)
+    y, acc = run_int_linear(rt, wq, ws, None, x, 8, K)
+    q, _ = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(8, N, K, K, wq, q))
+    assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, None, x))
+
+
+@pytest.mark.parametrize("bits,group,K,N,M", [(8, 64, 256, 9, 1), (8, 64, 256, 9, 5), (8, 64, 512, 70, 67),
+                                              (8, 2, 100, 7, 3), (4, 32, 256, 6, 1), (4, 32, 896, 40, 3),
+                                              (4, 896, 896, 40, 1), (8, 100, 100, 7, 1), (4, 2, 64, 3, 2)])
+def test_grouped_and_odd_integer_paths_bit_exact(rt, oracle, bits, group, K, N, M):
+    rng = np.random.default_rng(bits * 1000 + K + M)
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, bits, group)
+    b = rng.standard_normal(N, dtype=np.float32)
+    x = activations(rng, M, K)
+    y, acc = run_int_linear(rt, wq, ws, b, x, bits, group)
+    q, _ = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(bits, N, K, group, wq, q))
+    oracle.set_vnni_policy(0)
+    assert bits_equal(y, oracle.linear_int(bits, N, K, group, wq, ws, b, x))
+
+
+def test_golden_w8a8_vectors_on_gpu(rt, golden_kernels):
+    # the reference's own outputs (tests/golden/kernels.npz), straight on the GPU
+    g = golden_kernels
+    for tag, group, tokens in (("k2048", 2048, (1, 4, 16)), ("k5632", 5632, (1, 4)), ("odd", 100, (1, 3, 5)),
+                               ("g64", 64, (1, 2, 5))):
+        w, s, b = g[f"w8a8_{tag}_w"], g[f"w8a8_{tag}_s"], g.get(f"w8a8_{tag}_b")
+        for M in tokens:
+            y, _ = run_int_linear(rt, w, s, b, g[f"w8a8_{tag}_m{M}_x"], 8, group, acc=False)
+            assert bits_equal(y, g[f"w8a8_{tag}_m{M}_y"]), (tag, M)
+
+
+def fp_case(bits, w, K):
+    if bits == 32:
+        return w, None, 0
+    if bits == 16:
+        return round_to_bf16(w), None, 0
+    group = K if bits == 8 else 32
+    q, s = quantize(w, bits, group)
+    return q, s, group
+
+
+@pytest.mark.parametrize("bits", [32, 16, 8, 4])
+@pytest.mark.parametrize("M", [1, 2, 4, 17, 64])
+def test_fp_linear_within_tolerance(rt, oracle, bits, M):
+    rng = np.random.default_rng(bits + M)
+    K, N = 768, 130
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    data, scales, group = fp_case(bits, w, K)
+    b = rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    dw = rt.DeviceWeight(data, bits, K, scales, group, b)
+    dx = rt.DeviceArray.of(x)
+    dy = rt.DeviceArray((M, N), np.float32)
+    rt.linear(dw, dx, M, 32, dy)
+    y = dy.numpy()
+    ref = oracle.linear_fp(bits, N, K, group, data, scales, b, x)
+    # FP64 restatement of the same dequantized weights
+    if bits == 32:
+        wd = data.astype(np.float64)
+    elif bits == 16:
+        wd = (data.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    else:
+        if bits == 4:
+            un = np.empty((N, K), np.int8)
+            un[:, ::2] = data & 15
+            un[:, 1::2] = data >> 4
+            un[un >= 8] -= 16
+        else:
+            un = data
+        wd = un.astype(np.float64) * np.repeat(scales.astype(np.float64), group, axis=1)
+    e = x.astype(np.float64) @ wd.T + b
+    # test_decode_gemv.cpp:36-42 bound against FP64, twice that against the CPU path
+    assert np.all(np.abs(y - e) <= 2e-5 * (1 + np.abs(e)))
+    assert np.all(np.abs(y - ref) <= 4e-5 * (1 + np.abs(ref)))
+
+
+def test_norms_within_tolerance(rt, oracle):
+    from leaf_amd.runtime import check, library
+    rng = np.random.default_rng(9)
+    for width in (2048, 768, 77):
+        x = rng.standard_normal((3, width), dtype=np.float32)
+        g = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(width)).astype(np.float32)
+        dx, dg, db = rt.DeviceArray.of(x), rt.DeviceArray.of(g), rt.DeviceArray.of(b)
+        dy = rt.DeviceArray((3, width), np.float32)
+        for accurate in (0, 1):
+            check(library().lh_rmsnorm(dx.ptr, 3, width, dg.ptr, np.float32(1e-5), accurate, dy.ptr, None))
+            np.testing.assert_allclose(dy.numpy(), oracle.norm(x, g, None, 1e-5, 0, bool(accurate)), rtol=2e-6,
+                                       atol=2e-6)
+        check(library().lh_layernorm(dx.ptr, 3, width, dg.ptr, db.ptr, np.float32(1e-5), dy.ptr, None))
+        np.testing.assert_allclose(dy.numpy(), oracle.norm(x, g, b, 1e-5, 1, False), rtol=2e-6, atol=2e-6)
+
+
+def test_rope_kv_matches_reference_formula(rt, oracle):
+    from leaf_amd.runtime import check, library
+    rng = np.random.default_rng(11)
+    heads, kv, dim, rot, M, pos, cap = 4, 2, 64, 32, 3, 5, 16
+    qkv = rng.standard_normal((M, (heads + 2 * kv) * dim), dtype=np.float32)
+    freq = oracle.rope_frequencies(10000.0, rot)
+    cos, sin = oracle.rope_tables(freq, rot, 0, cap)
+    dq = rt.DeviceArray.of(qkv)
+    dcos, dsin = rt.DeviceArray.of(cos), rt.DeviceArray.of(sin)
+    qh = rt.DeviceArray((heads, M, dim), np.float32)
+    keys, values = rt.DeviceArray((kv, cap, dim), np.float32).zero(), rt.DeviceArray((kv, cap, dim), np.float32).zero()
+    check(library().lh_rope_kv(dq.ptr, M, heads, kv, dim, rot, pos, dcos.ptr, dsin.ptr, qh.ptr, keys.ptr, values.ptr,
+                               cap, None))
+    half = rot // 2
+    q = qkv[:, :heads * dim].reshape(M, heads, dim).transpose(1, 0, 2).copy()
+    c, s = cos[pos:pos + M][None, :, :], sin[pos:pos + M][None, :, :]
+    a, bb = q[..., :half].copy(), q[..., half:rot].copy()
+    q[..., :half] = a * c - bb * s
+    q[..., half:rot] = bb * c + a * s
+    assert bits_equal(qh.numpy(), q)
+    k = qkv[:, heads * dim:(heads + kv) * dim].reshape(M, kv, dim).transpose(1, 0, 2).copy()
+    a, bb = k[..., :half].copy(), k[..., half:rot].copy()
+    k[..., :half] = a * c - bb * s
+    k[..., half:rot] = bb * c + a * s
+    assert bits_equal(keys.numpy()[:, pos:pos + M], k)
+    v = qkv[:, (heads + kv) * dim:].reshape(M, kv, dim).transpose(1, 0, 2)
+    assert bits_equal(values.numpy()[:, pos:pos + M], v)
+
+
+@pytest.mark.parametrize("tokens,position,window", [(1, 640, 0), (1, 4351, 0), (1, 700, 64), (37, 0, 0),
+                                                    (13, 21, 0), (16, 5, 7)])
+def test_attention_matches_oracle(rt, oracle, tokens, position, window):
+    from leaf_amd.runtime import check, library
+    rng = np.random.default_rng(tokens * 100 + position)
+    heads, kv, dim = 14, 2, 64
+    total = position + tokens
+    cap = total + 3
+    q = rng.standard_normal((heads, tokens, dim), dtype=np.float32)
+    keys = rng.standard_normal((kv, cap, dim), dtype=np.float32)
+    values = rng.standard_normal((kv, cap, dim), dtype=np.float32)
+    dq, dk, dv = rt.DeviceArray.of(q), rt.DeviceArray.of(keys), rt.DeviceArray.of(values)
+    out = rt.DeviceArray((tokens, heads * dim), np.float32)
+    check(library().lh_attention(dq.ptr, dk.ptr, dv.ptr, cap, heads, kv, dim, tokens, position, window, out.ptr,
+                                 None))
+    mask = np.zeros((tokens, total), np.float32)
+    for t in range(tokens):
+        end = position + t + 1
+        begin = end - window if window and end > window else 0
+        mask[t, begin:end] = 1
+    scale = np.float32(1) / np.sqrt(np.sqrt(np.float32(dim)))
+    ref = oracle.attention(q, keys, values, mask, heads, kv, tokens, total, cap, dim, float(scale))
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=2e-6)
+
+
+def test_argmax_first_maximum(rt):
+    from leaf_amd.runtime import check, library
+    x = np.zeros((3, 50257), np.float32)
+    x[0, 7] = x[0, 9000] = 3.0
+    x[1] = -1.0
+    x[2, 50256] = 1.0
+    dx = rt.DeviceArray.of(x)
+    out = rt.DeviceArray((3,), np.uint32)
+    check(library().lh_argmax(dx.ptr, 3, 50257, out.ptr, None))
+    assert out.numpy().tolist() == [7, 0, 50256]

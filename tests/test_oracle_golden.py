@@ -1,0 +1,186 @@
+"""The oracle against the reference's own outputs (tests/golden/, written by
+tests/golden/make_golden.py from the reference build) and against closed forms.
+
+Every comparison is bit-exact: the oracle restates the reference's operation
+order, so any dropped term, swapped operand or wrong rounding shows up here.
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from leaf_amd import models
+from leaf_amd.artifact import quantize
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+W8A8_CASES = [("k2048", 2048, (1, 4, 16)), ("k5632", 5632, (1, 4)), ("k2048n128", 2048, (1,)),
+              ("odd", 100, (1, 3, 5)), ("g64", 64, (1, 2, 5))]
+
+
+@pytest.mark.parametrize("tag,group,tokens", W8A8_CASES)
+def test_w8a8_quantization_and_linear_match_reference(oracle, golden_kernels, tag, group, tokens):
+    g = golden_kernels
+    w, s = g[f"w8a8_{tag}_w"], g[f"w8a8_{tag}_s"]
+    b = g.get(f"w8a8_{tag}_b")
+    N, K = w.shape
+    for M in tokens:
+        x = g[f"w8a8_{tag}_m{M}_x"]
+        q, qs = oracle.quantize_rows(x)
+        assert np.array_equal(q, g[f"w8a8_{tag}_m{M}_q"]), "int8 activations differ"
+        assert bits_equal(qs, g[f"w8a8_{tag}_m{M}_qs"]), "activation scales differ"
+        oracle.set_vnni_policy(0)
+        assert bits_equal(oracle.linear_int(8, N, K, group, w, s, b, x), g[f"w8a8_{tag}_m{M}_y"])
+        if f"w8a8_{tag}_m{M}_yvnni" in g:
+            oracle.set_vnni_policy(1)
+            assert bits_equal(oracle.linear_int(8, N, K, group, w, s, b, x), g[f"w8a8_{tag}_m{M}_yvnni"])
+            oracle.set_vnni_policy(0)
+
+
+def test_int32_accumulators_are_exact_integer_sums(oracle, golden_kernels):
+    # closed form: acc[t, n, g] = sum over the group of int(w) * int(q), in int64
+    g = golden_kernels
+    w, q = g["w8a8_g64_w"], g["w8a8_g64_m5_q"]
+    N, K = w.shape
+    acc = oracle.int_accumulators(8, N, K, 64, w, q)
+    expect = np.einsum("tgk,ngk->tng", q.astype(np.int64).reshape(5, K // 64, 64),
+                       w.astype(np.int64).reshape(N, K // 64, 64))
+    assert np.array_equal(acc, expect)
+    # a planted mistake (one weight changed) must be seen
+    w2 = w.copy()
+    w2[3, 17] = np.int8(-w2[3, 17] if w2[3, 17] else 1)
+    assert not np.array_equal(oracle.int_accumulators(8, N, K, 64, w2, q), expect)
+
+
+def test_w4a8_matches_reference(oracle, golden_kernels):
+    g = golden_kernels
+    w, s = g["w4a8_w"], g["w4a8_s"]
+    for M in (1, 3):
+        assert bits_equal(oracle.linear_int(4, 6, 256, 32, w, s, None, g[f"w4a8_m{M}_x"]), g[f"w4a8_m{M}_y"])
+
+
+@pytest.mark.parametrize("tag,K", [("k768", 768), ("k896", 896), ("odd", 77)])
+def test_fp_linear_matches_reference(oracle, golden_kernels, tag, K):
+    g = golden_kernels
+    b = g[f"fp_{tag}_b"]
+    forms = [(32, g[f"fp_{tag}_w"], None, 0), (16, g[f"fp_{tag}_wbf16"], None, 0),
+             (8, g[f"fp_{tag}_w8"], g[f"fp_{tag}_s8"], K)]
+    if f"fp_{tag}_w4" in g:
+        forms.append((4, g[f"fp_{tag}_w4"], g[f"fp_{tag}_s4"], 32))
+    N = g[f"fp_{tag}_w"].shape[0]
+    for bits, data, scales, group in forms:
+        for M in (1, 2, 5):
+            y = oracle.linear_fp(bits, N, K, group, data, scales, b, g[f"fp_{tag}_b{bits}_m{M}_x"])
+            assert bits_equal(y, g[f"fp_{tag}_b{bits}_m{M}_y"]), (bits, M)
+    x = g[f"acc_{tag}_x"]
+    assert bits_equal(oracle.linear_accurate(32, N, K, g[f"fp_{tag}_w"], b, x), g[f"acc_{tag}_y32"])
+    assert bits_equal(oracle.linear_accurate(16, N, K, g[f"fp_{tag}_wbf16"], b, x), g[f"acc_{tag}_y16"])
+
+
+def test_fp32_gemv_within_fp64_bound(oracle):
+    # tests/native/test_decode_gemv.cpp:36-42: |y - e| <= 2e-5 (1 + |e|), e in FP64
+    rng = np.random.default_rng(815)
+    for K in (1, 7, 8, 31, 33, 65, 768, 3072):
+        for N in (1, 3, 33):
+            w = rng.uniform(-2, 2, (N, K)).astype(np.float32)
+            x = rng.uniform(-2, 2, (1, K)).astype(np.float32)
+            y = oracle.linear_fp(32, N, K, 0, w, None, None, x)[0]
+            e = w.astype(np.float64) @ x[0].astype(np.float64)
+            assert np.all(np.abs(y - e) <= 2e-5 * (1 + np.abs(e)))
+
+
+@pytest.mark.parametrize("tag", ["h2048", "h768"])
+def test_norms_match_reference(oracle, golden_kernels, tag):
+    g = golden_kernels
+    x, gm, b = g[f"norm_{tag}_x"], g[f"norm_{tag}_g"], g[f"norm_{tag}_b"]
+    assert bits_equal(oracle.norm(x, gm, None, 1e-5, 0, False), g[f"norm_{tag}_rms"])
+    assert bits_equal(oracle.norm(x, gm, None, 1e-5, 0, True), g[f"norm_{tag}_rmsacc"])
+    assert bits_equal(oracle.norm(x, gm, b, 1e-5, 1, False), g[f"norm_{tag}_ln"])
+
+
+def test_weight_quantization_closed_form_and_reference_example(oracle):
+    # tests/unit/test_decoder_plan.py:83-96 (zero rows and both signs, atol 0.03)
+    source = np.array([[0] * 8, [-7, -4, -2, -1, 1, 2, 4, 7]], dtype=np.float32)
+    for bits in (8, 4):
+        packed, scales = oracle.quantize_weights(source, bits, 8)
+        ref_packed, ref_scales = quantize(source, bits, 8)
+        assert np.array_equal(packed.view(np.uint8), ref_packed.view(np.uint8))
+        assert np.array_equal(scales, ref_scales)
+        if bits == 4:
+            un = np.empty(source.shape, np.int8)
+            un[:, ::2] = packed & 15
+            un[:, 1::2] = packed >> 4
+            un[un >= 8] -= 16
+        else:
+            un = packed
+        assert np.all(np.isfinite(scales)) and np.all(scales > 0)
+        np.testing.assert_allclose(un.astype(np.float32) * scales, source, atol=0.03)
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((7, 64), dtype=np.float32)
+    for bits, group in ((8, 64), (8, 16), (4, 32), (4, 2)):
+        p, s = oracle.quantize_weights(w, bits, group)
+        rp, rs = quantize(w, bits, group)
+        assert np.array_equal(p.view(np.uint8), rp.view(np.uint8)) and np.array_equal(s, rs)
+
+
+def test_rope_tables_and_attention_closed_forms(oracle):
+    f = oracle.rope_frequencies(10000.0, 64)
+    assert f[0] == 1.0 and np.all(np.diff(f) < 0)
+    np.testing.assert_allclose(f, 1.0 / 10000.0 ** (np.arange(32) * 2 / 64), rtol=1e-6)
+    c, s = oracle.rope_tables(f, 64, 5, 3)
+    np.testing.assert_allclose(c**2 + s**2, 1.0, rtol=1e-6)
+    angle = (np.float32(5) * f).astype(np.float64)        # float32 product, as the reference forms it
+    np.testing.assert_allclose(c[0], np.cos(angle), rtol=0, atol=2e-7)
+    np.testing.assert_allclose(s[2], np.sin((np.float32(7) * f).astype(np.float64)), rtol=0, atol=2e-7)
+    # GQA by index equals materialized repeat (tests/native/test_kernels.cpp:253-327)
+    rng = np.random.default_rng(722)
+    kv_heads, heads, dim, total, stride = 2, 14, 16, 65, 80
+    keys = rng.uniform(-0.3, 0.3, (kv_heads, stride, dim)).astype(np.float32)
+    values = rng.uniform(-0.3, 0.3, (kv_heads, stride, dim)).astype(np.float32)
+    q = rng.uniform(-0.3, 0.3, (heads, 1, dim)).astype(np.float32)
+    mask = np.ones((1, total), np.float32)
+    out = oracle.attention(q, keys, values, mask, heads, kv_heads, 1, total, stride, dim, 0.5)
+    rep = heads // kv_heads
+    keys_r = np.repeat(keys, rep, axis=0)
+    values_r = np.repeat(values, rep, axis=0)
+    dense = oracle.attention(q, keys_r, values_r, mask, heads, heads, 1, total, stride, dim, 0.5)
+    assert bits_equal(out, dense)
+    # softmax closed form in float64
+    s64 = np.einsum("hd,hkd->hk", q[:, 0].astype(np.float64), keys_r[:, :total].astype(np.float64)) * 0.25
+    p = np.exp(s64 - s64.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    e = np.einsum("hk,hkd->hd", p, values_r[:, :total].astype(np.float64)).reshape(1, -1)
+    np.testing.assert_allclose(out, e, atol=1e-6)
+
+
+def test_activations_closed_forms(oracle):
+    x = np.linspace(-6, 6, 41, dtype=np.float32)
+    np.testing.assert_allclose(oracle.activate(0, x), x / (1 + np.exp(-x.astype(np.float64))), rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(oracle.activate(2, x), 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x**3))),
+                               rtol=2e-6, atol=5e-7)
+    assert np.array_equal(oracle.activate(3, x), np.maximum(x, 0))
+    from math import erf
+    np.testing.assert_allclose(oracle.activate(1, x), [0.5 * v * (1 + erf(v / 2**0.5)) for v in x], rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("family", ["gpt2", "tinyllama", "qwen", "smollm2"])
+def test_decoder_matches_reference_binary(oracle, golden_decoders, artifacts, family):
+    arrays, meta = golden_decoders
+    m = meta[family]
+    path = artifacts[family]
+    assert hashlib.sha256(path.read_bytes()).hexdigest() == m["artifact_sha256"], "artifact writer drifted"
+    prompt = arrays[f"{family}_prompt"]
+    d = oracle.decoder(path, m["activation_bits"], m["fp32_math"] == "accurate")
+    rows = []
+    for pos in range(0, len(prompt), m["chunk"]):
+        rows.append(d.forward(prompt[pos:pos + m["chunk"]], all_logits=True))
+    logits = np.concatenate(rows)[m["rows"]]
+    assert bits_equal(logits, arrays[f"{family}_logits_rows"])
+    d.reset()
+    assert d.generate(prompt, 10) == arrays[f"{family}_tokens"].tolist()
