@@ -114,6 +114,21 @@ lh_status lh_forward(lh_session* session, const uint32_t* ids, size_t count, int
  * (decode_ms has room for limit entries; either may be NULL). */
 lh_status lh_generate(lh_session* session, const uint32_t* prompt, size_t count, uint32_t limit, uint32_t* tokens,
                       size_t* produced, double* prefill_ms, double* decode_ms);
+/* Device-side phase profile, the GPU counterpart of LEAF_DECODER_PROFILE
+ * (decoder.cpp:119-230): when enabled, every launch of a forward is bracketed
+ * by HIP events on the session's stream and accumulated per kernel class,
+ * with the algorithmic bytes it had to move.  Classes: "gemv_w8a8",
+ * "gemv_fp", "gemm_w8a8", "gemm_fp", "attention", "other". */
+typedef struct lh_profile_entry {
+    char name[24];
+    uint64_t launches;
+    double milliseconds;
+    double bytes;          /* algorithmic HBM bytes (weights, scales, inputs, outputs) */
+    double operations;     /* multiply-adds x 2 */
+} lh_profile_entry;
+lh_status lh_session_set_profiling(lh_session* session, int enable);
+/* Copies the accumulated entries and clears them. */
+lh_status lh_session_profile(lh_session* session, lh_profile_entry* out, size_t capacity, size_t* count);
 /* Device pointer of the last forward's logits (valid until the next call). */
 lh_status lh_session_logits_device(const lh_session* session, const float** logits, size_t* count);
 
@@ -127,6 +142,13 @@ lh_status lh_synchronize(void);
 lh_status lh_stream_create(lh_stream* out);
 lh_status lh_stream_destroy(lh_stream stream);
 lh_status lh_stream_synchronize(lh_stream stream);
+/* Capture the work submitted to `stream` into a replayable graph (HIP graph).
+ * Only kernel-level entry points may be called on the stream while capturing. */
+typedef struct lh_graph lh_graph;
+lh_status lh_stream_begin_capture(lh_stream stream);
+lh_status lh_stream_end_capture(lh_stream stream, lh_graph** out);
+lh_status lh_graph_launch(lh_graph* graph, lh_stream stream);
+lh_status lh_graph_destroy(lh_graph* graph);
 /* Device-side timing of work submitted to `stream` (HIP events). */
 typedef struct lh_timer lh_timer;
 lh_status lh_timer_start(lh_stream stream, lh_timer** out);

@@ -211,22 +211,39 @@ class _Init:
     def __init__(self, spec: DecoderSpec, seed: int):
         self.spec, self.seed = spec, seed
 
-    def __call__(self, name: str, rows: int, cols: int) -> np.ndarray:
+    def blocks(self, name: str, rows: int, cols: int, block_elements: int = 1 << 22):
+        """Yield (first_row, array) blocks of the tensor; one random stream per tensor,
+        so the values do not depend on the block size."""
         spec = self.spec
         digest = np.frombuffer(name.encode(), dtype=np.uint8).astype(np.uint64)
         key = int((digest * (np.arange(digest.size, dtype=np.uint64) + 1)).sum() % (1 << 31))
         rng = np.random.Generator(np.random.PCG64([self.seed, key, len(name)]))
-        if name.endswith("norm.weight"):
-            out = np.ones((rows, cols), np.float32)
-            if spec.norm_jitter:
-                out += rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(spec.norm_jitter)
-            return out
-        if name.endswith(".bias"):
-            if not spec.bias_std:
-                return np.zeros((rows, cols), np.float32)
-            return rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(spec.bias_std)
-        out = rng.standard_normal((rows, cols), dtype=np.float32)
-        out *= np.float32(spec.std)
+        step = max(1, min(rows, block_elements // max(cols, 1)))
+        buffer = np.empty((step, cols), np.float32)
+        for first in range(0, rows, step):
+            out = buffer[:min(step, rows - first)]
+            if name.endswith("norm.weight"):
+                if spec.norm_jitter:
+                    rng.standard_normal(out.shape, dtype=np.float32, out=out)
+                    out *= np.float32(spec.norm_jitter)
+                    out += np.float32(1)
+                else:
+                    out.fill(1)
+            elif name.endswith(".bias"):
+                if spec.bias_std:
+                    rng.standard_normal(out.shape, dtype=np.float32, out=out)
+                    out *= np.float32(spec.bias_std)
+                else:
+                    out.fill(0)
+            else:
+                rng.standard_normal(out.shape, dtype=np.float32, out=out)
+                out *= np.float32(spec.std)
+            yield first, out
+
+    def __call__(self, name: str, rows: int, cols: int) -> np.ndarray:
+        out = np.empty((rows, cols), np.float32)
+        for first, block in self.blocks(name, rows, cols):
+            out[first:first + len(block)] = block
         return out
 
 
@@ -276,18 +293,20 @@ def write_artifact(path: str | Path, spec: DecoderSpec, seed: int = 0) -> dict:
         for name, rows, cols, precision, group, start, size, scale_start, scales, source in descriptors:
             if source is None:
                 continue
-            array = init(source, rows, cols)
-            if precision == 32:
-                payload, scale_array = array.astype("<f4", copy=False), None
-            elif precision == 16:
-                payload, scale_array = round_to_bf16(array), None
-            else:
-                payload, scale_array = quantize(array, precision, group)
-            out.seek(base + start)
-            out.write(payload.tobytes())
-            if scales:
-                out.seek(base + scale_start)
-                out.write(scale_array.tobytes())
+            row_bytes = cols * precision // 8
+            groups = cols // group if group else 0
+            for first, array in init.blocks(source, rows, cols):
+                if precision == 32:
+                    payload, scale_array = array, None
+                elif precision == 16:
+                    payload, scale_array = round_to_bf16(array), None
+                else:
+                    payload, scale_array = quantize(array, precision, group)
+                out.seek(base + start + first * row_bytes)
+                out.write(memoryview(np.ascontiguousarray(payload)).cast("B"))
+                if scales:
+                    out.seek(base + scale_start + first * groups * 4)
+                    out.write(memoryview(scale_array).cast("B"))
         out.truncate(max(end, out.tell()))
     tmp.replace(path)
     return {"version": version, "tensor_count": len(descriptors), "bytes": path.stat().st_size,

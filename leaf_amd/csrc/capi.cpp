@@ -2,6 +2,7 @@
 // converts exceptions into a status code plus a thread-local message; nothing
 // throws across the ABI.
 #include <chrono>
+#include <cstdio>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -18,6 +19,7 @@ struct lh_context { leafhip::Context impl; };
 struct lh_model { std::unique_ptr<leafhip::Model> impl; };
 struct lh_session { std::unique_ptr<leafhip::Session> impl; };
 struct lh_timer { hipEvent_t start, stop; };
+struct lh_graph { hipGraphExec_t exec; };
 
 namespace {
 
@@ -66,6 +68,22 @@ void* scratch_bytes(size_t bytes) {
         g_scratch.buffers[slot].allocate(bytes);
     }
     return g_scratch.buffers[slot].ptr;
+}
+
+// Zero-initialized span counters of the decode attention kernel (it resets
+// them itself), one set per device.
+unsigned* attention_counters() {
+    static leafhip::DeviceBuffer counters[8];
+    static std::mutex lock;
+    int dev = 0;
+    leafhip::hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> guard(lock);
+    auto& b = counters[dev & 7];
+    if (!b.ptr) {
+        b.allocate(1024 * sizeof(unsigned));
+        leafhip::hip_check(hipMemset(b.ptr, 0, b.bytes), "hipMemset");
+    }
+    return b.as<unsigned>();
 }
 
 leafhip::WeightView view_of(const lh_weight* w) {
@@ -290,6 +308,38 @@ lh_status lh_generate(lh_session* session, const uint32_t* prompt, size_t count,
     });
 }
 
+lh_status lh_session_set_profiling(lh_session* session, int enable) {
+    return guarded([&] {
+        require_arg(session, "session is required");
+        session->impl->profiler.enabled = enable != 0;
+    });
+}
+
+lh_status lh_session_profile(lh_session* session, lh_profile_entry* out, size_t capacity, size_t* count) {
+    return guarded([&] {
+        require_arg(session && count, "session and count are required");
+        auto& p = session->impl->profiler;
+        size_t n = 0;
+        for (int k = 0; k < leafhip::Profiler::Count; ++k) {
+            const auto& t = p.totals[k];
+            if (!t.launches) continue;
+            if (out && n < capacity) {
+                lh_profile_entry e{};
+                std::snprintf(e.name, sizeof(e.name), "%s", leafhip::Profiler::name(k));
+                e.launches = t.launches;
+                e.milliseconds = t.ms;
+                e.bytes = t.bytes;
+                e.operations = t.ops;
+                out[n] = e;
+            }
+            ++n;
+        }
+        *count = n;
+        if (out)
+            for (auto& t : p.totals) t = leafhip::Profiler::Total();
+    });
+}
+
 lh_status lh_session_logits_device(const lh_session* session, const float** logits, size_t* count) {
     return guarded([&] {
         require_arg(session && logits && count, "session and outputs are required");
@@ -332,6 +382,37 @@ lh_status lh_stream_destroy(lh_stream stream) {
 }
 lh_status lh_stream_synchronize(lh_stream stream) {
     return guarded([&] { leafhip::hip_check(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); });
+}
+lh_status lh_stream_begin_capture(lh_stream stream) {
+    return guarded([&] {
+        require_arg(stream, "capture needs a created stream");
+        leafhip::hip_check(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+                           "hipStreamBeginCapture");
+    });
+}
+lh_status lh_stream_end_capture(lh_stream stream, lh_graph** out) {
+    return guarded([&] {
+        require_arg(stream && out, "stream and output are required");
+        hipGraph_t graph;
+        leafhip::hip_check(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture");
+        hipGraphExec_t exec;
+        const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        leafhip::hip_check(st, "hipGraphInstantiate");
+        *out = new lh_graph{exec};
+    });
+}
+lh_status lh_graph_launch(lh_graph* graph, lh_stream stream) {
+    return guarded([&] {
+        require_arg(graph, "graph is null");
+        leafhip::hip_check(hipGraphLaunch(graph->exec, as_stream(stream)), "hipGraphLaunch");
+    });
+}
+lh_status lh_graph_destroy(lh_graph* graph) {
+    return guarded([&] {
+        if (graph) (void)hipGraphExecDestroy(graph->exec);
+        delete graph;
+    });
 }
 lh_status lh_timer_start(lh_stream stream, lh_timer** out) {
     return guarded([&] {
@@ -448,12 +529,13 @@ lh_status lh_attention(const float* q_heads, const float* keys, const float* val
         a.kv_heads = int(kv_heads); a.tokens = int(tokens); a.position = int(position); a.dim = int(dim);
         a.capacity = int(capacity); a.window = int(window);
         a.scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(dim)));
-        if (tokens == 1) {
-            const size_t floats = ((position + tokens + 255) / 256) * heads * (dim + 2);
+        if (tokens == 1 && kv_heads <= 1024) {
+            const size_t floats = ((position + tokens + 15) / 16) * heads * (dim + 2);
             a.partial = static_cast<float*>(scratch_bytes(floats * sizeof(float)));
             a.partial_capacity = int(floats);
+            a.counters = attention_counters();
         }
-        leafhip::launch_attention(a, as_stream(stream));
+        leafhip::check(leafhip::launch_attention(a, as_stream(stream)), "attention launch rejected", LH_ERROR_UNSUPPORTED);
         leafhip::hip_check(hipGetLastError(), "attention launch");
     });
 }

@@ -35,11 +35,33 @@ enum Epilogue : int {
 
 // Token-major activations use row stride == width unless stated.
 void launch_embedding(const WeightView& table, const WeightView* positions, const uint32_t* ids, int tokens,
-                      int position_base, float scale, float* hidden, hipStream_t stream);
+                      int position_base, float scale, float* hidden, hipStream_t stream,
+                      const int* position_ptr = nullptr);
 void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream);
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream);
 void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y,
                           hipStream_t stream);
+
+// Epilogues over pairs of output rows computed by one wave (single token):
+//  kPairRopeKv: rows are a stacked [q | k | v] projection; rotate-half pairs
+//    (i, i + rotary/2) of q and k heads with the host-built tables, write q to
+//    q_heads [heads, 1, dim] and k, v into the caches at `position`
+//    (rotary() and KVCache::append, decoder.cpp:1259-1281, 1332-1343);
+//  kPairGated: rows are a stacked [gate | up] projection; act[j] =
+//    up[j] * activate(gate[j]) (decoder.cpp:1396-1414).
+enum PairMode : int { kPairNone = 0, kPairRopeKv = 1, kPairGated = 2 };
+struct PairEpilogue {
+    int mode = kPairNone;
+    int heads = 0, kv_heads = 0, dim = 0, rotary = 0, position = 0, capacity = 0;
+    const int* position_ptr = nullptr;  // when set, the position is read from device memory
+    const float* cosines = nullptr;
+    const float* sines = nullptr;
+    float* q_heads = nullptr;
+    float* keys = nullptr;
+    float* values = nullptr;
+    int width = 0, activation = 0;
+    float* act = nullptr;
+};
 
 // y[t, row] for t < tokens.  integer_activations selects W8A8/W4A8 (bits 8/4):
 // then either x (f32, quantized per token inside the kernel) or xq/xs (given).
@@ -60,10 +82,14 @@ struct LinearCall {
     float* xs_scratch = nullptr;    // [tokens]
     float* norm_scratch = nullptr;  // [tokens, cols] when `norm` cannot be fused into the kernel
     int force_path = 0;             // 0 auto, 1 GEMV, 2 generic, 3 GEMM
+    PairEpilogue pair;              // single-token paired epilogue (y unused when set)
 };
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
 // the call cannot run (missing scratch for the GEMM quantization).
 int launch_linear(const LinearCall& call, hipStream_t stream);
+// True when launch_linear runs the single-token integer GEMV that normalizes,
+// quantizes and applies paired epilogues inside the kernel.
+bool linear_fuses(const LinearCall& call);
 
 // RoPE + head-major reorder + KV append for `tokens` new tokens at `position`.
 // qkv is [tokens, qwidth + 2 * kvwidth]; q_heads gets [heads, tokens, dim];
@@ -74,6 +100,7 @@ struct RopeKvCall {
     int q_offset = 0, k_offset = 0, v_offset = 0;
     int tokens = 0, heads = 0, kv_heads = 0, dim = 0, rotary = 0;
     int position = 0;
+    const int* position_ptr = nullptr;  // when set, the position is read from device memory
     const float* cosines = nullptr; // [positions, rotary/2] tables built on the host
     const float* sines = nullptr;
     float* q_heads = nullptr;
@@ -91,11 +118,16 @@ struct AttentionCall {
     const float* values = nullptr;
     float* out = nullptr;           // [tokens, heads * dim]
     int heads = 0, kv_heads = 0, tokens = 0, position = 0, dim = 0, capacity = 0, window = 0;
+    const int* position_ptr = nullptr;  // decode only: position read from device memory
+    int spans = 0;                  // decode only: fixed number of key spans (0 = from position)
     float scale = 1.0f;             // applied twice: (q.k * scale) * scale (decoder.cpp:1348)
     float* partial = nullptr;       // split-K scratch (decode); may be null
     int partial_capacity = 0;       // floats available in partial
+    unsigned* counters = nullptr;   // kv_heads zero-initialized counters (decode); reset by the kernel
 };
-void launch_attention(const AttentionCall& call, hipStream_t stream);
+// Returns false when the call cannot run: a device-resident position
+// (position_ptr) is only supported by the single-token decode kernels.
+bool launch_attention(const AttentionCall& call, hipStream_t stream);
 
 // act = up * activate(gate) for gated MLPs, act = activate(up) otherwise.
 // gate_up holds [tokens, 2 * width] = [gate | up] when gated, [tokens, width] otherwise.
@@ -105,5 +137,13 @@ void launch_activation(const float* gate_up, int tokens, int width, int gated, i
 void launch_residual(float* hidden, const float* a, const float* b, int count, hipStream_t stream);
 // index of the first maximum of each row (std::max_element, main_decoder.cpp:102)
 void launch_argmax(const float* logits, int rows, int width, uint32_t* out, hipStream_t stream);
+// Greedy step on the device: argmax of one row into next_id[0] and host_out[0]
+// (mapped host memory, may be null), then position[0] += 1.
+void launch_argmax_advance(const float* logits, int width, uint32_t* next_id, uint32_t* host_out, int* position,
+                           hipStream_t stream);
+// Number of key spans the decode attention uses for `keys` visible keys.
+int attention_decode_spans(int keys, int dim);
+// Whether single-token attention runs the span kernels (graph-capturable).
+bool attention_decode_supported(int heads, int kv_heads, int dim);
 
 }  // namespace leafhip

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -110,10 +111,34 @@ public:
     }
 };
 
+// Per-kernel-class device timing (HIP events on the session stream).
+class Profiler {
+public:
+    enum Kind { GemvW8A8, GemvFp, GemmW8A8, GemmFp, Attention, Other, Count };
+    static const char* name(int kind);
+    bool enabled = false;
+    void begin(hipStream_t stream);
+    void end(hipStream_t stream, int kind, double bytes, double operations);
+    void collect();          // after the stream synchronized
+    struct Total { uint64_t launches = 0; double ms = 0, bytes = 0, ops = 0; };
+    Total totals[Count];
+    ~Profiler();
+private:
+    struct Pending { int kind; double bytes, ops; size_t event; };
+    std::vector<hipEvent_t> events_;
+    std::vector<Pending> pending_;
+    size_t used_ = 0;
+    hipEvent_t next_event();
+};
+
 class Session {
 public:
+    Profiler profiler;
     Session(Model& model, uint32_t max_context, uint32_t max_prefill);
-    void reset() { length = 0; }
+    void reset() {
+        length = 0;
+        device_position_valid_ = false;
+    }
     size_t cache_tokens() const { return length; }
     // Decoder::forward_into (decoder.cpp:1282-1444)
     void forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t capacity,
@@ -127,11 +152,30 @@ public:
 
 private:
     void plan(uint32_t tokens, bool all_logits);
-    void run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue, const NormView* fuse_norm);
+    void validate(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t host_capacity) const;
+    void launch(int M, size_t position, bool all_logits, const int* position_ptr, int spans);
+    bool graph_decode_ok() const;
+    void decode_graphed(uint32_t id, bool upload_id, float* host_logits, uint32_t* argmax);
+    void drop_graphs();
+    std::map<int, hipGraphExec_t> graphs_;
+    bool graphs_enabled_ = true;
+    bool device_position_valid_ = false;
+    DeviceBuffer position_;
+    int* host_position_ = nullptr;
+    uint32_t* mapped_argmax_ = nullptr;
+    LinearCall make_call(const Linear& l, const float* x, int tokens, float* y, int epilogue,
+                         const NormView* fuse_norm);
+    void run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue, const NormView* fuse_norm,
+                    const PairEpilogue* pair = nullptr);
+    template <typename F> void timed(int kind, double bytes, double ops, F&& launch) {
+        if (profiler.enabled) profiler.begin(stream());
+        launch();
+        if (profiler.enabled) profiler.end(stream(), kind, bytes, ops);
+    }
     hipStream_t stream() const { return model.context.stream; }
     DeviceBuffer kv_, rope_cos_, rope_sin_;
     DeviceBuffer hidden_, normed_, qkv_, q_heads_, attn_, attn_proj_, gate_up_, act_, proj_, logits_, xq_, xs_;
-    DeviceBuffer ids_, argmax_, partial_, scaled_;
+    DeviceBuffer ids_, argmax_, partial_, scaled_, counters_;
     uint32_t logits_rows_ = 0;
     uint32_t* host_ids_ = nullptr;   // pinned staging for token ids
     uint32_t* host_argmax_ = nullptr;

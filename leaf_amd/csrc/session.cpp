@@ -3,7 +3,9 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <cstdlib>
 #include <limits>
+#include <string>
 
 #include "runtime.h"
 
@@ -15,6 +17,48 @@ void grow(DeviceBuffer& b, size_t count) {
     if (b.bytes < count * sizeof(T)) b.allocate(count * sizeof(T));
 }
 }  // namespace
+
+const char* Profiler::name(int kind) {
+    static const char* names[] = {"gemv_w8a8", "gemv_fp", "gemm_w8a8", "gemm_fp", "attention", "other"};
+    return names[kind];
+}
+
+hipEvent_t Profiler::next_event() {
+    if (used_ == events_.size()) {
+        hipEvent_t e;
+        hip_check(hipEventCreate(&e), "hipEventCreate");
+        events_.push_back(e);
+    }
+    return events_[used_++];
+}
+
+void Profiler::begin(hipStream_t stream) {
+    hip_check(hipEventRecord(next_event(), stream), "hipEventRecord");
+}
+
+void Profiler::end(hipStream_t stream, int kind, double bytes, double operations) {
+    const size_t start = used_ - 1;
+    hip_check(hipEventRecord(next_event(), stream), "hipEventRecord");
+    pending_.push_back({kind, bytes, operations, start});
+}
+
+void Profiler::collect() {
+    for (const auto& p : pending_) {
+        float ms = 0;
+        hip_check(hipEventElapsedTime(&ms, events_[p.event], events_[p.event + 1]), "hipEventElapsedTime");
+        Total& t = totals[p.kind];
+        ++t.launches;
+        t.ms += ms;
+        t.bytes += p.bytes;
+        t.ops += p.ops;
+    }
+    pending_.clear();
+    used_ = 0;
+}
+
+Profiler::~Profiler() {
+    for (auto e : events_) (void)hipEventDestroy(e);
+}
 
 Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m) {
     const Config& c = m.config;
@@ -39,23 +83,34 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m
         hip_check(hipMemcpy(rope_cos_.ptr, cosines.data(), cosines.size() * 4, hipMemcpyHostToDevice), "rope upload");
         hip_check(hipMemcpy(rope_sin_.ptr, sines.data(), sines.size() * 4, hipMemcpyHostToDevice), "rope upload");
     }
-    // Split-K decode attention scratch: (max, sum, out[dim]) per head per 256 keys.
-    const size_t splits = (capacity + 255) / 256;
+    // Split-K decode attention scratch: (max, sum, out[dim]) per head per key
+    // span (spans are >= 16 keys).
+    const size_t splits = (capacity + 15) / 16;
     partial_.allocate(splits * c.heads * (c.head_dim + 2) * sizeof(float));
+    counters_.allocate(size_t(c.kv_heads) * sizeof(unsigned));
+    hip_check(hipMemset(counters_.ptr, 0, counters_.bytes), "hipMemset");
     grow<uint32_t>(argmax_, 1);
-    hip_check(hipHostMalloc((void**)&host_argmax_, sizeof(uint32_t)), "hipHostMalloc");
+    hip_check(hipHostMalloc((void**)&host_argmax_, sizeof(uint32_t), hipHostMallocMapped), "hipHostMalloc");
+    hip_check(hipHostGetDevicePointer((void**)&mapped_argmax_, host_argmax_, 0), "hipHostGetDevicePointer");
+    hip_check(hipHostMalloc((void**)&host_position_, sizeof(int)), "hipHostMalloc");
+    position_.allocate(sizeof(int));
+    const char* graphs = std::getenv("LEAF_DECODE_GRAPH");
+    graphs_enabled_ = !(graphs && std::string(graphs) == "0");
     plan(max_prefill ? max_prefill : 512, false);
 }
 
 Session::~Session() {
+    drop_graphs();
     if (host_ids_) (void)hipHostFree(host_ids_);
     if (host_argmax_) (void)hipHostFree(host_argmax_);
+    if (host_position_) (void)hipHostFree(host_position_);
 }
 
 // Workspaces for `tokens` rows; kept at their high-water mark like the CPU
 // runtime's vectors (decoder.cpp:755-765), so steady-state decode allocates nothing.
 void Session::plan(uint32_t tokens, bool all_logits) {
     const Config& c = model.config;
+    if (tokens > planned || (all_logits ? tokens : 1) > logits_rows_) drop_graphs();   // captured pointers move
     if (tokens > planned) {
         const size_t P = tokens;
         const size_t qkv_width = size_t(c.qwidth()) + 2 * c.kvwidth();
@@ -84,8 +139,21 @@ void Session::plan(uint32_t tokens, bool all_logits) {
     }
 }
 
+LinearCall Session::make_call(const Linear& l, const float* x, int tokens, float* y, int epilogue,
+                              const NormView* fuse_norm) {
+    LinearCall call;
+    call.w = l.view;
+    call.tokens = tokens;
+    call.y = y;
+    call.epilogue = epilogue;
+    call.integer_activations = model.integer_linear(l);
+    call.x = l.input_scale ? nullptr : x;
+    if (fuse_norm) call.norm = *fuse_norm;
+    return call;
+}
+
 void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue,
-                         const NormView* fuse_norm) {
+                         const NormView* fuse_norm, const PairEpilogue* pair) {
     LinearCall call;
     call.w = l.view;
     call.tokens = tokens;
@@ -102,12 +170,23 @@ void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, 
     }
     call.x = x;
     if (fuse_norm) call.norm = *fuse_norm;
-    const int path = launch_linear(call, stream());
+    if (pair) call.pair = *pair;
+    // Algorithmic traffic: weights, scales, activations (int8 when quantized),
+    // outputs: N*K*b_w + 4*N*(K/g) + K*M*b_x + 4*M*N.
+    const WeightView& w = l.view;
+    const double groups = (w.bits == 8 || w.bits == 4) ? double(w.cols) / w.group : 0.0;
+    const double bytes = double(w.rows) * w.cols * w.bits / 8 + 4.0 * w.rows * groups +
+                         double(w.cols) * tokens * (call.integer_activations ? 1 : 4) + 4.0 * tokens * w.rows;
+    const double ops = 2.0 * tokens * double(w.rows) * w.cols;
+    const int kind = tokens <= 4 ? (call.integer_activations ? Profiler::GemvW8A8 : Profiler::GemvFp)
+                                 : (call.integer_activations ? Profiler::GemmW8A8 : Profiler::GemmFp);
+    int path = 0;
+    timed(kind, bytes, ops, [&] { path = launch_linear(call, stream()); });
     check(path > 0, "linear launch rejected", LH_ERROR_UNSUPPORTED);
 }
 
-void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t host_capacity,
-                      uint32_t* argmax) {
+void Session::validate(const uint32_t* ids, size_t count, bool all_logits, float* host_logits,
+                       size_t host_capacity) const {
     const Config& c = model.config;
     // Input validation before any mutation (decoder.cpp:1286-1289).
     check(count > 0, "input tokens are empty", LH_ERROR_INVALID_ARGUMENT);
@@ -119,19 +198,112 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
     check(count <= uint32_t(std::numeric_limits<int32_t>::max()), "too many tokens", LH_ERROR_INVALID_ARGUMENT);
     const size_t out_rows = all_logits ? count : 1;
     check(!host_logits || host_capacity >= out_rows * c.vocab, "logits buffer too small", LH_ERROR_INVALID_ARGUMENT);
-    const int M = int(count);
+}
+
+void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t host_capacity,
+                      uint32_t* argmax) {
+    validate(ids, count, all_logits, host_logits, host_capacity);
     plan(uint32_t(count), all_logits);
     hipStream_t s = stream();
+    if (count == 1 && !all_logits && graph_decode_ok()) {
+        decode_graphed(ids[0], true, host_logits, argmax);
+        return;
+    }
     std::memcpy(host_ids_, ids, count * sizeof(uint32_t));
     hip_check(hipMemcpyAsync(ids_.ptr, host_ids_, count * sizeof(uint32_t), hipMemcpyHostToDevice, s), "ids upload");
+    launch(int(count), length, all_logits, nullptr, 0);
+    const int head_rows = all_logits ? int(count) : 1;
+    float* logits = logits_.as<float>();
+    launch_argmax(logits + size_t(head_rows - 1) * model.config.vocab, 1, int(model.config.vocab),
+                  argmax_.as<uint32_t>(), s);
+    hip_check(hipMemcpyAsync(host_argmax_, argmax_.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s), "argmax copy");
+    if (host_logits)
+        hip_check(hipMemcpyAsync(host_logits, logits, size_t(head_rows) * model.config.vocab * sizeof(float),
+                                 hipMemcpyDeviceToHost, s), "logits copy");
+    hip_check(hipStreamSynchronize(s), "forward");
+    if (profiler.enabled) profiler.collect();
+    if (argmax) *argmax = *host_argmax_;
+    logits_device = logits;
+    logits_count = size_t(head_rows) * model.config.vocab;
+    length += count;
+    device_position_valid_ = false;
+}
 
+// Single-token decode replayed from a captured graph.  Kernels read the
+// position from device memory; the graph ends with the device argmax, which
+// writes the next input id (for generate_continuation, main_decoder.cpp:95-113),
+// the host-visible argmax and the advanced position.
+bool Session::graph_decode_ok() const {
+    if (profiler.enabled || !graphs_enabled_) return false;
+    const Config& c = model.config;
+    return attention_decode_supported(int(c.heads), int(c.kv_heads), int(c.head_dim));
+}
+
+void Session::decode_graphed(uint32_t id, bool upload_id, float* host_logits, uint32_t* argmax) {
+    const Config& c = model.config;
+    hipStream_t s = stream();
+    const int needed = attention_decode_spans(int(length) + 1, int(c.head_dim));
+    const int most = attention_decode_spans(int(capacity), int(c.head_dim));
+    int bucket = 4;
+    while (bucket < needed) bucket *= 2;
+    bucket = std::min(bucket, most);
+    if (!device_position_valid_) {
+        *host_position_ = int(length);
+        hip_check(hipMemcpyAsync(position_.ptr, host_position_, sizeof(int), hipMemcpyHostToDevice, s), "position");
+        device_position_valid_ = true;
+    }
+    if (upload_id) {
+        *host_ids_ = id;
+        hip_check(hipMemcpyAsync(ids_.ptr, host_ids_, sizeof(uint32_t), hipMemcpyHostToDevice, s), "ids upload");
+    }
+    hipGraphExec_t& exec = graphs_[bucket];
+    if (!exec) {
+        hipGraph_t graph;
+        hip_check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            launch(1, length, false, position_.as<int>(), bucket);
+            launch_argmax_advance(logits_.as<float>(), int(c.vocab), ids_.as<uint32_t>(), mapped_argmax_,
+                                  position_.as<int>(), s);
+        } catch (...) {
+            (void)hipStreamEndCapture(s, &graph);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+        const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        hip_check(st, "hipGraphInstantiate");
+    }
+    hip_check(hipGraphLaunch(exec, s), "hipGraphLaunch");
+    if (host_logits)
+        hip_check(hipMemcpyAsync(host_logits, logits_.ptr, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s),
+                  "logits copy");
+    hip_check(hipStreamSynchronize(s), "decode");
+    if (argmax) *argmax = *host_argmax_;
+    logits_device = logits_.as<float>();
+    logits_count = c.vocab;
+    length += 1;
+}
+
+void Session::drop_graphs() {
+    for (auto& g : graphs_)
+        if (g.second) (void)hipGraphExecDestroy(g.second);
+    graphs_.clear();
+}
+
+// All kernels of one forward up to the logits.  With position_ptr set (graph
+// capture) every position-dependent kernel reads the position from device
+// memory and the decode attention runs a fixed number of key spans.
+void Session::launch(int M, size_t position, bool all_logits, const int* position_ptr, int spans) {
+    const Config& c = model.config;
+    hipStream_t s = stream();
     const int h = int(c.hidden), dim = int(c.head_dim);
     const int qw = int(c.qwidth()), kvw = int(c.kvwidth());
     const int qkv_width = qw + 2 * kvw;
     float* hidden = hidden_.as<float>();
     float* normed = normed_.as<float>();
     launch_embedding(model.embedding, model.has_positions ? &model.positions : nullptr, ids_.as<uint32_t>(), M,
-                     int(position + c.position_offset), c.embedding_scale, hidden, s);
+                     int((position_ptr ? 0 : position) + c.position_offset), c.embedding_scale, hidden, s,
+                     position_ptr);
     const float scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(c.head_dim)));
     const size_t plane = size_t(c.kv_heads) * capacity * dim;
 
@@ -140,8 +312,24 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
         const bool last = layer + 1 == c.layers;
         // ---- attention block
         float* qkv = qkv_.as<float>();
+        float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
+        float* values = keys + plane;
         const bool fuse_in = M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv && !L.qkv.input_scale;
-        if (fuse_in) {
+        // Single-token W8A8: one launch normalizes, quantizes, projects q|k|v,
+        // rotates and appends k, v to the cache.
+        PairEpilogue rope;
+        rope.mode = kPairRopeKv;
+        rope.heads = int(c.heads); rope.kv_heads = int(c.kv_heads); rope.dim = dim;
+        rope.rotary = c.position_kind == 0 ? int(c.rotary_dim) : 0; rope.position = int(position);
+        rope.capacity = int(capacity); rope.cosines = rope_cos_.as<float>(); rope.sines = rope_sin_.as<float>();
+        rope.q_heads = q_heads_.as<float>(); rope.keys = keys; rope.values = values;
+        rope.position_ptr = position_ptr;
+        const bool fuse_rope = fuse_in && !c.qk_norm && dim % 2 == 0 &&
+                               linear_fuses([&] { LinearCall t = make_call(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
+                                                  t.pair = rope; return t; }());
+        if (fuse_rope) {
+            run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm, &rope);
+        } else if (fuse_in) {
             run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
         } else {
             launch_norm(hidden, M, h, L.input_norm, normed, s);
@@ -175,16 +363,15 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
                 launch_norm(row + qw, int(c.kv_heads), dim, kn, row + qw, s);
             }
         }
-        float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
-        float* values = keys + plane;
         RopeKvCall rk;
         rk.qkv = qkv; rk.ld = qkv_width; rk.q_offset = 0; rk.k_offset = qw; rk.v_offset = qw + kvw;
         rk.tokens = M; rk.heads = int(c.heads); rk.kv_heads = int(c.kv_heads); rk.dim = dim;
         rk.rotary = c.position_kind == 0 ? int(c.rotary_dim) : 0;
         rk.position = int(position);
+        rk.position_ptr = position_ptr;
         rk.cosines = rope_cos_.as<float>(); rk.sines = rope_sin_.as<float>();
         rk.q_heads = q_heads_.as<float>(); rk.keys = keys; rk.values = values; rk.capacity = int(capacity);
-        launch_rope_kv(rk, s);
+        if (!fuse_rope) timed(Profiler::Other, 0, 0, [&] { launch_rope_kv(rk, s); });
 
         // After the last layer's KV append only the final row reaches the
         // head (decoder.cpp:1375-1387 trims the MLP the same way; here the
@@ -198,7 +385,15 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
         at.heads = int(c.heads); at.kv_heads = int(c.kv_heads); at.tokens = M; at.position = int(position);
         at.dim = dim; at.capacity = int(capacity); at.window = int(c.sliding_window); at.scale = scale;
         at.partial = partial_.as<float>(); at.partial_capacity = int(partial_.bytes / sizeof(float));
-        launch_attention(at, s);
+        at.counters = counters_.as<unsigned>();
+        at.position_ptr = position_ptr;
+        at.spans = spans;
+        {
+            // KV bytes read: keys and values of every visible position, per query row.
+            const double kv_bytes = 2.0 * 4.0 * c.kv_heads * dim * double(position + M) * (M == 1 ? 1 : 0.5 * M);
+            timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M,
+                  [&] { check(launch_attention(at, s), "attention launch rejected", LH_ERROR_UNSUPPORTED); });
+        }
         const float* attn_rows = attn_.as<float>() + size_t(first_row) * qw;
         float* hid = hidden + size_t(first_row) * h;
         float* attn_proj = attn_proj_.as<float>();
@@ -214,7 +409,18 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
         if (c.gated) {
             const bool fuse_post = rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up &&
                                    !L.gate_up.input_scale;
-            if (fuse_post) {
+            PairEpilogue gated;
+            gated.mode = kPairGated;
+            gated.width = f;
+            gated.activation = int(c.activation);
+            gated.act = act;
+            const bool fuse_act = fuse_post &&
+                                  linear_fuses([&] { LinearCall t = make_call(L.gate_up, hid, rows, gate_up, kStore,
+                                                                              &L.post_norm);
+                                                     t.pair = gated; return t; }());
+            if (fuse_act) {
+                run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm, &gated);
+            } else if (fuse_post) {
                 run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm);
             } else {
                 launch_norm(hid, rows, h, L.post_norm, normed, s);
@@ -232,7 +438,7 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
                     }
                 }
             }
-            launch_activation(gate_up, rows, f, 1, int(c.activation), act, s);
+            if (!fuse_act) timed(Profiler::Other, 0, 0, [&] { launch_activation(gate_up, rows, f, 1, int(c.activation), act, s); });
         } else {
             launch_norm(hid, rows, h, L.post_norm, normed, s);
             run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
@@ -249,24 +455,12 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
     }
     const int head_rows = all_logits ? M : 1;
     // `hidden` now points at the rows the head reads: all rows, or the last one.
-    const float* head_in = hidden;
-    const float* x = head_in;
+    const float* x = hidden;
     if (c.final_norm) {
-        launch_norm(head_in, head_rows, h, model.final_norm, normed, s);
+        launch_norm(hidden, head_rows, h, model.final_norm, normed, s);
         x = normed;
     }
-    float* logits = logits_.as<float>();
-    run_linear(model.head, x, head_rows, logits, kStore, nullptr);
-    launch_argmax(logits + size_t(head_rows - 1) * c.vocab, 1, int(c.vocab), argmax_.as<uint32_t>(), s);
-    hip_check(hipMemcpyAsync(host_argmax_, argmax_.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s), "argmax copy");
-    if (host_logits)
-        hip_check(hipMemcpyAsync(host_logits, logits, size_t(head_rows) * c.vocab * sizeof(float),
-                                 hipMemcpyDeviceToHost, s), "logits copy");
-    hip_check(hipStreamSynchronize(s), "forward");
-    if (argmax) *argmax = *host_argmax_;
-    logits_device = logits;
-    logits_count = size_t(head_rows) * c.vocab;
-    length = position + count;
+    run_linear(model.head, x, head_rows, logits_.as<float>(), kStore, nullptr);
 }
 
 }  // namespace leafhip

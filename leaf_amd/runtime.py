@@ -39,6 +39,11 @@ class ModelInfo(C.Structure):
         ("artifact_bytes", C.c_uint64), ("device_bytes", C.c_uint64)]
 
 
+class ProfileEntry(C.Structure):
+    _fields_ = [("name", C.c_char * 24), ("launches", C.c_uint64), ("milliseconds", C.c_double),
+                ("bytes", C.c_double), ("operations", C.c_double)]
+
+
 class SessionOptions(C.Structure):
     _fields_ = [("max_context", C.c_uint32), ("max_prefill", C.c_uint32)]
 
@@ -75,12 +80,16 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_forward": ([vp, vp, sz, i32, vp, sz, vp], i32),
         "lh_generate": ([vp, vp, sz, u32, vp, C.POINTER(sz), vp, vp], i32),
         "lh_session_logits_device": ([vp, C.POINTER(vp), C.POINTER(sz)], i32),
+        "lh_session_set_profiling": ([vp, i32], i32),
+        "lh_session_profile": ([vp, vp, sz, C.POINTER(sz)], i32),
         "lh_device_alloc": ([sz, C.POINTER(vp)], i32), "lh_device_free": ([vp], i32),
         "lh_copy_to_device": ([vp, vp, sz], i32), "lh_copy_to_host": ([vp, vp, sz], i32),
         "lh_memset_device": ([vp, i32, sz], i32), "lh_synchronize": ([], i32),
         "lh_stream_create": ([C.POINTER(vp)], i32), "lh_stream_destroy": ([vp], i32),
         "lh_stream_synchronize": ([vp], i32),
         "lh_timer_start": ([vp, C.POINTER(vp)], i32), "lh_timer_stop": ([vp, vp, C.POINTER(C.c_double)], i32),
+        "lh_stream_begin_capture": ([vp], i32), "lh_stream_end_capture": ([vp, C.POINTER(vp)], i32),
+        "lh_graph_launch": ([vp, vp], i32), "lh_graph_destroy": ([vp], i32),
         "lh_quantize_rows_i8": ([vp, sz, sz, vp, vp, vp], i32),
         "lh_linear": ([C.POINTER(Weight), vp, sz, u32, vp, vp, vp], i32),
         "lh_linear_q": ([C.POINTER(Weight), vp, vp, sz, vp, vp, vp], i32),
@@ -257,6 +266,17 @@ class Decoder:
         n = produced.value
         return tokens[:n].tolist(), prefill.value, decode[:max(n - 1, 0)].tolist()
 
+    def set_profiling(self, enable: bool) -> None:
+        check(library().lh_session_set_profiling(self._session, int(enable)))
+
+    def profile(self) -> dict:
+        """Per-kernel-class device time since the last call: {name: {launches, ms, bytes, ops}}."""
+        entries = (ProfileEntry * 16)()
+        n = C.c_size_t()
+        check(library().lh_session_profile(self._session, C.cast(entries, C.c_void_p), 16, C.byref(n)))
+        return {e.name.decode(): {"launches": e.launches, "ms": e.milliseconds, "bytes": e.bytes,
+                                  "ops": e.operations} for e in entries[:n.value]}
+
     @property
     def vocabulary_size(self) -> int:
         return self.info.vocab
@@ -297,6 +317,48 @@ def linear_q(weight: DeviceWeight, q: DeviceArray, scales: DeviceArray, tokens: 
 
 def quantize_rows(x: DeviceArray, rows: int, cols: int, q: DeviceArray, scales: DeviceArray, stream=None) -> None:
     check(library().lh_quantize_rows_i8(x.ptr, rows, cols, q.ptr, scales.ptr, stream))
+
+
+class Stream:
+    """A library-created HIP stream (needed for graph capture)."""
+
+    def __init__(self):
+        self.handle = C.c_void_p()
+        check(library().lh_stream_create(C.byref(self.handle)))
+
+    def synchronize(self):
+        check(library().lh_stream_synchronize(self.handle))
+
+    def close(self):
+        if getattr(self, "handle", None) and self.handle.value:
+            library().lh_stream_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+    __del__ = close
+
+
+class Graph:
+    """Work captured from a stream and replayed as one HIP graph."""
+
+    def __init__(self, stream: Stream, record):
+        check(library().lh_stream_begin_capture(stream.handle))
+        try:
+            record()
+        finally:
+            self.handle = C.c_void_p()
+            status = library().lh_stream_end_capture(stream.handle, C.byref(self.handle))
+        check(status)
+        self.stream = stream
+
+    def launch(self):
+        check(library().lh_graph_launch(self.handle, self.stream.handle))
+
+    def close(self):
+        if getattr(self, "handle", None) and self.handle.value:
+            library().lh_graph_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+    __del__ = close
 
 
 class Timer:

@@ -12,8 +12,17 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-# max |gpu - cpu| / max |cpu| over the logits of a forward
+# max |gpu - cpu| / max |cpu| over the logits of a forward.  FP32 / BF16 /
+# weight-only INT4 models: 1e-3.  W8A8 models: 2e-2 -- the GPU sums the norm
+# and softmax reductions in another order than the CPU, a 1-ulp difference in
+# an activation can move it across an int8 rounding boundary, and that whole
+# quantization step then shows in the logits; greedy tokens must still agree.
 LOGIT_TOLERANCE = 1e-3
+W8A8_LOGIT_TOLERANCE = 2e-2
+
+
+def tolerance(activation_bits):
+    return W8A8_LOGIT_TOLERANCE if activation_bits == 8 else LOGIT_TOLERANCE
 
 
 def rel_error(a, b):
@@ -41,12 +50,12 @@ def test_chunked_logits_and_greedy_tokens_match_reference(runtime, oracle, golde
     ref_rows = arrays[f"{family}_logits_rows"]
     err = rel_error(logits[m["rows"]], ref_rows)
     print(f"{family}: chunked all-logits relative error {err:.2e}")
-    assert err <= LOGIT_TOLERANCE
+    assert err <= tolerance(m["activation_bits"])
     # every row against the oracle (same arithmetic as the reference)
     od = oracle.decoder(artifacts[family], m["activation_bits"], m["fp32_math"] == "accurate")
     full = np.concatenate([od.forward(prompt[p:p + m["chunk"]], all_logits=True)
                            for p in range(0, len(prompt), m["chunk"])])
-    assert rel_error(logits, full) <= LOGIT_TOLERANCE
+    assert rel_error(logits, full) <= tolerance(m["activation_bits"])
     dec.reset()
     assert dec.cache_tokens() == 0
     tokens, prefill_ms, decode_ms = dec.generate(prompt, 10)
@@ -63,7 +72,7 @@ def test_decode_steps_match_oracle_token_by_token(runtime, oracle, artifacts, fa
     rng = np.random.default_rng(77)
     prompt = rng.integers(0, dec.vocabulary_size, 33).astype(np.uint32)   # >= 32: final-layer trim on the CPU
     a, b = dec.forward(prompt), od.forward(prompt)
-    assert rel_error(a, b) <= LOGIT_TOLERANCE
+    assert rel_error(a, b) <= tolerance(bits)
     worst = 0.0
     for step in range(24):
         tok = int(np.argmax(b))
@@ -72,7 +81,7 @@ def test_decode_steps_match_oracle_token_by_token(runtime, oracle, artifacts, fa
         a, b = dec.forward([tok]), od.forward([tok])
         worst = max(worst, rel_error(a, b))
     print(f"{family}: worst decode-step relative logit error {worst:.2e}")
-    assert worst <= LOGIT_TOLERANCE
+    assert worst <= tolerance(bits)
     dec.close()
 
 
@@ -111,3 +120,34 @@ def test_rejects_corrupt_artifacts(runtime, tmp_path, artifacts):
         runtime.Decoder(artifacts["tinyllama"], 8, "accurate")
     with pytest.raises(runtime.LeafError, match="source BF16 storage requires FP32 activations"):
         runtime.Decoder(artifacts["smollm2"], 8)
+
+
+@pytest.mark.parametrize("family,prompt_tokens", [("gpt2", 150), ("tinyllama", 230), ("qwen", 230),
+                                                  ("smollm2", 230)])
+def test_graph_replayed_decode_is_bit_identical_to_eager(runtime, artifacts, monkeypatch, family, prompt_tokens):
+    """Single-token steps replay a captured graph per attention-span bucket
+    (device-resident position, device argmax feeding the next id); the result
+    must not differ by a bit from launching the same kernels one by one,
+    across bucket boundaries and after a reset."""
+    from leaf_amd import models
+    bits, math = models.RUN_POLICY[family]
+    rng = np.random.default_rng(5)
+    runs = []
+    for graphs in ("1", "0"):
+        monkeypatch.setenv("LEAF_DECODE_GRAPH", graphs)
+        dec = runtime.Decoder(artifacts[family], bits, math, max_context=prompt_tokens + 70)
+        prompt = (rng.integers(0, dec.vocabulary_size, prompt_tokens).astype(np.uint32) if graphs == "1"
+                  else runs[0][0])
+        logits, tokens = [], []
+        for rep in range(2):
+            dec.reset()
+            tok = dec.forward_into(prompt, None)
+            for _ in range(60):                      # 230-token prompts cross 256 keys
+                row = dec.forward([tok])
+                logits.append(row)
+                tok = int(dec.last_argmax.value)
+                tokens.append(tok)
+        dec.close()
+        runs.append((prompt, np.stack(logits), tokens))
+    assert runs[0][2] == runs[1][2]
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
