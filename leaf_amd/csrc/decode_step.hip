@@ -1,0 +1,1031 @@
+// Persistent single-token decode step for W8A8 decoders on MI355X (gfx950).
+//
+// Why one launch per token: a TinyLlama-shape layer streams 44 MB of int8
+// weights (5.5 us at 8 TB/s), but as seven separate launches it costs ~36 us,
+// because each launch pays wave start-up, a cold HBM round trip and its
+// reductions in series.  Here one block of 512 threads per CU stays resident
+// for the whole token, and its waves split into two roles:
+//
+//   * 2 exchange waves move the activation vectors between blocks.  Phases
+//     hand vectors to each other through exchange buffers of 64-bit words
+//     (epoch << 32 | f32 bits), written and read with agent-scope relaxed
+//     atomics: a reader spins on the data itself until every word carries the
+//     epoch of the phase it waits for -- no fences, no barrier counters (one
+//     round trip, ~2 us, against ~8 us for fenced barriers, measured).  Every
+//     block normalizes and quantizes the whole input vector itself (the
+//     per-token absmax of the W8A8 quantization is global) and posts the int8
+//     vector in LDS.  These waves also run attention: (KV head, span of 64
+//     keys) items whose cached keys are fetched during the q|k|v phase, merged
+//     by the last span of each KV head to arrive (per-head counter).
+//   * 6 weight waves own whole rows of every matrix of a layer and keep them
+//     in registers.  After computing a phase they load the same phase of the
+//     next layer, so the weight stream runs a full layer ahead of the
+//     dependency chain.  They wait for their input on an LDS flag, which
+//     counts on lgkmcnt: the loads in flight (vmcnt) never delay that wait,
+//     the way they would delay an exchange poll issued behind them.
+//
+// Arithmetic per output is that of the multi-launch path: exact int32 dot,
+// ((float)acc * s_x) * s_w + bias, residual adds as y + v, RoPE a*c - b*s /
+// b*c + a*s with the host-built tables, SiLU gate up * silu(gate).  Every spin
+// is bounded: on timeout a block raises the abort flag, which every other
+// block observes, and all blocks leave the kernel.
+#include "decode_step.h"
+
+#include <math.h>
+
+#include "device_common.h"
+
+namespace leafhip {
+namespace {
+
+typedef unsigned long long u64;
+
+// Global-address-space views of generic pointers: the loads and atomics then
+// compile to global_* instructions, which count only on vmcnt, so waiting for
+// LDS never waits for the weight stream in flight.
+#define LEAF_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *(const LEAF_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ void stg(T* p, T v) {
+    *(LEAF_GLOBAL T*)p = v;
+}
+__device__ __forceinline__ v4u ldg_stream(const void* p) {
+    return __builtin_nontemporal_load((const LEAF_GLOBAL v4u*)p);
+}
+
+constexpr int kT = kStepThreads;                             // 512
+constexpr int kWaves = kT / kWave;                           // 8: two per SIMD, 256 VGPRs each
+constexpr int kA = 2;                                        // exchange waves
+constexpr int kAT = kA * kWave;                              // exchange lanes
+constexpr int kB = kWaves - kA;                              // weight waves
+constexpr int kKCH = kStepMaxHidden / 16 / kWave;            // 16-byte chunks per lane, hidden-wide int8 row
+constexpr int kKCF = kStepMaxFfn / 16 / kWave;               // ... ffn-wide int8 row
+constexpr int kNH = (kStepMaxHidden + kAT - 1) / kAT;        // hidden values per exchange lane
+constexpr int kNF = (kStepMaxFfn + kAT - 1) / kAT;           // ffn values per exchange lane
+constexpr int kSpanF4 = kStepSpanKeys * kStepDim / 4;        // float4 of a K (or V) span
+constexpr int kNQ = (kStepMaxGroup * kStepDim + kAT - 1) / kAT + 1;   // q values (+ new k or v) per exchange lane
+constexpr int kNK = kSpanF4 / kAT;                           // float4 of a K (or V) span per exchange lane
+static_assert(kNK * kAT == kSpanF4, "exchange lanes cover a span exactly");
+constexpr int kQP = 1;                                       // q|k|v pairs per weight wave
+constexpr int kOR = 2;                                       // o / down rows per weight wave
+constexpr int kGP = 4;                                       // gate|up pairs per weight wave
+constexpr int kHeadsA = (kStepMaxGroup + kA - 1) / kA;       // query heads per exchange wave
+constexpr int kKStride = kStepDim + 4;                       // padded K row in LDS
+constexpr int kMergeBatch = 8;                               // span partials polled together
+constexpr unsigned kSpinLimit = 1u << 20;                    // about a second of polling
+
+static_assert(sizeof(StepLayer) % 16 == 0, "layer descriptors are copied as 16-byte words");
+
+struct __align__(16) Shared {
+    // Layer descriptors, copied once: read from LDS they are not vector loads,
+    // which would wait (in order) behind every weight prefetch in flight.
+    unsigned char layer_bytes[kStepMaxLayers * sizeof(StepLayer)];
+    int8_t xq[2][kStepMaxFfn];      // quantized input, double-buffered by phase
+    float h_in[kStepMaxHidden];     // layer input (residual of o_proj)
+    float h_mid[kStepMaxHidden];    // after o_proj (residual of down_proj)
+    float xf[kStepMaxHidden];       // normalized FP32 input of the head
+    float k[kStepSpanKeys * kKStride];
+    float v[kStepSpanKeys * kStepDim];
+    float q[kStepMaxGroup * kStepDim];
+    float e[kStepMaxGroup * kStepSpanKeys];
+    float sx[2];                    // activation scale per xq buffer
+    float red[2 * kA];              // exchange-wave reductions: [parity][wave]
+    float best_v[kWaves];
+    int best_i[kWaves];
+    int ready;                      // last phase whose input the exchange waves posted
+    int a_count;                    // exchange-wave barrier arrivals
+    int abort;
+    int last;                       // this block merges the attention spans of its KV head
+};
+
+__device__ __forceinline__ const StepLayer& layer_at(const Shared& s, int L) {
+    return reinterpret_cast<const StepLayer*>(s.layer_bytes)[L];
+}
+
+__device__ __forceinline__ u64 tagged(unsigned epoch, float v) {
+    return (u64(epoch) << 32) | __float_as_uint(v);
+}
+__device__ __forceinline__ void publish(u64* p, unsigned epoch, float v) {
+    __hip_atomic_store((LEAF_GLOBAL u64*)p, tagged(epoch, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 fetch(const u64* p) {
+    return __hip_atomic_load((const LEAF_GLOBAL u64*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool aborted(const unsigned* flag) {
+    return __hip_atomic_load((const LEAF_GLOBAL unsigned*)flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+__device__ __forceinline__ void raise_abort(const StepParams& P) {
+    __hip_atomic_store((LEAF_GLOBAL unsigned*)P.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (P.host_abort) *P.host_abort = 1u;
+}
+__device__ __forceinline__ int lds_load(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Completes this wave's LDS accesses and keeps the compiler from moving
+// memory operations across (no vmcnt wait: loads in flight stay in flight).
+__device__ __forceinline__ void lds_done() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Waits until src[index(i)] carries `epoch` for every i < N whose index is
+// not negative (absent elements read as 0); the values land in out[].  All
+// loads are issued together and only missing words are polled again; indices
+// are recomputed per poll rather than held in registers.  Returns false (after
+// raising the abort flag) on timeout or when another block aborted.
+template <int N, typename Index>
+__device__ __forceinline__ bool await(const u64* src, Index index, unsigned epoch, float (&out)[N],
+                                      const StepParams& P) {
+    // Branch-free: absent elements load word 0 and are replaced by a tagged
+    // zero; a lane that is still missing a word re-polls its whole set.
+    u64 w[N];
+    auto poll = [&] {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int k = index(i);
+            const u64 v = fetch(src + (k >= 0 ? k : 0));
+            w[i] = k >= 0 ? v : tagged(epoch, 0.0f);
+        }
+    };
+    poll();
+    for (unsigned spin = 0;; ++spin) {
+        bool ready = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) ready = ready && unsigned(w[i] >> 32) == epoch;
+        if (ready) break;
+        if (spin >= kSpinLimit || ((spin & 255u) == 255u && aborted(P.abort_flag))) {
+            raise_abort(P);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        poll();
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __uint_as_float(unsigned(w[i]));
+    return true;
+}
+
+// Exchange-lane ownership of a vector: lane a holds x[4 g + j] = element
+// 4 (g kAT + a) + j.  Quads of consecutive elements keep LDS stores and gamma
+// loads 16 bytes wide, while each load instruction of a wave covers 64
+// neighbouring quads (coalesced: the exchange words live in uncached memory,
+// where a strided word costs a whole memory transaction).  Vectors handled
+// this way have n % 4 == 0 and buffers of at least kAT * N words.
+__device__ __forceinline__ int quad_of(int g, int a) { return g * kAT + a; }
+
+// A raw buffer resource over exchange words: its loads take a per-lane
+// 32-bit offset plus a wave-uniform SGPR offset, so a lane's quads need one
+// address register rather than one 64-bit address per word.  Loads use sc1
+// (coherent at agent scope), like the atomic loads of fetch().
+constexpr int kRawBufferWord3 = 0x00020000;   // descriptor word 3 of a raw (untyped) buffer on gfx9
+constexpr int kLoadSc1 = 16;                  // cache-policy bit sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t exchange_view(const u64* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(base), (short)0, 0x7fffffff, kRawBufferWord3);
+}
+
+// Spins until *p carries `epoch`; false (abort raised) on timeout or abort.
+__device__ __forceinline__ bool spin_until(const u64* p, unsigned epoch, unsigned& spin, const StepParams& P) {
+    while (unsigned(fetch(p) >> 32) != epoch) {
+        if (++spin >= kSpinLimit || ((spin & 255u) == 255u && aborted(P.abort_flag))) {
+            raise_abort(P);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
+// This lane's quads of the n-element vector src once they all carry
+// `epoch`; elements past n read as 0 and are not waited for.  A lane first
+// watches one word it needs, then reads all of them; a word still missing is
+// watched alone before the next full read (a full re-read per spin from every
+// lane of every block would crowd the memory pipeline the weight waves use).
+template <int N>
+__device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoch, float (&out)[N], int a,
+                                            const StepParams& P) {
+    static_assert(N % 4 == 0, "groups of four words");
+    constexpr int G = N / 4;
+    const int live = n / 4 - a;   // quad g of this lane is inside the vector when g * kAT < live
+    const u64* mine = src + 4 * a;
+    unsigned spin = 0;
+    if (live > 0 && !spin_until(mine + 4 * kAT * min(G - 1, (live - 1) / kAT) + 3, epoch, spin, P)) return false;
+    const __amdgpu_buffer_rsrc_t view = exchange_view(src);
+    u64 w[N];
+    for (;;) {
+        asm volatile("" ::: "memory");   // a fresh read each time round
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(view, 32 * a + 8 * (i % 4), 32 * kAT * (i / 4), kLoadSc1);
+            w[i] = (u64(v.y) << 32) | v.x;
+        }
+        int missing = -1;
+#pragma unroll
+        for (int i = N - 1; i >= 0; --i)
+            missing = ((i / 4) * kAT < live && unsigned(w[i] >> 32) != epoch) ? i : missing;
+        if (missing < 0) break;
+        if (!spin_until(mine + 4 * kAT * (missing >> 2) + (missing & 3), epoch, spin, P)) return false;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = (i / 4) * kAT < live ? __uint_as_float(unsigned(w[i])) : 0.0f;
+    return true;
+}
+
+// One word once it carries `epoch` (wanted false: 0 without waiting).
+__device__ __forceinline__ bool await_one(const u64* p, bool wanted, unsigned epoch, float& out, const StepParams& P) {
+    unsigned spin = 0;
+    out = 0.0f;
+    if (!wanted) return true;
+    if (!spin_until(p, epoch, spin, P)) return false;
+    out = __uint_as_float(unsigned(fetch(p)));
+    return true;
+}
+
+// ------------------------------------------------------ exchange waves ---
+// Barrier of the exchange waves (an LDS arrival counter).  Returns false
+// when the kernel is being abandoned.
+__device__ __forceinline__ bool a_sync(Shared& s, int& round) {
+    lds_done();
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&s.a_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    round += kA;
+    for (unsigned spin = 0; lds_load(&s.a_count) < round; ++spin) {
+        if (spin > kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(0);
+    }
+    asm volatile("" ::: "memory");
+    return true;
+}
+
+// The exchange waves agree on `ok`; false means all of them leave the kernel.
+__device__ __forceinline__ bool a_agree(bool ok, Shared& s, int& round) {
+    if (!__all(ok) && (threadIdx.x & 63) == 0) lds_store(&s.abort, 1);
+    if (!a_sync(s, round)) return false;
+    return lds_load(&s.abort) == 0;
+}
+
+// Sums (or maxes) over the exchange lanes; every exchange wave gets the same bits.
+__device__ __forceinline__ float a_sum(float v, Shared& s, int& round, int& parity) {
+    v = wave_sum_f32(v);
+    if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
+    a_sync(s, round);
+    float r = s.red[kA * parity];
+#pragma unroll
+    for (int w = 1; w < kA; ++w) r += s.red[kA * parity + w];
+    parity ^= 1;
+    return r;
+}
+__device__ __forceinline__ float a_max(float v, Shared& s, int& round, int& parity) {
+    v = wave_max_f32(v);
+    if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
+    a_sync(s, round);
+    float r = s.red[kA * parity];
+#pragma unroll
+    for (int w = 1; w < kA; ++w) r = fmaxf(r, s.red[kA * parity + w]);
+    parity ^= 1;
+    return r;
+}
+
+// Posts phase `phase`: every exchange wave has finished writing its input.
+__device__ __forceinline__ void post(Shared& s, int phase, int& round) {
+    a_sync(s, round);
+    if (threadIdx.x == 0) lds_store(&s.ready, phase);
+}
+
+// RMSNorm of the n values held as quads (decoder.cpp:706-727).
+template <int N>
+__device__ __forceinline__ void rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
+                                              Shared& s, int& round, int& parity) {
+    const int live = n / 4 - a;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) sq += (i / 4) * kAT < live ? x[i] * x[i] : 0.0f;
+    sq = a_sum(sq, s, round, parity);
+    const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
+}
+
+// Per-token symmetric int8 quantization into s.xq[buf] (decoder.cpp:1028-1043).
+// Quads past n (zeros) land in the buffer's tail, which no reader uses.
+template <int N>
+__device__ __forceinline__ void quantize_into(const float (&x)[N], int n, int buf, int a, Shared& s, int& round,
+                                              int& parity) {
+    static_assert(N % 4 == 0, "quads");
+    const int live = n / 4 - a;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / 4) * kAT < live ? fabsf(x[i]) : 0.0f);
+    amax = a_max(amax, s, round, parity);
+    const float sx = fmaxf(amax / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+#pragma unroll
+    for (int g = 0; g < N / 4; ++g) {
+        const float* v = x + 4 * g;
+        *reinterpret_cast<uint32_t*>(s.xq[buf] + 4 * quad_of(g, a)) =
+            (uint32_t)(quantize_one(v[0], multiplier) & 255) |
+            ((uint32_t)(quantize_one(v[1], multiplier) & 255) << 8) |
+            ((uint32_t)(quantize_one(v[2], multiplier) & 255) << 16) |
+            ((uint32_t)(quantize_one(v[3], multiplier) & 255) << 24);
+    }
+    if (a == 0) s.sx[buf] = sx;
+}
+
+// This lane's quads into dst (natural element order; dst holds kAT * N floats).
+template <int N>
+__device__ __forceinline__ void store_quads(float* dst, const float (&x)[N], int a) {
+    static_assert(N % 4 == 0, "quads");
+#pragma unroll
+    for (int g = 0; g < N / 4; ++g)
+        *reinterpret_cast<v4f*>(dst + 4 * quad_of(g, a)) = v4f{x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]};
+}
+
+// gamma for this lane's quads; quads past n read the last one (their x are 0).
+template <int N>
+__device__ __forceinline__ void fetch_gamma(float (&g)[N], const float* gamma, int n, int a) {
+    static_assert(N % 4 == 0, "quads");
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+        const v4f v = ldg(reinterpret_cast<const v4f*>(gamma + 4 * min(quad_of(q, a), n / 4 - 1)));
+        g[4 * q] = v[0];
+        g[4 * q + 1] = v[1];
+        g[4 * q + 2] = v[2];
+        g[4 * q + 3] = v[3];
+    }
+}
+
+// -------------------------------------------------------- weight waves ---
+// One int8 row of `m` into registers: lane holds chunks lane + 64 j.  Slots
+// past the row end reload its last chunk (same cache line as a neighbour's
+// load, so no extra traffic); row_dot ignores them.  Branch-free, so every
+// load of a phase is in flight at once.  A row the wave does not need (live
+// false: not owned, or past the last layer) is still loaded, from one 16-byte
+// chunk the whole wave shares: every phase then issues the same loads on
+// every path, which keeps the compiler's in-order wait counts exact across
+// the layer loop (with a path that skips loads it must assume the worst and
+// waits for every load in flight, next-layer prefetches included).
+template <int KC>
+__device__ __forceinline__ void load_row(v4u (&w)[KC], const WeightView& m, int row, int lane, bool live) {
+    const int last = m.cols / 16 - 1;
+    const uint8_t* base = static_cast<const uint8_t*>(m.data) + (size_t)(live ? row : 0) * m.cols;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) w[j] = ldg_stream(base + 16 * (live ? min(lane + kWave * j, last) : 0));
+}
+
+// Exact int32 dot of a register-held row with the int8 input in LDS, summed over the wave.
+template <int KC>
+__device__ __forceinline__ int row_dot(const v4u (&w)[KC], const int8_t* xq, int chunks, int lane) {
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+        const int c = lane + kWave * j;
+        const v4u x = *reinterpret_cast<const v4u*>(xq + 16 * min(c, chunks - 1));
+        int a = dot4((int)w[j].x, (int)x.x, 0);
+        a = dot4((int)w[j].y, (int)x.y, a);
+        a = dot4((int)w[j].z, (int)x.z, a);
+        a = dot4((int)w[j].w, (int)x.w, a);
+        acc += c < chunks ? a : 0;
+    }
+    return wave_sum_i32(acc);
+}
+
+// ((float)acc * s_x) * s_w + b  (decoder.cpp:568, 1229), separate roundings.
+__device__ __forceinline__ float dequant(int acc, float sx, float sw, float bias) {
+    const float term = (float)acc * sx;
+    return term * sw + bias;
+}
+
+// Per-row scale and bias, fetched a layer ahead like the rows.
+struct RowScale {
+    float scale = 0.0f, bias = 0.0f;
+    __device__ __forceinline__ void fetch(const WeightView& m, int r, bool live) {
+        scale = ldg(m.scales + (live ? r : 0));
+        bias = ldg(m.bias + (live ? r : 0));
+    }
+};
+
+// Rows of rotate-half pair p of a stacked [q | k | v] projection: (i, i + rotary/2)
+// in rotated heads, neighbouring rows elsewhere.
+__device__ __forceinline__ void rope_rows(int p, int heads, int kv_heads, int rotary, int& r0, int& r1) {
+    const int per_head = kStepDim / 2, half = rotary / 2;
+    const int hb = p / per_head, j = p % per_head;
+    const bool rotated = hb < heads + kv_heads;
+    if (rotated && j < half) {
+        r0 = hb * kStepDim + j;
+        r1 = r0 + half;
+    } else {
+        const int base = rotated ? rotary : 0;
+        r0 = hb * kStepDim + base + 2 * (rotated ? j - half : j);
+        r1 = r0 + 1;
+    }
+}
+
+__device__ __forceinline__ float activate(int activation, float x) {
+    // Decoder::Impl::activate (decoder.cpp:982-987)
+    if (activation == 0) return x / (1.0f + expf(-x));
+    if (activation == 1) return 0.5f * x * (1.0f + erff(x * 0.7071067811865475f));
+    if (activation == 2) return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+    return x < 0.0f ? 0.0f : x;
+}
+
+__device__ __forceinline__ float embed_value(const WeightView& w, uint32_t id, int c) {
+    const size_t index = (size_t)id * w.cols + c;
+    if (w.bits == 32) return ldg(static_cast<const float*>(w.data) + index);
+    return (float)ldg(static_cast<const int8_t*>(w.data) + index) * ldg(w.scales + id);
+}
+
+// Waits (weight waves) until the exchange waves posted `phase`.
+__device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
+    for (unsigned spin = 0;; ++spin) {
+        if (lds_load(&s.ready) >= phase) break;
+        if (lds_load(&s.abort) || spin > 64 * kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+    return true;
+}
+
+// Phase timeline: the first thread of each role stamps the 100 MHz device
+// clock at phase boundaries into trace[block][point]: points 64 * layer + k
+// (k < 8 exchange waves, 8 + 8 * w + j weight wave w), then the head's.  Off (null)
+// outside diagnostics.
+__device__ __forceinline__ void stamp(unsigned long long* trace, int block, int point, int thread = 0) {
+    if (trace && threadIdx.x == thread)
+        stg(trace + (size_t)block * kStepTracePoints + point, (unsigned long long)__builtin_amdgcn_s_memrealtime());
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// Where the rows of one block sit: q|k|v rotate-half pairs, o/down rows and
+// gate|up pairs are split into contiguous ranges per block.
+struct Ownership {
+    int q_first, q_end, r_first, r_end, g_first, g_end;
+    __device__ Ownership(const StepParams& P, int b, int G) {
+        const int nq = (P.heads + 2 * P.kv_heads) * kStepDim / 2;
+        q_first = (int)((long long)b * nq / G);
+        q_end = (int)((long long)(b + 1) * nq / G);
+        r_first = (int)((long long)b * P.hidden / G);
+        r_end = (int)((long long)(b + 1) * P.hidden / G);
+        g_first = (int)((long long)b * P.ffn / G);
+        g_end = (int)((long long)(b + 1) * P.ffn / G);
+    }
+};
+
+// ======================================================= exchange role ===
+// Returns false when the kernel is abandoned (abort).
+__device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
+    int a = threadIdx.x;                     // 0 .. kAT - 1
+    const int G = gridDim.x, b = blockIdx.x;
+    const int H = P.hidden, F = P.ffn, dim = kStepDim;
+    const int qw = P.heads * dim, kvw = P.kv_heads * dim;
+    const int group = P.heads / P.kv_heads;
+    const int pos = P.position;
+    int round = 0, parity = 0;
+    auto epoch = [&](int layer, int phase) { return P.epoch + (unsigned)(layer * 8 + phase); };
+    (void)G;
+
+    // this block's attention item: (KV head, span of keys)
+    const int end = pos + 1;
+    const int begin = (P.window > 0 && end > P.window) ? end - P.window : 0;
+    const int spans = (end - begin + kStepSpanKeys - 1) / kStepSpanKeys;
+    const bool has_item = b < P.kv_heads * spans;
+    const int item_g = has_item ? b / spans : 0, item_s = has_item ? b % spans : 0;
+    const int k0 = begin + item_s * kStepSpanKeys, k1 = min(end, k0 + kStepSpanKeys);
+    const int cached_end = min(k1, pos), keys = k1 - k0;
+    const bool new_key = pos >= k0 && pos < k1;
+
+    float x[kNH];
+    {
+        const uint32_t id = ldg(P.token);
+#pragma unroll
+        for (int i = 0; i < kNH; ++i) {
+            const int e = 4 * quad_of(i / 4, a) + i % 4;
+            x[i] = e < H ? embed_value(P.embedding, id, e) * P.embedding_scale : 0.0f;
+        }
+    }
+    for (int L = 0; L < P.layers; ++L) {
+        // A fresh copy of the lane index per layer keeps per-lane address
+        // arithmetic inside the loop instead of hoisting dozens of 64-bit
+        // addresses into registers for the whole kernel.
+        asm volatile("" : "+v"(a));
+        const int lane = a & 63, aw = a >> 6;
+        const StepLayer& Ly = layer_at(s, L);
+        const float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
+        const float* Vc = Kc + (size_t)P.kv_heads * P.capacity * dim;
+        float gamma[kNH];
+        fetch_gamma(gamma, Ly.input_gamma, H, a);
+
+        // ---- layer input (x, polled at the end of the previous layer) -> RMSNorm -> int8 for q|k|v
+        stamp(P.trace, b, 64 * L + 1);
+        // cached keys and values of this block's span (rows past the cached
+        // ones load key 0 again; they are overwritten or never read)
+        v4u kv_pre[2 * kNK] = {};
+        if (has_item) {
+#pragma unroll
+            for (int j = 0; j < kNK; ++j) {
+                const int f = a + kAT * j, key = k0 + f / 16, part = f % 16;   // 16 float4 per 64-float row
+                const size_t at = ((size_t)item_g * P.capacity + (key < cached_end ? key : 0)) * dim + 4 * part;
+                kv_pre[j] = ldg(reinterpret_cast<const v4u*>(Kc + at));
+                kv_pre[kNK + j] = ldg(reinterpret_cast<const v4u*>(Vc + at));
+            }
+        }
+        store_quads(s.h_in, x, a);
+        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
+        quantize_into(x, H, 0, a, s, round, parity);
+        post(s, 4 * L + 0, round);
+        stamp(P.trace, b, 64 * L + 2);
+        if (has_item) {
+            // the cached keys and values, loaded during the norm, into LDS
+#pragma unroll
+            for (int j = 0; j < kNK; ++j) {
+                const int f = a + kAT * j, kl = f / 16, part = f % 16;
+                *reinterpret_cast<v4u*>(s.k + kl * kKStride + 4 * part) = kv_pre[j];
+                *reinterpret_cast<v4u*>(s.v + kl * dim + 4 * part) = kv_pre[kNK + j];
+            }
+        }
+
+        // ---- attention of this block's item
+        if (has_item) {
+            // q of the group's heads, and the new key's k (lanes < dim) or v
+            // (the q|k|v buffer is padded so a lane's quads stay inside it)
+            float got[kNQ - 1], kv_got;
+            const int q_base = item_g * group * dim;
+            const int kv_word = a < dim ? qw + item_g * dim + a : qw + kvw + item_g * dim + (a - dim);
+            const bool has_kv = new_key && a < 2 * dim;
+            const bool ok_q = await_quads(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
+            const bool ok_kv = ok_q && await_one(P.x_qkv + kv_word, has_kv, epoch(L, 1), kv_got, P);
+            if (!a_agree(ok_kv, s, round)) return false;
+            stamp(P.trace, b, 64 * L + 3);
+            store_quads(s.q, got, a);
+            if (has_kv) {
+                const int nl = pos - k0;
+                if (a < dim) s.k[nl * kKStride + a] = kv_got;
+                else s.v[nl * dim + (a - dim)] = kv_got;
+            }
+            if (!a_sync(s, round)) return false;
+            stamp(P.trace, b, 64 * L + 56);
+            // wave aw scores heads aw, aw + 2, ...; lane = key
+            float m[kHeadsA], l[kHeadsA];
+#pragma unroll
+            for (int h = 0; h < kHeadsA; ++h) {
+                const int gh = aw + kA * h;
+                m[h] = -INFINITY;
+                l[h] = 0.0f;
+                if (gh < group) {
+                    float sc = -INFINITY;
+                    if (lane < keys) {
+                        const float* qr = s.q + gh * dim;
+                        const float* kr = s.k + lane * kKStride;
+                        float sum = 0.0f;
+#pragma unroll 8
+                        for (int d = 0; d < dim; ++d) sum = sum + qr[d] * kr[d];
+                        sc = sum * P.attention_scale * P.attention_scale;
+                    }
+                    m[h] = wave_max_f32(sc);
+                    const float e = lane < keys ? expf(sc - m[h]) : 0.0f;
+                    l[h] = wave_sum_f32(e);
+                    s.e[gh * kStepSpanKeys + lane] = e;
+                }
+            }
+            lds_done();
+#pragma unroll
+            for (int h = 0; h < kHeadsA; ++h) {
+                const int gh = aw + kA * h;
+                if (gh < group) {
+                    const float* er = s.e + gh * kStepSpanKeys;
+                    float o = 0.0f;
+#pragma unroll 8
+                    for (int kk = 0; kk < keys; ++kk) o = fmaf(er[kk], s.v[kk * dim + lane], o);
+                    u64* part = P.x_part + ((size_t)(item_g * spans + item_s) * group + gh) * (dim + 2);
+                    publish(part + 2 + lane, epoch(L, 2), o);
+                    if (lane == 0) {
+                        publish(part, epoch(L, 2), m[h]);
+                        publish(part + 1, epoch(L, 2), l[h]);
+                    }
+                }
+            }
+            stamp(P.trace, b, 64 * L + 57);
+            if (a == 0) {
+                LEAF_GLOBAL unsigned* counter = (LEAF_GLOBAL unsigned*)(P.counters + item_g);
+                const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int last = done + 1 == (unsigned)spans;
+                if (last) {
+                    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __builtin_amdgcn_s_waitcnt(0);
+                }
+                lds_store(&s.last, last);
+            }
+            if (!a_sync(s, round)) return false;
+            stamp(P.trace, b, 64 * L + 58);
+            if (lds_load(&s.last)) {
+                bool ok = true;
+                const size_t stride = (size_t)group * (dim + 2);
+#pragma unroll
+                for (int h = 0; h < kHeadsA; ++h) {
+                    const int gh = aw + kA * h;
+                    if (gh < group && ok) {
+                        const u64* base = P.x_part + ((size_t)item_g * spans * group + gh) * (dim + 2);
+                        float ml[2];
+                        auto ml_index = [&](int i) { return lane < spans ? (int)(lane * stride) + i : -1; };
+                        ok = await(base, ml_index, epoch(L, 2), ml, P);
+                        const float ms = lane < spans ? ml[0] : -INFINITY;
+                        const float mx = wave_max_f32(ms);
+                        const float weight = lane < spans ? expf(ms - mx) : 0.0f;
+                        const float total = wave_sum_f32(lane < spans ? ml[1] * weight : 0.0f);
+                        float acc = 0.0f;
+                        for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
+                            float os[kMergeBatch];
+                            auto o_index = [&](int j) {
+                                return s0 + j < spans ? (int)((s0 + j) * stride + 2 + lane) : -1;
+                            };
+                            ok = await(base, o_index, epoch(L, 2), os, P);
+#pragma unroll
+                            for (int j = 0; j < kMergeBatch; ++j) {
+                                const float wj = __shfl(weight, (s0 + j) & 63, kWave);
+                                if (s0 + j < spans) acc = fmaf(os[j], wj, acc);
+                            }
+                        }
+                        if (ok)
+                            publish(P.x_attn + (item_g * group + gh) * dim + lane, epoch(L, 3),
+                                    total > 0.0f ? acc / total : 0.0f);
+                    }
+                }
+                if (!a_agree(ok, s, round)) return false;
+                stamp(P.trace, b, 64 * L + 60);
+            }
+        }
+        stamp(P.trace, b, 64 * L + 4);
+
+        // ---- attention output -> int8 for o_proj
+        {
+            float xa[kNH];
+            if (!a_agree(await_quads(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
+            stamp(P.trace, b, 64 * L + 5);
+            quantize_into(xa, qw, 1, a, s, round, parity);
+            post(s, 4 * L + 1, round);
+        }
+        // ---- after o_proj -> RMSNorm -> int8 for gate|up
+        fetch_gamma(gamma, Ly.post_gamma, H, a);
+        if (!a_agree(await_quads(P.x_mid, H, epoch(L, 4), x, a, P), s, round)) return false;
+        stamp(P.trace, b, 64 * L + 6);
+        store_quads(s.h_mid, x, a);
+        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
+        quantize_into(x, H, 0, a, s, round, parity);
+        post(s, 4 * L + 2, round);
+        // ---- SiLU-gated activation -> int8 for down_proj
+        {
+            float xd[kNF];
+            if (!a_agree(await_quads(P.x_act, F, epoch(L, 5), xd, a, P), s, round)) return false;
+            stamp(P.trace, b, 64 * L + 7);
+            quantize_into(xd, F, 1, a, s, round, parity);
+            post(s, 4 * L + 3, round);
+        }
+        // ---- the next layer's input (the last layer's feeds the head below)
+        if (L + 1 < P.layers) {
+            stamp(P.trace, b, 64 * (L + 1) + 0);
+            if (!a_agree(await_quads(P.x_hidden, H, epoch(L, 6), x, a, P), s, round)) return false;
+        }
+    }
+    // ---- final RMSNorm -> FP32 input of the head
+    {
+        float gamma[kNH];
+        fetch_gamma(gamma, P.final_gamma, H, a);
+        stamp(P.trace, b, 64 * P.layers + 0);
+        if (!a_agree(await_quads(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, round)) return false;
+        stamp(P.trace, b, 64 * P.layers + 1);
+        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
+        store_quads(s.xf, x, a);
+        post(s, 4 * P.layers, round);
+    }
+    return true;
+}
+
+// ========================================================= weight role ===
+struct LayerRows {
+    v4u q[kQP][2][kKCH];
+    v4u o[kOR][kKCH];
+    v4u g[kGP][2][kKCH];
+    v4u d[kOR][kKCF];
+    RowScale qs[kQP][2], os[kOR], gs[kGP][2], ds[kOR];
+};
+
+__device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
+    const int t = threadIdx.x, lane = t & 63;
+    const int bw = __builtin_amdgcn_readfirstlane((t >> 6) - kA);   // 0 .. kB - 1, wave-uniform
+    const int G = gridDim.x, b = blockIdx.x;
+    const int H = P.hidden, F = P.ffn, dim = kStepDim;
+    const int pos = P.position;
+    auto epoch = [&](int layer, int phase) { return P.epoch + (unsigned)(layer * 8 + phase); };
+    const Ownership own(P, b, G);
+
+    int qr[kQP][2];
+    bool has_q[kQP], has_r[kOR], has_g[kGP];
+    float rope_c[kQP], rope_s[kQP];
+#pragma unroll
+    for (int k = 0; k < kQP; ++k) {
+        const int p = own.q_first + bw + kB * k;
+        has_q[k] = p < own.q_end;
+        qr[k][0] = qr[k][1] = 0;
+        rope_c[k] = 1.0f;
+        rope_s[k] = 0.0f;
+        if (has_q[k]) {
+            rope_rows(p, P.heads, P.kv_heads, P.rotary, qr[k][0], qr[k][1]);
+            const int half = P.rotary / 2, i0 = qr[k][0] % dim;
+            if (qr[k][0] / dim < P.heads + P.kv_heads && i0 < half) {
+                rope_c[k] = ldg(P.cosines + (size_t)pos * half + i0);
+                rope_s[k] = ldg(P.sines + (size_t)pos * half + i0);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kOR; ++k) has_r[k] = own.r_first + bw + kB * k < own.r_end;
+#pragma unroll
+    for (int k = 0; k < kGP; ++k) has_g[k] = own.g_first + bw + kB * k < own.g_end;
+
+    LayerRows w;
+    // Loads of one phase's rows; `more` false loads nothing useful (the last
+    // layer has no successor) but keeps the load count of every path equal.
+    auto load_qkv = [&](const StepLayer& Ly, bool more) {
+#pragma unroll
+        for (int k = 0; k < kQP; ++k)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                load_row(w.q[k][r], Ly.qkv, qr[k][r], lane, has_q[k] && more);
+                w.qs[k][r].fetch(Ly.qkv, qr[k][r], has_q[k] && more);
+            }
+    };
+    auto load_o = [&](const StepLayer& Ly, bool more) {
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) {
+            const int row = own.r_first + bw + kB * k;
+            load_row(w.o[k], Ly.o, row, lane, has_r[k] && more);
+            w.os[k].fetch(Ly.o, row, has_r[k] && more);
+        }
+    };
+    auto load_gate_up = [&](const StepLayer& Ly, bool more) {
+#pragma unroll
+        for (int k = 0; k < kGP; ++k) {
+            const int p = own.g_first + bw + kB * k;
+            load_row(w.g[k][0], Ly.gate_up, p, lane, has_g[k] && more);
+            load_row(w.g[k][1], Ly.gate_up, F + p, lane, has_g[k] && more);
+            w.gs[k][0].fetch(Ly.gate_up, p, has_g[k] && more);
+            w.gs[k][1].fetch(Ly.gate_up, F + p, has_g[k] && more);
+        }
+    };
+    auto load_down = [&](const StepLayer& Ly, bool more) {
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) {
+            const int row = own.r_first + bw + kB * k;
+            load_row(w.d[k], Ly.down, row, lane, has_r[k] && more);
+            w.ds[k].fetch(Ly.down, row, has_r[k] && more);
+        }
+    };
+    load_qkv(layer_at(s, 0), true);
+    load_o(layer_at(s, 0), true);
+    load_gate_up(layer_at(s, 0), true);
+    load_down(layer_at(s, 0), true);
+
+    for (int L = 0; L < P.layers; ++L) {
+        float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
+        float* Vc = Kc + (size_t)P.kv_heads * P.capacity * dim;
+        const bool more = L + 1 < P.layers;
+        const StepLayer& next = layer_at(s, more ? L + 1 : L);
+        // ---- q|k|v, RoPE, KV append
+        if (!wait_ready(s, 4 * L + 0)) return false;
+        stamp(P.trace, b, 64 * L + 8 + 8 * bw, kAT + kWave * bw);
+        {
+            const float sx = s.sx[0];
+#pragma unroll
+            for (int k = 0; k < kQP; ++k)
+                if (has_q[k]) {
+                    const int a0 = row_dot(w.q[k][0], s.xq[0], H / 16, lane);
+                    const int a1 = row_dot(w.q[k][1], s.xq[0], H / 16, lane);
+                    if (lane == 0) {
+                        const int r0 = qr[k][0], r1 = qr[k][1];
+                        float v0 = dequant(a0, sx, w.qs[k][0].scale, w.qs[k][0].bias);
+                        float v1 = dequant(a1, sx, w.qs[k][1].scale, w.qs[k][1].bias);
+                        const int hb = r0 / dim, i0 = r0 % dim, i1 = r1 % dim, half = P.rotary / 2;
+                        if (hb < P.heads + P.kv_heads && i0 < half) {
+                            const float c = rope_c[k], sn = rope_s[k];
+                            const float x0 = v0 * c - v1 * sn;
+                            const float x1 = v1 * c + v0 * sn;
+                            v0 = x0;
+                            v1 = x1;
+                        }
+                        publish(P.x_qkv + r0, epoch(L, 1), v0);
+                        publish(P.x_qkv + r1, epoch(L, 1), v1);
+                        if (hb >= P.heads) {
+                            float* dst = hb < P.heads + P.kv_heads
+                                             ? Kc + ((size_t)(hb - P.heads) * P.capacity + pos) * dim
+                                             : Vc + ((size_t)(hb - P.heads - P.kv_heads) * P.capacity + pos) * dim;
+                            stg(dst + i0, v0);
+                            stg(dst + i1, v1);
+                        }
+                    }
+                }
+        }
+        stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
+        load_qkv(next, more);
+        // ---- o_proj + residual
+        if (!wait_ready(s, 4 * L + 1)) return false;
+        stamp(P.trace, b, 64 * L + 10 + 8 * bw, kAT + kWave * bw);
+        {
+            const float sx = s.sx[1];
+#pragma unroll
+            for (int k = 0; k < kOR; ++k)
+                if (has_r[k]) {
+                    const int row = own.r_first + bw + kB * k;
+                    const int acc = row_dot(w.o[k], s.xq[1], P.heads * dim / 16, lane);
+                    if (lane == 0)
+                        publish(P.x_mid + row, epoch(L, 4),
+                                s.h_in[row] + dequant(acc, sx, w.os[k].scale, w.os[k].bias));
+                }
+        }
+        stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
+        load_o(next, more);
+        // ---- gate|up + SiLU gate
+        if (!wait_ready(s, 4 * L + 2)) return false;
+        stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
+        {
+            const float sx = s.sx[0];
+#pragma unroll
+            for (int k = 0; k < kGP; ++k)
+                if (has_g[k]) {
+                    const int p = own.g_first + bw + kB * k;
+                    const int ag = row_dot(w.g[k][0], s.xq[0], H / 16, lane);
+                    const int au = row_dot(w.g[k][1], s.xq[0], H / 16, lane);
+                    if (lane == 0) {
+                        const float gate = dequant(ag, sx, w.gs[k][0].scale, w.gs[k][0].bias);
+                        const float up = dequant(au, sx, w.gs[k][1].scale, w.gs[k][1].bias);
+                        publish(P.x_act + p, epoch(L, 5), up * activate(P.activation, gate));
+                    }
+                }
+        }
+        stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
+        load_gate_up(next, more);
+        // ---- down_proj + residual
+        if (!wait_ready(s, 4 * L + 3)) return false;
+        stamp(P.trace, b, 64 * L + 14 + 8 * bw, kAT + kWave * bw);
+        {
+            const float sx = s.sx[1];
+#pragma unroll
+            for (int k = 0; k < kOR; ++k)
+                if (has_r[k]) {
+                    const int row = own.r_first + bw + kB * k;
+                    const int acc = row_dot(w.d[k], s.xq[1], F / 16, lane);
+                    if (lane == 0)
+                        publish(P.x_hidden + row, epoch(L, 6),
+                                s.h_mid[row] + dequant(acc, sx, w.ds[k].scale, w.ds[k].bias));
+                }
+        }
+        stamp(P.trace, b, 64 * L + 15 + 8 * bw, kAT + kWave * bw);
+        load_down(next, more);
+    }
+    return wait_ready(s, 4 * P.layers);
+}
+
+__global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
+    __shared__ Shared s;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int G = gridDim.x, b = blockIdx.x;
+    const int H = P.hidden;
+    if (t == 0) {
+        s.ready = -1;
+        s.a_count = 0;
+        s.abort = 0;
+        s.last = 0;
+    }
+    {
+        const int words = P.layers * (int)(sizeof(StepLayer) / 16);
+        const v4u* src = reinterpret_cast<const v4u*>(P.layer);
+        v4u* dst = reinterpret_cast<v4u*>(s.layer_bytes);
+        for (int i = t; i < words; i += kT) dst[i] = ldg(src + i);
+    }
+    __syncthreads();
+    const bool ok = wave < kA ? exchange_role(P, s) : weight_role(P, s);
+    if (!ok) return;                            // both roles leave together (abort flag in LDS)
+    __syncthreads();
+
+    // ---------------- FP32 LM head and greedy argmax (all waves)
+    const int V = P.vocab;
+    const int v_first = (int)((long long)b * V / G), v_end = (int)((long long)(b + 1) * V / G);
+    const int chunks = H / 4;                                  // float4 per row
+    float best = -INFINITY;
+    int best_i = V;
+    const float* head = static_cast<const float*>(P.head.data);
+    constexpr int kPerLane = kStepMaxHidden / 4 / kWave;       // float4 per lane of a row
+    for (int r = v_first + wave; r < v_end; r += 2 * kWaves) {
+        const int r2 = r + kWaves;
+        const bool two = r2 < v_end;
+        v4f wa[kPerLane], wb[kPerLane];
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int c = min(lane + kWave * j, chunks - 1);
+            wa[j] = __builtin_nontemporal_load((const LEAF_GLOBAL v4f*)(head + (size_t)r * H) + c);
+            wb[j] = __builtin_nontemporal_load((const LEAF_GLOBAL v4f*)(head + (size_t)(two ? r2 : r) * H) + c);
+        }
+        float aa = 0.0f, ab = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int c = lane + kWave * j;
+            if (c < chunks) {
+                const v4f xv = *reinterpret_cast<const v4f*>(s.xf + 4 * c);
+                aa = fmaf(wa[j].x, xv.x, aa); aa = fmaf(wa[j].y, xv.y, aa);
+                aa = fmaf(wa[j].z, xv.z, aa); aa = fmaf(wa[j].w, xv.w, aa);
+                ab = fmaf(wb[j].x, xv.x, ab); ab = fmaf(wb[j].y, xv.y, ab);
+                ab = fmaf(wb[j].z, xv.z, ab); ab = fmaf(wb[j].w, xv.w, ab);
+            }
+        }
+        aa = wave_sum_f32(aa);
+        const float la = aa + ldg(P.head.bias + r);
+        if (lane == 0) stg(P.logits + r, la);
+        if (better(la, r, best, best_i)) { best = la; best_i = r; }
+        if (two) {
+            ab = wave_sum_f32(ab);
+            const float lb = ab + ldg(P.head.bias + r2);
+            if (lane == 0) stg(P.logits + r2, lb);
+            if (better(lb, r2, best, best_i)) { best = lb; best_i = r2; }
+        }
+    }
+    if (lane == 0) {
+        s.best_v[wave] = best;
+        s.best_i[wave] = best_i;
+    }
+    __syncthreads();
+    stamp(P.trace, b, 64 * P.layers + 2);
+    const unsigned final_epoch = P.epoch + (unsigned)(P.layers * 8 + 1);
+    if (t == 0) {
+        float bv = s.best_v[0];
+        int bi = s.best_i[0];
+        for (int w = 1; w < kWaves; ++w)
+            if (better(s.best_v[w], s.best_i[w], bv, bi)) { bv = s.best_v[w]; bi = s.best_i[w]; }
+        publish(P.x_best + 2 * b, final_epoch, bv);
+        publish(P.x_best + 2 * b + 1, final_epoch, __int_as_float(bi));
+    }
+    if (b != 0) return;
+    // Block 0: the first maximal logit over all blocks (std::max_element).
+    float cand[2];
+    {
+        auto best_index = [&](int i) { return t < G ? 2 * t + i : -1; };
+        const bool done = await(P.x_best, best_index, final_epoch, cand, P);
+        if (!__syncthreads_and(done)) return;
+    }
+    float bv = t < G ? cand[0] : -INFINITY;
+    int bi = t < G ? __float_as_int(cand[1]) : V;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, kWave);
+        const int oi = __shfl_xor(bi, o, kWave);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) {
+        s.best_v[wave] = bv;
+        s.best_i[wave] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < kWaves; ++w)
+            if (better(s.best_v[w], s.best_i[w], bv, bi)) { bv = s.best_v[w]; bi = s.best_i[w]; }
+        stg(P.token, (uint32_t)bi);
+        if (P.host_token) *P.host_token = (uint32_t)bi;
+        stamp(P.trace, b, 64 * P.layers + 3);
+    }
+}
+
+}  // namespace
+
+int decode_step_spans(int keys) { return (keys + kStepSpanKeys - 1) / kStepSpanKeys; }
+
+int decode_step_blocks(int device) {
+    int cus = 0, resident = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, reinterpret_cast<const void*>(decode_step_kernel), kT,
+                                                     0) != hipSuccess)
+        return 0;
+    return resident >= 1 ? cus : 0;
+}
+
+bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int vocab, int blocks) {
+    if (dim != kStepDim || kv_heads <= 0 || heads % kv_heads || heads / kv_heads > kStepMaxGroup) return false;
+    if (hidden <= 0 || hidden > kStepMaxHidden || hidden % 16 || heads * dim != hidden) return false;
+    if (ffn <= 0 || ffn > kStepMaxFfn || ffn % 16 || vocab <= 0 || blocks <= 0 || blocks > kT) return false;
+    const int pairs = (heads + 2 * kv_heads) * dim / 2;
+    // rows per weight wave: kQP q|k|v pairs, kOR o/down rows, kGP gate|up pairs
+    return (pairs + blocks - 1) / blocks <= kQP * kB && (hidden + blocks - 1) / blocks <= kOR * kB &&
+           (ffn + blocks - 1) / blocks <= kGP * kB;
+}
+
+hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream) {
+    StepParams p = params;
+    void* args[] = {&p};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(blocks), dim3(kT), args,
+                                      0, stream);
+}
+
+}  // namespace leafhip

@@ -5,10 +5,13 @@
 // rejected here too, before anything reaches the device.
 #include "runtime.h"
 
+#include <mutex>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <mutex>
 
 namespace leafhip {
 
@@ -28,6 +31,48 @@ void DeviceBuffer::allocate(size_t n) {
 
 void DeviceBuffer::release() {
     if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+namespace {
+struct UncachedBlock {
+    int device;
+    void* ptr;
+    size_t bytes;
+};
+std::mutex uncached_mutex;
+std::vector<UncachedBlock> uncached_free;   // released blocks, kept for reuse
+}  // namespace
+
+void UncachedBuffer::allocate(size_t n) {
+    release();
+    if (n == 0) return;
+    n = (n + 65535) / 65536 * 65536;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> lock(uncached_mutex);
+        size_t best = uncached_free.size();
+        for (size_t i = 0; i < uncached_free.size(); ++i) {
+            const UncachedBlock& f = uncached_free[i];
+            if (f.device == device && f.bytes >= n && (best == uncached_free.size() || f.bytes < uncached_free[best].bytes))
+                best = i;
+        }
+        if (best < uncached_free.size()) {
+            ptr = uncached_free[best].ptr;
+            bytes = uncached_free[best].bytes;
+            uncached_free.erase(uncached_free.begin() + best);
+            return;
+        }
+    }
+    hip_check(hipExtMallocWithFlags(&ptr, n, hipDeviceMallocUncached), "hipExtMallocWithFlags(uncached)");
+    bytes = n;
+}
+
+void UncachedBuffer::release() {
+    if (!ptr) return;
+    std::lock_guard<std::mutex> lock(uncached_mutex);
+    uncached_free.push_back({device, ptr, bytes});
     ptr = nullptr;
     bytes = 0;
 }

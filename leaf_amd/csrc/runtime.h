@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "../../include/leafhip.h"
+#include "decode_step.h"
 #include "kernels.h"
 
 namespace leafhip {
@@ -38,6 +39,24 @@ struct DeviceBuffer {
     ~DeviceBuffer() { release(); }
     void allocate(size_t n);
     void release();
+    template <typename T> T* as() const { return static_cast<T*>(ptr); }
+};
+
+// Device memory that bypasses the L2 caches (hipDeviceMallocUncached), for
+// words that blocks on different XCDs exchange within one kernel: a cached
+// poll can keep reading a stale L2 line long after another XCD stored the
+// word.  Allocations are pooled per device and never returned to HIP, since
+// memory of this kind must stay allocated once a kernel has read it.
+struct UncachedBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int device = -1;
+    UncachedBuffer() = default;
+    UncachedBuffer(const UncachedBuffer&) = delete;
+    UncachedBuffer& operator=(const UncachedBuffer&) = delete;
+    ~UncachedBuffer() { release(); }
+    void allocate(size_t n);   // on the current device, from the pool when it can
+    void release();            // back to the pool
     template <typename T> T* as() const { return static_cast<T*>(ptr); }
 };
 
@@ -114,7 +133,7 @@ public:
 // Per-kernel-class device timing (HIP events on the session stream).
 class Profiler {
 public:
-    enum Kind { GemvW8A8, GemvFp, GemmW8A8, GemmFp, Attention, Other, Count };
+    enum Kind { GemvW8A8, GemvFp, GemmW8A8, GemmFp, Attention, Other, DecodeStep, Count };
     static const char* name(int kind);
     bool enabled = false;
     void begin(hipStream_t stream);
@@ -138,6 +157,7 @@ public:
     void reset() {
         length = 0;
         device_position_valid_ = false;
+        step_token_valid_ = false;
     }
     size_t cache_tokens() const { return length; }
     // Decoder::forward_into (decoder.cpp:1282-1444)
@@ -156,6 +176,22 @@ private:
     void launch(int M, size_t position, bool all_logits, const int* position_ptr, int spans);
     bool graph_decode_ok() const;
     void decode_graphed(uint32_t id, bool upload_id, float* host_logits, uint32_t* argmax);
+    // Persistent single-token step (decode_step.hip) for W8A8 decoders it fits.
+    void step_prepare();
+    bool step_usable() const;
+    void decode_step(uint32_t id, float* host_logits, uint32_t* argmax);
+    int step_blocks_ = 0;
+    bool step_enabled_ = true;
+    bool step_token_valid_ = false;   // ids_[0] holds the previous step's argmax
+    uint32_t step_token_ = 0;
+    unsigned step_launch_ = 0;
+    double step_bytes_ = 0;          // algorithmic bytes of one step, without KV
+    double step_kv_bytes_ = 0;       // KV bytes per visible key
+    StepParams step_;
+    DeviceBuffer step_layers_, step_trace_;
+    UncachedBuffer step_exchange_;
+    std::string step_trace_path_;
+    unsigned* step_host_abort_ = nullptr;
     void drop_graphs();
     std::map<int, hipGraphExec_t> graphs_;
     bool graphs_enabled_ = true;

@@ -2,6 +2,7 @@
 // and the forward pass of Decoder::Impl::forward_into (decoder.cpp:1282-1444).
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <cstdlib>
 #include <limits>
@@ -19,7 +20,8 @@ void grow(DeviceBuffer& b, size_t count) {
 }  // namespace
 
 const char* Profiler::name(int kind) {
-    static const char* names[] = {"gemv_w8a8", "gemv_fp", "gemm_w8a8", "gemm_fp", "attention", "other"};
+    static const char* names[] = {"gemv_w8a8", "gemv_fp", "gemm_w8a8", "gemm_fp", "attention", "other",
+                                  "decode_step"};
     return names[kind];
 }
 
@@ -97,10 +99,14 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m
     const char* graphs = std::getenv("LEAF_DECODE_GRAPH");
     graphs_enabled_ = !(graphs && std::string(graphs) == "0");
     plan(max_prefill ? max_prefill : 512, false);
+    const char* step = std::getenv("LEAF_DECODE_STEP");
+    step_enabled_ = !(step && std::string(step) == "0");
+    if (step_enabled_) step_prepare();
 }
 
 Session::~Session() {
     drop_graphs();
+    if (step_host_abort_) (void)hipHostFree(step_host_abort_);
     if (host_ids_) (void)hipHostFree(host_ids_);
     if (host_argmax_) (void)hipHostFree(host_argmax_);
     if (host_position_) (void)hipHostFree(host_position_);
@@ -205,6 +211,11 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
     validate(ids, count, all_logits, host_logits, host_capacity);
     plan(uint32_t(count), all_logits);
     hipStream_t s = stream();
+    if (count == 1 && !all_logits && step_usable()) {
+        decode_step(ids[0], host_logits, argmax);
+        return;
+    }
+    step_token_valid_ = false;
     if (count == 1 && !all_logits && graph_decode_ok()) {
         decode_graphed(ids[0], true, host_logits, argmax);
         return;
@@ -282,6 +293,172 @@ void Session::decode_graphed(uint32_t id, bool upload_id, float* host_logits, ui
     logits_device = logits_.as<float>();
     logits_count = c.vocab;
     length += 1;
+}
+
+// ---------------------------------------------------------------------------
+// Persistent decode step.  Used for single-token forwards of W8A8 decoders with
+// per-row int8 matrices, RMSNorm, RoPE, a SiLU/GELU/ReLU-gated MLP, head dim 64
+// and an FP32 head -- the TinyLlama shape -- when the geometry fits one block
+// per CU (decode_step_fits).  Everything else takes the graph-replayed path.
+void Session::step_prepare() {
+    const Model& m = model;
+    const Config& c = m.config;
+    if (m.activation_bits != 8 || m.accurate || c.norm_kind != 0 || !c.gated || c.position_kind != 0 || c.qk_norm ||
+        c.parallel || !c.final_norm || c.head_dim != kStepDim || c.rotary_dim > c.head_dim ||
+        c.layers > uint32_t(kStepMaxLayers))
+        return;
+    if (m.final_norm.beta || m.head.view.bits != 32 || m.head.input_scale) return;
+    if (!(m.embedding.bits == 32 || (m.embedding.bits == 8 && m.embedding.group == m.embedding.cols))) return;
+    auto per_row_int8 = [](const Linear& l) {
+        return l.present && l.view.bits == 8 && l.view.group == l.view.cols && !l.input_scale && l.view.bias;
+    };
+    for (const Layer& L : m.layers) {
+        if (!L.stacked_qkv || !L.stacked_gate_up || !per_row_int8(L.qkv) || !per_row_int8(L.o) ||
+            !per_row_int8(L.gate_up) || !per_row_int8(L.down) || L.input_norm.beta || L.post_norm.beta)
+            return;
+    }
+    const int blocks = decode_step_blocks(m.context.device);
+    if (!decode_step_fits(int(c.hidden), int(c.intermediate), int(c.heads), int(c.kv_heads), int(c.head_dim),
+                          int(c.vocab), blocks))
+        return;
+    std::vector<StepLayer> layers(c.layers);
+    for (uint32_t i = 0; i < c.layers; ++i) {
+        const Layer& L = m.layers[i];
+        layers[i].qkv = L.qkv.view;
+        layers[i].o = L.o.view;
+        layers[i].gate_up = L.gate_up.view;
+        layers[i].down = L.down.view;
+        layers[i].input_gamma = L.input_norm.gamma;
+        layers[i].post_gamma = L.post_norm.gamma;
+    }
+    step_layers_.allocate(layers.size() * sizeof(StepLayer));
+    hip_check(hipMemcpy(step_layers_.ptr, layers.data(), step_layers_.bytes, hipMemcpyHostToDevice), "step upload");
+    // Exchange words, per-head counters and the abort flag, zeroed once.
+    const size_t group = c.heads / c.kv_heads;
+    const size_t qkv = size_t(c.qwidth()) + 2 * c.kvwidth();
+    const size_t part = size_t(c.kv_heads) * kStepMaxSpans * group * (c.head_dim + 2);
+    // The kernel polls each vector in fixed per-lane blocks, so every vector
+    // is padded to its largest width plus kStepPadWords.
+    const size_t hidden_words = size_t(kStepMaxHidden) + kStepPadWords;
+    const size_t qkv_words = qkv + kStepPadWords, ffn_words = size_t(kStepMaxFfn) + kStepPadWords;
+    const size_t words = 3 * hidden_words + qkv_words + ffn_words + part + 2 * size_t(blocks);
+    step_exchange_.allocate(words * 8 + (c.kv_heads + 1) * sizeof(unsigned));
+    hip_check(hipMemset(step_exchange_.ptr, 0, step_exchange_.bytes), "hipMemset");
+    auto* w = step_exchange_.as<unsigned long long>();
+    StepParams& p = step_;
+    p.x_hidden = w; w += hidden_words;
+    p.x_mid = w; w += hidden_words;
+    p.x_qkv = w; w += qkv_words;
+    p.x_attn = w; w += hidden_words;
+    p.x_act = w; w += ffn_words;
+    p.x_part = w; w += part;
+    p.x_best = w; w += 2 * size_t(blocks);
+    p.counters = reinterpret_cast<unsigned*>(w);
+    p.abort_flag = p.counters + c.kv_heads;
+    hip_check(hipHostMalloc((void**)&step_host_abort_, sizeof(unsigned), hipHostMallocMapped), "hipHostMalloc");
+    *step_host_abort_ = 0;
+    hip_check(hipHostGetDevicePointer((void**)&p.host_abort, step_host_abort_, 0), "hipHostGetDevicePointer");
+    p.layers = int(c.layers);
+    p.hidden = int(c.hidden);
+    p.ffn = int(c.intermediate);
+    p.heads = int(c.heads);
+    p.kv_heads = int(c.kv_heads);
+    p.rotary = int(c.rotary_dim);
+    p.vocab = int(c.vocab);
+    p.window = int(c.sliding_window);
+    p.capacity = int(capacity);
+    p.activation = int(c.activation);
+    p.epsilon = c.epsilon;
+    p.embedding_scale = c.embedding_scale;
+    p.attention_scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(c.head_dim)));
+    p.layer = static_cast<const StepLayer*>(step_layers_.ptr);
+    p.embedding = m.embedding;
+    p.head = m.head.view;
+    p.final_gamma = m.final_norm.gamma;
+    p.cosines = rope_cos_.as<float>();
+    p.sines = rope_sin_.as<float>();
+    p.kv = kv_.as<float>();
+    // Algorithmic bytes: int8 weights and f32 row scales of every layer, the
+    // FP32 head, plus K and V of every visible key (added per step).
+    double bytes = 0;
+    for (const Layer& L : m.layers)
+        for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
+            bytes += double(l->view.rows) * l->view.cols + 4.0 * l->view.rows;
+    bytes += 4.0 * double(m.head.view.rows) * m.head.view.cols;
+    step_bytes_ = bytes;
+    step_kv_bytes_ = 2.0 * 4.0 * c.layers * c.kv_heads * c.head_dim;
+    step_blocks_ = blocks;
+    // LEAF_DECODE_STEP_TRACE=<file>: append every step's phase timeline
+    // (blocks x kStepTracePoints u64 stamps of the 100 MHz device clock).
+    if (const char* trace = std::getenv("LEAF_DECODE_STEP_TRACE")) {
+        step_trace_path_ = trace;
+        step_trace_.allocate(size_t(blocks) * kStepTracePoints * 8);
+        hip_check(hipMemset(step_trace_.ptr, 0, step_trace_.bytes), "hipMemset");
+    }
+}
+
+bool Session::step_usable() const {
+    if (!step_blocks_ || !step_enabled_) return false;
+    const Config& c = model.config;
+    const size_t end = length + 1;
+    const size_t begin = (c.sliding_window && end > c.sliding_window) ? end - c.sliding_window : 0;
+    const int spans = decode_step_spans(int(end - begin));
+    return spans <= kStepMaxSpans && size_t(spans) * c.kv_heads <= size_t(step_blocks_);
+}
+
+void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
+    const Config& c = model.config;
+    hipStream_t s = stream();
+    if (!step_token_valid_ || step_token_ != id) {
+        *host_ids_ = id;
+        hip_check(hipMemcpyAsync(ids_.ptr, host_ids_, sizeof(uint32_t), hipMemcpyHostToDevice, s), "ids upload");
+    }
+    if (++step_launch_ >= (1u << 20)) {
+        // Epoch tags would repeat: start the exchange words from zero again.
+        hip_check(hipMemsetAsync(step_exchange_.ptr, 0, step_exchange_.bytes, s), "hipMemsetAsync");
+        step_launch_ = 1;
+    }
+    StepParams p = step_;
+    p.position = int(length);
+    p.epoch = step_launch_ << 12;
+    p.token = ids_.as<uint32_t>();
+    p.host_token = mapped_argmax_;
+    p.logits = logits_.as<float>();
+    p.trace = step_trace_.as<unsigned long long>();
+    *step_host_abort_ = 0;
+    const double bytes = step_bytes_ + step_kv_bytes_ * double(length + 1);
+    hipError_t launched = hipSuccess;
+    timed(Profiler::DecodeStep, bytes, 0, [&] { launched = launch_decode_step(p, step_blocks_, s); });
+    hip_check(launched, "decode step launch");
+    if (host_logits)
+        hip_check(hipMemcpyAsync(host_logits, logits_.ptr, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s),
+                  "logits copy");
+    hip_check(hipStreamSynchronize(s), "decode step");
+    if (profiler.enabled) profiler.collect();
+    if (*step_host_abort_) {
+        // A wait timed out: counters and exchange words may be mid-round.
+        // Start the next step from zeroed state.
+        *step_host_abort_ = 0;
+        hip_check(hipMemset(step_exchange_.ptr, 0, step_exchange_.bytes), "hipMemset");
+        step_token_valid_ = false;
+        check(false, "decode step timed out waiting for another block", LH_ERROR_DEVICE);
+    }
+    if (!step_trace_path_.empty()) {
+        std::vector<unsigned long long> stamps(step_trace_.bytes / 8);
+        hip_check(hipMemcpy(stamps.data(), step_trace_.ptr, step_trace_.bytes, hipMemcpyDeviceToHost), "trace copy");
+        if (FILE* f = std::fopen(step_trace_path_.c_str(), "ab")) {
+            std::fwrite(stamps.data(), 8, stamps.size(), f);
+            std::fclose(f);
+        }
+    }
+    const uint32_t next = *host_argmax_;
+    if (argmax) *argmax = next;
+    step_token_ = next;
+    step_token_valid_ = true;
+    logits_device = logits_.as<float>();
+    logits_count = c.vocab;
+    length += 1;
+    device_position_valid_ = false;
 }
 
 void Session::drop_graphs() {

@@ -47,6 +47,7 @@ class Oracle:
         self.lib = lib
         lib.oracle_quantize_rows.argtypes = [_f32p, _sz, _sz, _i8p, _f32p]
         lib.oracle_set_vnni_policy.argtypes = [C.c_int]
+        lib.oracle_set_norm_order.argtypes = [C.c_int]
         lib.oracle_int_accumulators.argtypes = [C.c_uint, _sz, _sz, _sz, C.c_void_p, _i8p, _sz, _i32p]
         for name in ("oracle_linear_int", "oracle_linear_fp"):
             getattr(lib, name).argtypes = [C.c_uint, _sz, _sz, _sz, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -75,6 +76,10 @@ class Oracle:
                                                 C.c_char_p, _sz]
 
     # -- kernels ------------------------------------------------------------
+    def set_norm_order(self, order: int) -> None:
+        """0: sequential square sums (the reference); 1: pairwise."""
+        self.lib.oracle_set_norm_order(order)
+
     def set_vnni_policy(self, policy: int) -> None:
         """0: fused grouped-W8A8 epilogue (default), 1: VNNI tile form, -1: this CPU's choice."""
         self.lib.oracle_set_vnni_policy(policy)

@@ -230,6 +230,27 @@ float accurate_dot(const Matrix& w, size_t row, const float* x) {
 }
 
 // ------------------------------------------------------------------ R9 -----
+// 0: the reference's sequential square sum; 1: pairwise (tree) sums, the order
+// a parallel reduction uses.  The second exists only to measure how far W8A8
+// logits move when nothing but the summation order changes.
+int g_norm_order = 0;
+
+float square_sum(const float* in, size_t width, float mean) {
+    float square = 0;
+    if (g_norm_order == 0) {
+        for (size_t c = 0; c < width; ++c) { const float v = in[c] - mean; square += v * v; }
+        return square;
+    }
+    std::vector<float> t(width);
+    for (size_t c = 0; c < width; ++c) { const float v = in[c] - mean; t[c] = v * v; }
+    for (size_t n = width; n > 1;) {
+        const size_t half = (n + 1) / 2;
+        for (size_t i = 0; i + half < n; ++i) t[i] = t[i] + t[i + half];
+        n = half;
+    }
+    return width ? t[0] : 0.0f;
+}
+
 void norm_rows(const float* x, size_t M, size_t width, const float* gamma, const float* beta,
                float epsilon, unsigned kind, bool accurate, float* y) {
     for (size_t r = 0; r < M; ++r) {
@@ -246,7 +267,7 @@ void norm_rows(const float* x, size_t M, size_t width, const float* gamma, const
             for (size_t c = 0; c < width; ++c) { const float s = in[c] * in[c]; total += s; }
             square = static_cast<float>(total);
         } else {
-            for (size_t c = 0; c < width; ++c) { const float v = in[c] - mean; square += v * v; }
+            square = square_sum(in, width, mean);
         }
         const float scale = 1.0f / std::sqrt(square / static_cast<float>(width) + epsilon);
         for (size_t c = 0; c < width; ++c) {
@@ -606,6 +627,7 @@ struct oracle_decoder {
 extern "C" {
 
 void oracle_set_vnni_policy(int policy) { g_vnni_policy = policy; }
+void oracle_set_norm_order(int order) { g_norm_order = order; }
 
 void oracle_quantize_rows(const float* x, size_t M, size_t K, int8_t* q, float* scales) {
     quantize_rows(x, M, K, q, scales);

@@ -20,6 +20,9 @@ extern "C" {
 // what the GPU computes), 1 = unfused (quant_vnni_tile), -1 = what this CPU's
 // reference build would pick.
 void oracle_set_vnni_policy(int policy);
+// RMSNorm / LayerNorm square sum: 0 = the reference's sequential order (default),
+// 1 = pairwise.  Only for measuring the order sensitivity of W8A8 logits.
+void oracle_set_norm_order(int order);
 // R2: per-token activation quantization, q in [-127,127] stored as int8.
 void oracle_quantize_rows(const float* x, size_t M, size_t K, int8_t* q, float* scales);
 // R3 integer part: acc[t][row][g] = exact sum_{col in group g} w[row,col] * q[t,col].

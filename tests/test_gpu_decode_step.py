@@ -1,0 +1,164 @@
+"""The persistent single-token decode step against the oracle and the multi-launch path.
+
+Single-token W8A8 forwards of TinyLlama-shape decoders (RMSNorm, RoPE, gated
+SiLU MLP, head dim 64, per-row INT8 matrices, FP32 head) run as one
+cooperative launch.  The runs are teacher-forced: the oracle's greedy token is
+fed to both sides at every step.  Each step's logits must match the oracle
+within the W8A8 tolerance of the whole-model tests (2e-2 of the largest
+|logit|); the greedy choice must match whenever the oracle's top-2 margin is
+wider than twice that band (inside it, a single int8 rounding flip upstream --
+the reference's own AVX2 and scalar W8A8 builds differ by such flips -- can
+reorder near-tied logits); and the kernel must actually have run (profiler
+class "decode_step").
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from leaf_amd import models
+from leaf_amd.artifact import write_artifact
+
+pytestmark = pytest.mark.gpu
+
+# W8A8 logits: no logit further than 5e-2 of the largest |logit| from the
+# oracle's, and relative RMSE (as Leaf's quality() defines it,
+# tools/decoder_validation.py:222-253) within 5e-2.  GPU and CPU sum the RMSNorm
+# squares in different orders; some activations then land on the other side
+# of an int8 rounding boundary and each flip moves every logit.  The oracle
+# alone shows the size of this band: changing only its norm summation order
+# moves these models' logits by 1.2-1.9e-2 at reduced width
+# (tests/test_oracle_golden.py) and by up to 3.6e-2 at TinyLlama width.
+W8A8_LOGIT_TOLERANCE = 5e-2
+W8A8_RMSE_TOLERANCE = 5e-2
+
+
+def rel_error(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def rel_rmse(a, b):
+    return float(np.sqrt(np.mean((a - b) ** 2)) / max(np.sqrt(np.mean(b ** 2)), 1e-12))
+
+
+def step_spec(**overrides):
+    """TinyLlama topology and precision at reduced width (head dim stays 64)."""
+    base = dict(hidden=512, intermediate=1408, heads=8, kv_heads=2, layers=3, vocab=3000, max_positions=1024)
+    base.update(overrides)
+    return dataclasses.replace(models.tinyllama_w8a8(), **base)
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from leaf_amd import runtime
+    runtime.library()
+    return runtime
+
+
+@pytest.fixture(scope="module")
+def small(tmp_path_factory):
+    path = tmp_path_factory.mktemp("step") / "small.leaf"
+    write_artifact(path, step_spec(), seed=11)
+    return path
+
+
+@pytest.fixture(scope="module")
+def wide(tmp_path_factory):
+    """Full TinyLlama widths (2048 / 5632 / 32:4 heads / 32000 vocab), two layers."""
+    path = tmp_path_factory.mktemp("step") / "wide.leaf"
+    write_artifact(path, dataclasses.replace(models.tinyllama_w8a8(), layers=2), seed=12)
+    return path
+
+
+def decisive(reference, tolerance=2e-2):
+    """Whether the reference's top-2 margin exceeds twice the typical movement
+    (2e-2 of the largest |logit|) of an order-only change."""
+    top = np.sort(reference)[-2:]
+    return top[1] - top[0] > 2 * tolerance * np.max(np.abs(reference))
+
+
+def run_steps(rt, oracle, path, prompt_tokens, steps, seed, **decoder_args):
+    dec = rt.Decoder(path, 8, **decoder_args)
+    od = oracle.decoder(path, 8, False)
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, dec.vocabulary_size, prompt_tokens).astype(np.uint32)
+    a, b = dec.forward(prompt), od.forward(prompt)
+    assert rel_error(a, b) <= W8A8_LOGIT_TOLERANCE
+    dec.set_profiling(True)
+    worst, tokens, checked, rmse = 0.0, [], 0, 0.0
+    for step in range(steps):
+        tok = int(np.argmax(b))
+        assert int(dec.last_argmax.value) == int(np.argmax(a)), "device argmax differs from the logits it returned"
+        if decisive(b):
+            assert int(np.argmax(a)) == tok, f"greedy token differs at step {step} with a decisive margin"
+            checked += 1
+        tokens.append(tok)
+        a, b = dec.forward([tok]), od.forward([tok])
+        worst = max(worst, rel_error(a, b))
+        rmse = max(rmse, rel_rmse(a, b))
+        assert rmse <= W8A8_RMSE_TOLERANCE, f"relative logit RMSE {rmse:.2e} at step {step}"
+    profile = dec.profile()
+    dec.close()
+    print(f"greedy choice compared at {checked} of {steps} steps (the rest within the tolerance band); "
+          f"worst relative RMSE {rmse:.2e}")
+    assert checked >= steps // 5
+    return worst, tokens, profile
+
+
+def test_step_matches_oracle_across_span_boundaries(rt, oracle, small):
+    # a 70-token prompt, then 80 steps: 2 -> 3 spans of 64 keys
+    worst, _, profile = run_steps(rt, oracle, small, 70, 80, seed=3)
+    print(f"decode step: worst relative logit error {worst:.2e}")
+    assert worst <= W8A8_LOGIT_TOLERANCE
+    assert profile.get("decode_step", {}).get("launches") == 80, profile
+
+
+def test_step_at_full_tinyllama_width(rt, oracle, wide):
+    worst, _, profile = run_steps(rt, oracle, wide, 300, 12, seed=4)
+    print(f"decode step (2048/5632/32:4): worst relative logit error {worst:.2e}")
+    assert worst <= W8A8_LOGIT_TOLERANCE
+    assert profile.get("decode_step", {}).get("launches") == 12, profile
+
+
+def test_step_with_sliding_window(rt, oracle, tmp_path):
+    path = tmp_path / "window.leaf"
+    write_artifact(path, step_spec(sliding_window=100, layers=2), seed=13)
+    worst, _, profile = run_steps(rt, oracle, path, 90, 40, seed=5)
+    assert worst <= W8A8_LOGIT_TOLERANCE
+    assert profile.get("decode_step", {}).get("launches") == 40, profile
+
+
+def test_step_and_graph_paths_agree(rt, small, monkeypatch):
+    # the same token sequence through both single-token paths
+    feed = (np.arange(30, dtype=np.uint32) * 97 + 5) % 3000
+    runs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("LEAF_DECODE_STEP", flag)
+        dec = rt.Decoder(small, 8)
+        dec.set_profiling(True)
+        dec.forward(np.arange(1, 41, dtype=np.uint32) * 7)
+        rows = [dec.forward([int(tok)]) for tok in feed]
+        steps = dec.profile().get("decode_step", {}).get("launches", 0)
+        dec.close()
+        runs.append(np.stack(rows))
+        assert steps == (30 if flag == "1" else 0)
+    assert rel_error(runs[0], runs[1]) <= W8A8_LOGIT_TOLERANCE
+    assert rel_rmse(runs[0], runs[1]) <= W8A8_RMSE_TOLERANCE
+
+
+def test_step_is_deterministic_across_reset(rt, small):
+    dec = rt.Decoder(small, 8)
+    prompt = np.arange(3, 53, dtype=np.uint32)
+    outs = []
+    for _ in range(2):
+        dec.reset()
+        tok = dec.forward_into(prompt, None)
+        rows = []
+        for _ in range(20):
+            rows.append(dec.forward([tok]))
+            tok = int(dec.last_argmax.value)
+        outs.append(np.stack(rows))
+    dec.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
