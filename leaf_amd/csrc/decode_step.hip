@@ -11,12 +11,13 @@
 //     (epoch << 32 | f32 bits), written and read with agent-scope relaxed
 //     atomics: a reader spins on the data itself until every word carries the
 //     epoch of the phase it waits for -- no fences, no barrier counters (one
-//     round trip, ~2 us, against ~8 us for fenced barriers, measured).  Every
+//     round trip against ~8 us for fenced barriers, measured).  The words live
+//     in uncached device memory and each wave reads them coalesced.  Every
 //     block normalizes and quantizes the whole input vector itself (the
 //     per-token absmax of the W8A8 quantization is global) and posts the int8
 //     vector in LDS.  These waves also run attention: (KV head, span of 64
-//     keys) items whose cached keys are fetched during the q|k|v phase, merged
-//     by the last span of each KV head to arrive (per-head counter).
+//     keys) items whose cached keys are fetched during the RMSNorm, and merge
+//     waves (one per query head, in the last blocks) that combine the spans.
 //   * 6 weight waves own whole rows of every matrix of a layer and keep them
 //     in registers.  After computing a phase they load the same phase of the
 //     next layer, so the weight stream runs a full layer ahead of the
@@ -74,7 +75,7 @@ constexpr int kOR = 2;                                       // o / down rows pe
 constexpr int kGP = 4;                                       // gate|up pairs per weight wave
 constexpr int kHeadsA = (kStepMaxGroup + kA - 1) / kA;       // query heads per exchange wave
 constexpr int kKStride = kStepDim + 4;                       // padded K row in LDS
-constexpr int kMergeBatch = 8;                               // span partials polled together
+constexpr int kMergeBatch = 16;                              // span partials polled together
 constexpr unsigned kSpinLimit = 1u << 20;                    // about a second of polling
 
 static_assert(sizeof(StepLayer) % 16 == 0, "layer descriptors are copied as 16-byte words");
@@ -98,8 +99,60 @@ struct __align__(16) Shared {
     int ready;                      // last phase whose input the exchange waves posted
     int a_count;                    // exchange-wave barrier arrivals
     int abort;
-    int last;                       // this block merges the attention spans of its KV head
 };
+
+// Wave reductions on DPP lane moves instead of LDS-crossbar shuffles: xor 1
+// and xor 2 (quad permutes), then the half-row and row mirrors (once lanes of
+// a quad, then of a half-row, agree, these pair each lane with the other
+// half), then the four row totals read out and combined in a fixed order, so
+// every lane gets the same bits.
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+template <int Ctrl>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xF, 0xF, false);
+}
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(dpp<Ctrl>(__float_as_int(v)));
+}
+__device__ __forceinline__ float rows_f32(float v, int row) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * row));
+}
+__device__ __forceinline__ float dpp_sum_f32(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return (rows_f32(v, 0) + rows_f32(v, 1)) + (rows_f32(v, 2) + rows_f32(v, 3));
+}
+__device__ __forceinline__ float dpp_max_f32(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    return fmaxf(fmaxf(rows_f32(v, 0), rows_f32(v, 1)), fmaxf(rows_f32(v, 2), rows_f32(v, 3)));
+}
+__device__ __forceinline__ int dpp_sum_i32(int v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
+// Makes every LDS read of a step complete before any of its arithmetic: the
+// register-pressure-driven scheduler otherwise interleaves each read with its
+// use, paying one LDS round trip per read instead of one per step.
+__device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[8]) {
+    asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]));
+}
+__device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[4]) {
+    asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+}
 
 __device__ __forceinline__ const StepLayer& layer_at(const Shared& s, int L) {
     return reinterpret_cast<const StepLayer*>(s.layer_bytes)[L];
@@ -201,19 +254,25 @@ __device__ __forceinline__ bool spin_until(const u64* p, unsigned epoch, unsigne
 }
 
 // This lane's quads of the n-element vector src once they all carry
-// `epoch`; elements past n read as 0 and are not waited for.  A lane first
+// `epoch`.  Quads past n are not waited for and hold whatever the buffer
+// holds there (callers mask them out or never read them).  A lane first
 // watches one word it needs, then reads all of them; a word still missing is
 // watched alone before the next full read (a full re-read per spin from every
 // lane of every block would crowd the memory pipeline the weight waves use).
-template <int N>
-__device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoch, float (&out)[N], int a,
+// G0 > 0 takes the lane's quads G0 .. G0 + N/4 - 1 only (a long vector in
+// parts, so fewer 64-bit words are held at once); Watch false skips the first
+// watched word (a part read after another part's watch saw the vector land).
+template <int N, int G0 = 0, bool Watch = true>
+__device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoch, float* out, int a,
                                             const StepParams& P) {
     static_assert(N % 4 == 0, "groups of four words");
     constexpr int G = N / 4;
-    const int live = n / 4 - a;   // quad g of this lane is inside the vector when g * kAT < live
+    src += 4 * kAT * G0;
+    const int live = n / 4 - a - kAT * G0;   // quad g (from G0) is inside the vector when g * kAT < live
     const u64* mine = src + 4 * a;
     unsigned spin = 0;
-    if (live > 0 && !spin_until(mine + 4 * kAT * min(G - 1, (live - 1) / kAT) + 3, epoch, spin, P)) return false;
+    if (Watch && live > 0 && !spin_until(mine + 4 * kAT * min(G - 1, (live - 1) / kAT) + 3, epoch, spin, P))
+        return false;
     const __amdgpu_buffer_rsrc_t view = exchange_view(src);
     u64 w[N];
     for (;;) {
@@ -231,7 +290,7 @@ __device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoc
         if (!spin_until(mine + 4 * kAT * (missing >> 2) + (missing & 3), epoch, spin, P)) return false;
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = (i / 4) * kAT < live ? __uint_as_float(unsigned(w[i])) : 0.0f;
+    for (int i = 0; i < N; ++i) out[i] = __uint_as_float(unsigned(w[i]));
     return true;
 }
 
@@ -269,7 +328,7 @@ __device__ __forceinline__ bool a_agree(bool ok, Shared& s, int& round) {
 
 // Sums (or maxes) over the exchange lanes; every exchange wave gets the same bits.
 __device__ __forceinline__ float a_sum(float v, Shared& s, int& round, int& parity) {
-    v = wave_sum_f32(v);
+    v = dpp_sum_f32(v);
     if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
     a_sync(s, round);
     float r = s.red[kA * parity];
@@ -279,7 +338,7 @@ __device__ __forceinline__ float a_sum(float v, Shared& s, int& round, int& pari
     return r;
 }
 __device__ __forceinline__ float a_max(float v, Shared& s, int& round, int& parity) {
-    v = wave_max_f32(v);
+    v = dpp_max_f32(v);
     if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
     a_sync(s, round);
     float r = s.red[kA * parity];
@@ -389,7 +448,7 @@ __device__ __forceinline__ int row_dot(const v4u (&w)[KC], const int8_t* xq, int
         a = dot4((int)w[j].w, (int)x.w, a);
         acc += c < chunks ? a : 0;
     }
-    return wave_sum_i32(acc);
+    return dpp_sum_i32(acc);
 }
 
 // ((float)acc * s_x) * s_w + b  (decoder.cpp:568, 1229), separate roundings.
@@ -476,6 +535,83 @@ struct Ownership {
     }
 };
 
+// Attention over this block's span of keys (K rows in s.k, V rows in s.v,
+// q of the group's heads in s.q) for the wave's query heads aw, aw + kA, ...
+// (HPW of them; heads past the group repeat the last one, branch-free, so all
+// heads' LDS reads overlap).  Publishes per head: max score, sum of
+// exp(score - max), and the unnormalized output sum_k exp(s_k - max) v_k.
+// Every staged row is finite: rows past the span hold key 0's values and get
+// weight 0.
+template <int HPW>
+__device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, int lane, int aw, int group, int keys,
+                                               u64* parts, unsigned epoch) {
+    constexpr int dim = kStepDim;
+    // scores: lane = key, four dims of its K row at a time
+    float sum[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) sum[h] = 0.0f;
+#pragma unroll 2
+    for (int d4 = 0; d4 < dim / 4; ++d4) {
+        const v4f kv = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
+        v4f qv[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+            qv[h] = *reinterpret_cast<const v4f*>(s.q + min(aw + kA * h, group - 1) * dim + 4 * d4);
+        all_loaded(kv, qv);
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum[h] = fmaf(qv[h][j], kv[j], sum[h]);
+    }
+    float m[HPW], l[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        const int gh = aw + kA * h;
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+        if (gh < group) {
+            const float sc = lane < keys ? sum[h] * P.attention_scale * P.attention_scale : -INFINITY;
+            m[h] = dpp_max_f32(sc);
+            const float e = lane < keys ? expf(sc - m[h]) : 0.0f;
+            l[h] = dpp_sum_f32(e);
+            s.e[gh * kStepSpanKeys + lane] = e;
+        }
+    }
+    lds_done();   // each wave reads back only its own heads' weights
+    // e . V: lane = dim, keys in order, V rows shared by the wave's heads
+    float o[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) o[h] = 0.0f;
+    const int keys4 = (keys + 3) & ~3;
+#pragma unroll 2
+    for (int kk = 0; kk < keys4; kk += 4) {
+        v4f v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = s.v[(kk + j) * dim + lane];
+        v4f e4[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+            e4[h] = *reinterpret_cast<const v4f*>(s.e + min(aw + kA * h, group - 1) * kStepSpanKeys + kk);
+        all_loaded(v, e4);
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[h] = fmaf(e4[h][j], v[j], o[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        const int gh = aw + kA * h;
+        if (gh < group) {
+            u64* part = parts + (size_t)gh * (dim + 2);
+            publish(part + 2 + lane, epoch, o[h]);
+            if (lane == 0) {
+                publish(part, epoch, m[h]);
+                publish(part + 1, epoch, l[h]);
+            }
+        }
+    }
+}
+
 // ======================================================= exchange role ===
 // Returns false when the kernel is abandoned (abort).
 __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
@@ -487,7 +623,6 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     const int pos = P.position;
     int round = 0, parity = 0;
     auto epoch = [&](int layer, int phase) { return P.epoch + (unsigned)(layer * 8 + phase); };
-    (void)G;
 
     // this block's attention item: (KV head, span of keys)
     const int end = pos + 1;
@@ -498,6 +633,8 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     const int k0 = begin + item_s * kStepSpanKeys, k1 = min(end, k0 + kStepSpanKeys);
     const int cached_end = min(k1, pos), keys = k1 - k0;
     const bool new_key = pos >= k0 && pos < k1;
+    // merge blocks: the last ceil(heads / kA) blocks, one query head per wave
+    const bool merge_block = (G - 1 - b) * kA < P.heads;
 
     float x[kNH];
     {
@@ -513,7 +650,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // arithmetic inside the loop instead of hoisting dozens of 64-bit
         // addresses into registers for the whole kernel.
         asm volatile("" : "+v"(a));
-        const int lane = a & 63, aw = a >> 6;
+        const int lane = a & 63, aw = __builtin_amdgcn_readfirstlane(a >> 6);   // aw: wave-uniform
         const StepLayer& Ly = layer_at(s, L);
         const float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
         const float* Vc = Kc + (size_t)P.kv_heads * P.capacity * dim;
@@ -549,7 +686,10 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
         }
 
-        // ---- attention of this block's item
+        // ---- attention, flash-decoding style: item blocks score one KV
+        // head's span of keys for all heads of its group and publish (max,
+        // sum, unnormalized output) per head; merge waves (one per query head,
+        // in the last blocks) combine the spans as soon as they land.
         if (has_item) {
             // q of the group's heads, and the new key's k (lanes < dim) or v
             // (the q|k|v buffer is padded so a lane's quads stay inside it)
@@ -557,7 +697,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             const int q_base = item_g * group * dim;
             const int kv_word = a < dim ? qw + item_g * dim + a : qw + kvw + item_g * dim + (a - dim);
             const bool has_kv = new_key && a < 2 * dim;
-            const bool ok_q = await_quads(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
+            const bool ok_q = await_quads<kNQ - 1>(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
             const bool ok_kv = ok_q && await_one(P.x_qkv + kv_word, has_kv, epoch(L, 1), kv_got, P);
             if (!a_agree(ok_kv, s, round)) return false;
             stamp(P.trace, b, 64 * L + 3);
@@ -569,109 +709,62 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
             if (!a_sync(s, round)) return false;
             stamp(P.trace, b, 64 * L + 56);
-            // wave aw scores heads aw, aw + 2, ...; lane = key
-            float m[kHeadsA], l[kHeadsA];
-#pragma unroll
-            for (int h = 0; h < kHeadsA; ++h) {
-                const int gh = aw + kA * h;
-                m[h] = -INFINITY;
-                l[h] = 0.0f;
-                if (gh < group) {
-                    float sc = -INFINITY;
-                    if (lane < keys) {
-                        const float* qr = s.q + gh * dim;
-                        const float* kr = s.k + lane * kKStride;
-                        float sum = 0.0f;
-#pragma unroll 8
-                        for (int d = 0; d < dim; ++d) sum = sum + qr[d] * kr[d];
-                        sc = sum * P.attention_scale * P.attention_scale;
-                    }
-                    m[h] = wave_max_f32(sc);
-                    const float e = lane < keys ? expf(sc - m[h]) : 0.0f;
-                    l[h] = wave_sum_f32(e);
-                    s.e[gh * kStepSpanKeys + lane] = e;
-                }
-            }
-            lds_done();
-#pragma unroll
-            for (int h = 0; h < kHeadsA; ++h) {
-                const int gh = aw + kA * h;
-                if (gh < group) {
-                    const float* er = s.e + gh * kStepSpanKeys;
-                    float o = 0.0f;
-#pragma unroll 8
-                    for (int kk = 0; kk < keys; ++kk) o = fmaf(er[kk], s.v[kk * dim + lane], o);
-                    u64* part = P.x_part + ((size_t)(item_g * spans + item_s) * group + gh) * (dim + 2);
-                    publish(part + 2 + lane, epoch(L, 2), o);
-                    if (lane == 0) {
-                        publish(part, epoch(L, 2), m[h]);
-                        publish(part + 1, epoch(L, 2), l[h]);
-                    }
-                }
-            }
+            if (P.trace && threadIdx.x == 0) stg(P.trace + (size_t)b * kStepTracePoints + 64 * L + 61, (unsigned long long)__builtin_amdgcn_s_memtime());
+            u64* parts = P.x_part + (size_t)(item_g * spans + item_s) * group * (dim + 2);
+            if (group <= 4 * kA) attention_item<4>(P, s, lane, aw, group, keys, parts, epoch(L, 2));
+            else attention_item<kHeadsA>(P, s, lane, aw, group, keys, parts, epoch(L, 2));
             stamp(P.trace, b, 64 * L + 57);
-            if (a == 0) {
-                LEAF_GLOBAL unsigned* counter = (LEAF_GLOBAL unsigned*)(P.counters + item_g);
-                const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const int last = done + 1 == (unsigned)spans;
-                if (last) {
-                    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __builtin_amdgcn_s_waitcnt(0);
-                }
-                lds_store(&s.last, last);
-            }
-            if (!a_sync(s, round)) return false;
-            stamp(P.trace, b, 64 * L + 58);
-            if (lds_load(&s.last)) {
-                bool ok = true;
+        }
+        if (merge_block) {
+            // this wave's query head mh: combine its spans (lane s holds span
+            // s's max and sum; lane d accumulates output element d)
+            bool ok = true;
+            const int mh = (G - 1 - b) * kA + aw;
+            if (mh < P.heads) {
+                const int g = mh / group, gh = mh % group;
                 const size_t stride = (size_t)group * (dim + 2);
+                const u64* base = P.x_part + ((size_t)g * spans * group + gh) * (dim + 2);
+                // wait for every span's (max, sum) pair (lane s: span s),
+                // then read the outputs kMergeBatch spans per round trip
+                float ml[2];
+                unsigned spin = 0;
+                if (lane < spans) ok = spin_until(base + lane * stride + 1, epoch(L, 2), spin, P);
+                auto ml_index = [&](int i) { return lane < spans ? (int)(lane * stride) + i : -1; };
+                ok = __all(ok) && await(base, ml_index, epoch(L, 2), ml, P);
+                const float ms = lane < spans ? ml[0] : -INFINITY;
+                const float mx = dpp_max_f32(ms);
+                const float weight = lane < spans ? expf(ms - mx) : 0.0f;
+                const float total = dpp_sum_f32(lane < spans ? ml[1] * weight : 0.0f);
+                float acc = 0.0f;
+                for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
+                    float os[kMergeBatch];
+                    auto o_index = [&](int j) { return s0 + j < spans ? (int)((s0 + j) * stride + 2 + lane) : -1; };
+                    ok = await(base, o_index, epoch(L, 2), os, P);
 #pragma unroll
-                for (int h = 0; h < kHeadsA; ++h) {
-                    const int gh = aw + kA * h;
-                    if (gh < group && ok) {
-                        const u64* base = P.x_part + ((size_t)item_g * spans * group + gh) * (dim + 2);
-                        float ml[2];
-                        auto ml_index = [&](int i) { return lane < spans ? (int)(lane * stride) + i : -1; };
-                        ok = await(base, ml_index, epoch(L, 2), ml, P);
-                        const float ms = lane < spans ? ml[0] : -INFINITY;
-                        const float mx = wave_max_f32(ms);
-                        const float weight = lane < spans ? expf(ms - mx) : 0.0f;
-                        const float total = wave_sum_f32(lane < spans ? ml[1] * weight : 0.0f);
-                        float acc = 0.0f;
-                        for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
-                            float os[kMergeBatch];
-                            auto o_index = [&](int j) {
-                                return s0 + j < spans ? (int)((s0 + j) * stride + 2 + lane) : -1;
-                            };
-                            ok = await(base, o_index, epoch(L, 2), os, P);
-#pragma unroll
-                            for (int j = 0; j < kMergeBatch; ++j) {
-                                const float wj = __shfl(weight, (s0 + j) & 63, kWave);
-                                if (s0 + j < spans) acc = fmaf(os[j], wj, acc);
-                            }
-                        }
-                        if (ok)
-                            publish(P.x_attn + (item_g * group + gh) * dim + lane, epoch(L, 3),
-                                    total > 0.0f ? acc / total : 0.0f);
+                    for (int j = 0; j < kMergeBatch; ++j) {
+                        const float wj = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, weight), (s0 + j) & 63));
+                        acc = s0 + j < spans ? fmaf(os[j], wj, acc) : acc;
                     }
                 }
-                if (!a_agree(ok, s, round)) return false;
-                stamp(P.trace, b, 64 * L + 60);
+                if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), total > 0.0f ? acc / total : 0.0f);
             }
+            if (!a_agree(ok, s, round)) return false;
+            stamp(P.trace, b, 64 * L + 60);
         }
         stamp(P.trace, b, 64 * L + 4);
 
         // ---- attention output -> int8 for o_proj
         {
             float xa[kNH];
-            if (!a_agree(await_quads(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
+            if (!a_agree(await_quads<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
             stamp(P.trace, b, 64 * L + 5);
             quantize_into(xa, qw, 1, a, s, round, parity);
             post(s, 4 * L + 1, round);
         }
         // ---- after o_proj -> RMSNorm -> int8 for gate|up
         fetch_gamma(gamma, Ly.post_gamma, H, a);
-        if (!a_agree(await_quads(P.x_mid, H, epoch(L, 4), x, a, P), s, round)) return false;
+        if (!a_agree(await_quads<kNH>(P.x_mid, H, epoch(L, 4), x, a, P), s, round)) return false;
         stamp(P.trace, b, 64 * L + 6);
         store_quads(s.h_mid, x, a);
         rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
@@ -680,7 +773,10 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- SiLU-gated activation -> int8 for down_proj
         {
             float xd[kNF];
-            if (!a_agree(await_quads(P.x_act, F, epoch(L, 5), xd, a, P), s, round)) return false;
+            // in two halves (fewer words held at once), one watched word
+            const bool ok = await_quads<kNF / 2, kNF / 8>(P.x_act, F, epoch(L, 5), xd + kNF / 2, a, P) &&
+                            await_quads<kNF / 2, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
+            if (!a_agree(ok, s, round)) return false;
             stamp(P.trace, b, 64 * L + 7);
             quantize_into(xd, F, 1, a, s, round, parity);
             post(s, 4 * L + 3, round);
@@ -688,7 +784,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- the next layer's input (the last layer's feeds the head below)
         if (L + 1 < P.layers) {
             stamp(P.trace, b, 64 * (L + 1) + 0);
-            if (!a_agree(await_quads(P.x_hidden, H, epoch(L, 6), x, a, P), s, round)) return false;
+            if (!a_agree(await_quads<kNH>(P.x_hidden, H, epoch(L, 6), x, a, P), s, round)) return false;
         }
     }
     // ---- final RMSNorm -> FP32 input of the head
@@ -696,7 +792,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         float gamma[kNH];
         fetch_gamma(gamma, P.final_gamma, H, a);
         stamp(P.trace, b, 64 * P.layers + 0);
-        if (!a_agree(await_quads(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, round)) return false;
+        if (!a_agree(await_quads<kNH>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, round)) return false;
         stamp(P.trace, b, 64 * P.layers + 1);
         rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
         store_quads(s.xf, x, a);
@@ -899,7 +995,6 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         s.ready = -1;
         s.a_count = 0;
         s.abort = 0;
-        s.last = 0;
     }
     {
         const int words = P.layers * (int)(sizeof(StepLayer) / 16);
@@ -942,12 +1037,12 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
                 ab = fmaf(wb[j].z, xv.z, ab); ab = fmaf(wb[j].w, xv.w, ab);
             }
         }
-        aa = wave_sum_f32(aa);
+        aa = dpp_sum_f32(aa);
         const float la = aa + ldg(P.head.bias + r);
         if (lane == 0) stg(P.logits + r, la);
         if (better(la, r, best, best_i)) { best = la; best_i = r; }
         if (two) {
-            ab = wave_sum_f32(ab);
+            ab = dpp_sum_f32(ab);
             const float lb = ab + ldg(P.head.bias + r2);
             if (lane == 0) stg(P.logits + r2, lb);
             if (better(lb, r2, best, best_i)) { best = lb; best_i = r2; }

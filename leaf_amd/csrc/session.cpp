@@ -378,12 +378,12 @@ void Session::step_prepare() {
     p.cosines = rope_cos_.as<float>();
     p.sines = rope_sin_.as<float>();
     p.kv = kv_.as<float>();
-    // Algorithmic bytes: int8 weights and f32 row scales of every layer, the
-    // FP32 head, plus K and V of every visible key (added per step).
+    // Algorithmic bytes: int8 weights, f32 row scales and biases of every
+    // layer, the FP32 head, plus K and V of every visible key (added per step).
     double bytes = 0;
     for (const Layer& L : m.layers)
         for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
-            bytes += double(l->view.rows) * l->view.cols + 4.0 * l->view.rows;
+            bytes += double(l->view.rows) * l->view.cols + 8.0 * l->view.rows;
     bytes += 4.0 * double(m.head.view.rows) * m.head.view.cols;
     step_bytes_ = bytes;
     step_kv_bytes_ = 2.0 * 4.0 * c.layers * c.kv_heads * c.head_dim;
