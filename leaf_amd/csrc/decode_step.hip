@@ -97,6 +97,7 @@ struct __align__(16) Shared {
     float best_v[kWaves];
     int best_i[kWaves];
     int ready;                      // last phase whose input the exchange waves posted
+    int published;                  // phase outputs this block's weight waves published (kB per phase)
     int a_count;                    // exchange-wave barrier arrivals
     int abort;
 };
@@ -223,16 +224,19 @@ __device__ __forceinline__ bool await(const u64* src, Index index, unsigned epoc
     return true;
 }
 
-// Exchange-lane ownership of a vector: lane a holds x[4 g + j] = element
-// 4 (g kAT + a) + j.  Quads of consecutive elements keep LDS stores and gamma
-// loads 16 bytes wide, while each load instruction of a wave covers 64
-// neighbouring quads (coalesced: the exchange words live in uncached memory,
-// where a strided word costs a whole memory transaction).  Vectors handled
-// this way have n % 4 == 0 and buffers of at least kAT * N words.
-__device__ __forceinline__ int quad_of(int g, int a) { return g * kAT + a; }
+// Exchange-lane ownership of a vector: lane a holds x[kRun g + j] = element
+// kRun (g kAT + a) + j.  A run of two elements is one 16-byte load of two
+// tagged words, and a wave's load instruction reads 1 KiB of consecutive
+// memory: the exchange words live in uncached memory, where a wave
+// instruction whose lanes are not contiguous turns into many small
+// transactions (runs of four, read as two 16-byte halves 32 bytes apart,
+// measured 2.7 us for 24 KiB per block).  Vectors handled this way have
+// n % kRun == 0 and buffers of at least kAT * N words.
+constexpr int kRun = 2;
+__device__ __forceinline__ int run_of(int g, int a) { return g * kAT + a; }
 
 // A raw buffer resource over exchange words: its loads take a per-lane
-// 32-bit offset plus a wave-uniform SGPR offset, so a lane's quads need one
+// 32-bit offset plus a wave-uniform SGPR offset, so a lane's runs need one
 // address register rather than one 64-bit address per word.  Loads use sc1
 // (coherent at agent scope), like the atomic loads of fetch().
 constexpr int kRawBufferWord3 = 0x00020000;   // descriptor word 3 of a raw (untyped) buffer on gfx9
@@ -253,25 +257,26 @@ __device__ __forceinline__ bool spin_until(const u64* p, unsigned epoch, unsigne
     return true;
 }
 
-// This lane's quads of the n-element vector src once they all carry
-// `epoch`.  Quads past n are not waited for and hold whatever the buffer
-// holds there (callers mask them out or never read them).  A lane first
-// watches one word it needs, then reads all of them; a word still missing is
-// watched alone before the next full read (a full re-read per spin from every
-// lane of every block would crowd the memory pipeline the weight waves use).
-// G0 > 0 takes the lane's quads G0 .. G0 + N/4 - 1 only (a long vector in
-// parts, so fewer 64-bit words are held at once); Watch false skips the first
-// watched word (a part read after another part's watch saw the vector land).
+// This lane's runs of the n-element vector src once they all carry
+// `epoch`.  Runs past n are not waited for and hold whatever the buffer holds
+// there (callers mask them out or never read them).  A lane first watches one
+// word it needs, then reads all of them; a word still missing is watched alone
+// before the next full read (a full re-read per spin from every lane of every
+// block would crowd the memory pipeline the weight waves use).  G0 > 0 takes
+// the lane's runs G0 .. G0 + N/kRun - 1 only (a long vector in parts, so
+// fewer 64-bit words are held at once); Watch false skips the first watched
+// word (the caller knows the vector is landing).
 template <int N, int G0 = 0, bool Watch = true>
-__device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoch, float* out, int a,
-                                            const StepParams& P) {
-    static_assert(N % 4 == 0, "groups of four words");
-    constexpr int G = N / 4;
-    src += 4 * kAT * G0;
-    const int live = n / 4 - a - kAT * G0;   // quad g (from G0) is inside the vector when g * kAT < live
-    const u64* mine = src + 4 * a;
+__device__ __forceinline__ bool await_runs(const u64* src, int n, unsigned epoch, float* out, int a,
+                                           const StepParams& P) {
+    static_assert(N % kRun == 0, "whole runs");
+    constexpr int G = N / kRun;
+    src += kRun * kAT * G0;
+    const int live = n / kRun - a - kAT * G0;   // run g (from G0) is inside the vector when g * kAT < live
+    const u64* mine = src + kRun * a;
     unsigned spin = 0;
-    if (Watch && live > 0 && !spin_until(mine + 4 * kAT * min(G - 1, (live - 1) / kAT) + 3, epoch, spin, P))
+    if (Watch && live > 0 &&
+        !spin_until(mine + kRun * kAT * min(G - 1, (live - 1) / kAT) + kRun - 1, epoch, spin, P))
         return false;
     const __amdgpu_buffer_rsrc_t view = exchange_view(src);
     u64 w[N];
@@ -279,15 +284,16 @@ __device__ __forceinline__ bool await_quads(const u64* src, int n, unsigned epoc
         asm volatile("" ::: "memory");   // a fresh read each time round
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(view, 32 * a + 8 * (i % 4), 32 * kAT * (i / 4), kLoadSc1);
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(view, 8 * kRun * a + 8 * (i % kRun),
+                                                              8 * kRun * kAT * (i / kRun), kLoadSc1);
             w[i] = (u64(v.y) << 32) | v.x;
         }
         int missing = -1;
 #pragma unroll
         for (int i = N - 1; i >= 0; --i)
-            missing = ((i / 4) * kAT < live && unsigned(w[i] >> 32) != epoch) ? i : missing;
+            missing = ((i / kRun) * kAT < live && unsigned(w[i] >> 32) != epoch) ? i : missing;
         if (missing < 0) break;
-        if (!spin_until(mine + 4 * kAT * (missing >> 2) + (missing & 3), epoch, spin, P)) return false;
+        if (!spin_until(mine + kRun * kAT * (missing / kRun) + missing % kRun, epoch, spin, P)) return false;
     }
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = __uint_as_float(unsigned(w[i]));
@@ -348,20 +354,33 @@ __device__ __forceinline__ float a_max(float v, Shared& s, int& round, int& pari
     return r;
 }
 
+// Waits until this block's weight waves issued their stores of `phases`
+// phases (kB each).  Blocks publish within about a microsecond of each other,
+// so this is when the exchange waves start reading a vector: the first full
+// read then usually finds every word, one round trip sooner than watching a
+// remote word first.  Missing words are still watched and read again.
+__device__ __forceinline__ bool wait_published(Shared& s, int phases) {
+    for (unsigned spin = 0; lds_load(&s.published) < kB * phases; ++spin) {
+        if (spin > kSpinLimit || lds_load(&s.abort)) return false;
+        __builtin_amdgcn_s_sleep(0);
+    }
+    return true;
+}
+
 // Posts phase `phase`: every exchange wave has finished writing its input.
 __device__ __forceinline__ void post(Shared& s, int phase, int& round) {
     a_sync(s, round);
     if (threadIdx.x == 0) lds_store(&s.ready, phase);
 }
 
-// RMSNorm of the n values held as quads (decoder.cpp:706-727).
+// RMSNorm of the n values held as runs (decoder.cpp:706-727).
 template <int N>
 __device__ __forceinline__ void rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
                                               Shared& s, int& round, int& parity) {
-    const int live = n / 4 - a;
+    const int live = n / kRun - a;
     float sq = 0.0f;
 #pragma unroll
-    for (int i = 0; i < N; ++i) sq += (i / 4) * kAT < live ? x[i] * x[i] : 0.0f;
+    for (int i = 0; i < N; ++i) sq += (i / kRun) * kAT < live ? x[i] * x[i] : 0.0f;
     sq = a_sum(sq, s, round, parity);
     const float scale = 1.0f / sqrtf(sq / (float)n + eps);
 #pragma unroll
@@ -369,50 +388,45 @@ __device__ __forceinline__ void rms_normalize(float (&x)[N], int n, const float 
 }
 
 // Per-token symmetric int8 quantization into s.xq[buf] (decoder.cpp:1028-1043).
-// Quads past n (zeros) land in the buffer's tail, which no reader uses.
+// Runs past n land in the buffer's tail, which no reader uses.
 template <int N>
 __device__ __forceinline__ void quantize_into(const float (&x)[N], int n, int buf, int a, Shared& s, int& round,
                                               int& parity) {
-    static_assert(N % 4 == 0, "quads");
-    const int live = n / 4 - a;
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
+    const int live = n / kRun - a;
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / 4) * kAT < live ? fabsf(x[i]) : 0.0f);
+    for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / kRun) * kAT < live ? fabsf(x[i]) : 0.0f);
     amax = a_max(amax, s, round, parity);
     const float sx = fmaxf(amax / 127.0f, 1e-12f);
     const float multiplier = 1.0f / sx;
 #pragma unroll
-    for (int g = 0; g < N / 4; ++g) {
-        const float* v = x + 4 * g;
-        *reinterpret_cast<uint32_t*>(s.xq[buf] + 4 * quad_of(g, a)) =
-            (uint32_t)(quantize_one(v[0], multiplier) & 255) |
-            ((uint32_t)(quantize_one(v[1], multiplier) & 255) << 8) |
-            ((uint32_t)(quantize_one(v[2], multiplier) & 255) << 16) |
-            ((uint32_t)(quantize_one(v[3], multiplier) & 255) << 24);
+    for (int g = 0; g < N / kRun; ++g) {
+        const float* v = x + kRun * g;
+        *reinterpret_cast<uint16_t*>(s.xq[buf] + kRun * run_of(g, a)) =
+            (uint16_t)((quantize_one(v[0], multiplier) & 255) | ((quantize_one(v[1], multiplier) & 255) << 8));
     }
     if (a == 0) s.sx[buf] = sx;
 }
 
-// This lane's quads into dst (natural element order; dst holds kAT * N floats).
+// This lane's runs into dst (natural element order; dst holds kAT * N floats).
 template <int N>
-__device__ __forceinline__ void store_quads(float* dst, const float (&x)[N], int a) {
-    static_assert(N % 4 == 0, "quads");
+__device__ __forceinline__ void store_runs(float* dst, const float (&x)[N], int a) {
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
 #pragma unroll
-    for (int g = 0; g < N / 4; ++g)
-        *reinterpret_cast<v4f*>(dst + 4 * quad_of(g, a)) = v4f{x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]};
+    for (int g = 0; g < N / kRun; ++g)
+        *reinterpret_cast<v2f*>(dst + kRun * run_of(g, a)) = v2f{x[kRun * g], x[kRun * g + 1]};
 }
 
-// gamma for this lane's quads; quads past n read the last one (their x are 0).
+// gamma for this lane's runs; runs past n read the last one (their x are 0).
 template <int N>
 __device__ __forceinline__ void fetch_gamma(float (&g)[N], const float* gamma, int n, int a) {
-    static_assert(N % 4 == 0, "quads");
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
 #pragma unroll
-    for (int q = 0; q < N / 4; ++q) {
-        const v4f v = ldg(reinterpret_cast<const v4f*>(gamma + 4 * min(quad_of(q, a), n / 4 - 1)));
-        g[4 * q] = v[0];
-        g[4 * q + 1] = v[1];
-        g[4 * q + 2] = v[2];
-        g[4 * q + 3] = v[3];
+    for (int q = 0; q < N / kRun; ++q) {
+        const v2f v = ldg(reinterpret_cast<const v2f*>(gamma + kRun * min(run_of(q, a), n / kRun - 1)));
+        g[kRun * q] = v[0];
+        g[kRun * q + 1] = v[1];
     }
 }
 
@@ -496,6 +510,12 @@ __device__ __forceinline__ float embed_value(const WeightView& w, uint32_t id, i
     return (float)ldg(static_cast<const int8_t*>(w.data) + index) * ldg(w.scales + id);
 }
 
+// A weight wave has issued the stores of its current phase.
+__device__ __forceinline__ void note_published(Shared& s) {
+    asm volatile("" ::: "memory");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&s.published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Waits (weight waves) until the exchange waves posted `phase`.
 __device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
     for (unsigned spin = 0;; ++spin) {
@@ -509,7 +529,8 @@ __device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
 
 // Phase timeline: the first thread of each role stamps the 100 MHz device
 // clock at phase boundaries into trace[block][point]: points 64 * layer + k
-// (k < 8 exchange waves, 8 + 8 * w + j weight wave w), then the head's.  Off (null)
+// (k < 8 exchange waves, 8 + 8 * w + j weight wave w, 56-62 inside attention
+// and the ffn-vector read), then the head's.  Off (null)
 // outside diagnostics.
 __device__ __forceinline__ void stamp(unsigned long long* trace, int block, int point, int thread = 0) {
     if (trace && threadIdx.x == thread)
@@ -641,7 +662,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         const uint32_t id = ldg(P.token);
 #pragma unroll
         for (int i = 0; i < kNH; ++i) {
-            const int e = 4 * quad_of(i / 4, a) + i % 4;
+            const int e = kRun * run_of(i / kRun, a) + i % kRun;
             x[i] = e < H ? embed_value(P.embedding, id, e) * P.embedding_scale : 0.0f;
         }
     }
@@ -671,7 +692,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
                 kv_pre[kNK + j] = ldg(reinterpret_cast<const v4u*>(Vc + at));
             }
         }
-        store_quads(s.h_in, x, a);
+        store_runs(s.h_in, x, a);
         rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
         quantize_into(x, H, 0, a, s, round, parity);
         post(s, 4 * L + 0, round);
@@ -692,16 +713,17 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // in the last blocks) combine the spans as soon as they land.
         if (has_item) {
             // q of the group's heads, and the new key's k (lanes < dim) or v
-            // (the q|k|v buffer is padded so a lane's quads stay inside it)
+            // (the q|k|v buffer is padded so a lane's runs stay inside it)
             float got[kNQ - 1], kv_got;
             const int q_base = item_g * group * dim;
             const int kv_word = a < dim ? qw + item_g * dim + a : qw + kvw + item_g * dim + (a - dim);
             const bool has_kv = new_key && a < 2 * dim;
-            const bool ok_q = await_quads<kNQ - 1>(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
+            const bool ok_q = wait_published(s, 4 * L + 1) &&
+                              await_runs<kNQ - 1, 0, false>(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
             const bool ok_kv = ok_q && await_one(P.x_qkv + kv_word, has_kv, epoch(L, 1), kv_got, P);
             if (!a_agree(ok_kv, s, round)) return false;
             stamp(P.trace, b, 64 * L + 3);
-            store_quads(s.q, got, a);
+            store_runs(s.q, got, a);
             if (has_kv) {
                 const int nl = pos - k0;
                 if (a < dim) s.k[nl * kKStride + a] = kv_got;
@@ -757,25 +779,30 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- attention output -> int8 for o_proj
         {
             float xa[kNH];
-            if (!a_agree(await_quads<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
+            if (!a_agree(await_runs<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
             stamp(P.trace, b, 64 * L + 5);
             quantize_into(xa, qw, 1, a, s, round, parity);
             post(s, 4 * L + 1, round);
         }
         // ---- after o_proj -> RMSNorm -> int8 for gate|up
         fetch_gamma(gamma, Ly.post_gamma, H, a);
-        if (!a_agree(await_quads<kNH>(P.x_mid, H, epoch(L, 4), x, a, P), s, round)) return false;
+        if (!a_agree(wait_published(s, 4 * L + 2) && await_runs<kNH, 0, false>(P.x_mid, H, epoch(L, 4), x, a, P), s,
+                     round))
+            return false;
         stamp(P.trace, b, 64 * L + 6);
-        store_quads(s.h_mid, x, a);
+        store_runs(s.h_mid, x, a);
         rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
         quantize_into(x, H, 0, a, s, round, parity);
         post(s, 4 * L + 2, round);
         // ---- SiLU-gated activation -> int8 for down_proj
         {
             float xd[kNF];
-            // in two halves (fewer words held at once), one watched word
-            const bool ok = await_quads<kNF / 2, kNF / 8>(P.x_act, F, epoch(L, 5), xd + kNF / 2, a, P) &&
-                            await_quads<kNF / 2, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
+            // in two halves (fewer words held at once)
+            bool ok = wait_published(s, 4 * L + 3);
+            stamp(P.trace, b, 64 * L + 61);
+            ok = ok && await_runs<kNF / 2, kNF / 2 / kRun, false>(P.x_act, F, epoch(L, 5), xd + kNF / 2, a, P);
+            stamp(P.trace, b, 64 * L + 62);
+            ok = ok && await_runs<kNF / 2, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
             if (!a_agree(ok, s, round)) return false;
             stamp(P.trace, b, 64 * L + 7);
             quantize_into(xd, F, 1, a, s, round, parity);
@@ -784,7 +811,9 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- the next layer's input (the last layer's feeds the head below)
         if (L + 1 < P.layers) {
             stamp(P.trace, b, 64 * (L + 1) + 0);
-            if (!a_agree(await_quads<kNH>(P.x_hidden, H, epoch(L, 6), x, a, P), s, round)) return false;
+            if (!a_agree(wait_published(s, 4 * L + 4) && await_runs<kNH, 0, false>(P.x_hidden, H, epoch(L, 6), x, a, P),
+                         s, round))
+                return false;
         }
     }
     // ---- final RMSNorm -> FP32 input of the head
@@ -792,10 +821,13 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         float gamma[kNH];
         fetch_gamma(gamma, P.final_gamma, H, a);
         stamp(P.trace, b, 64 * P.layers + 0);
-        if (!a_agree(await_quads<kNH>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, round)) return false;
+        if (!a_agree(wait_published(s, 4 * P.layers) &&
+                         await_runs<kNH, 0, false>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P),
+                     s, round))
+            return false;
         stamp(P.trace, b, 64 * P.layers + 1);
         rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
-        store_quads(s.xf, x, a);
+        store_runs(s.xf, x, a);
         post(s, 4 * P.layers, round);
     }
     return true;
@@ -925,6 +957,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                     }
                 }
         }
+        note_published(s);
         stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
         load_qkv(next, more);
         // ---- o_proj + residual
@@ -942,6 +975,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                                 s.h_in[row] + dequant(acc, sx, w.os[k].scale, w.os[k].bias));
                 }
         }
+        note_published(s);
         stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
         load_o(next, more);
         // ---- gate|up + SiLU gate
@@ -962,6 +996,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                     }
                 }
         }
+        note_published(s);
         stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
         load_gate_up(next, more);
         // ---- down_proj + residual
@@ -979,6 +1014,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                                 s.h_mid[row] + dequant(acc, sx, w.ds[k].scale, w.ds[k].bias));
                 }
         }
+        note_published(s);
         stamp(P.trace, b, 64 * L + 15 + 8 * bw, kAT + kWave * bw);
         load_down(next, more);
     }
@@ -993,6 +1029,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     const int H = P.hidden;
     if (t == 0) {
         s.ready = -1;
+        s.published = 0;
         s.a_count = 0;
         s.abort = 0;
     }

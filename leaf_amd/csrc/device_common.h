@@ -18,6 +18,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 // 128-bit streaming load (non-temporal: weights are read once per forward).
 __device__ __forceinline__ uint4 load_stream16(const void* p) {
