@@ -797,12 +797,10 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- SiLU-gated activation -> int8 for down_proj
         {
             float xd[kNF];
-            // in two halves (fewer words held at once)
             bool ok = wait_published(s, 4 * L + 3);
             stamp(P.trace, b, 64 * L + 61);
-            ok = ok && await_runs<kNF / 2, kNF / 2 / kRun, false>(P.x_act, F, epoch(L, 5), xd + kNF / 2, a, P);
+            ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
             stamp(P.trace, b, 64 * L + 62);
-            ok = ok && await_runs<kNF / 2, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
             if (!a_agree(ok, s, round)) return false;
             stamp(P.trace, b, 64 * L + 7);
             quantize_into(xd, F, 1, a, s, round, parity);
