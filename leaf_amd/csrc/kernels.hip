@@ -873,6 +873,142 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int 
     }
 }
 
+// ----------------------------------------- prefill attention: f32 MFMA ---
+// Flash attention for head dim 64 (every supported decoder family).  A block
+// owns one query head and 64 tokens; wave w owns tokens t0 + 16w .. +15.  Key
+// tiles of 64 keys are staged in LDS (K and V, rows padded to 68 floats: the
+// MFMA operand reads then hit every bank twice, the minimum for 64 lanes),
+// the next tile waiting in registers while this one is used.
+//
+// Per 16 keys a wave computes S^T = K Q^T with v_mfma_f32_16x16x4_f32 (lane l
+// feeds key row l % 16 and query column l % 16 at dims 4c + l / 16), which
+// leaves lane l with the scores of query l % 16 for keys 4 (l / 16) + r,
+// r < 4: exactly the B operand of O^T += V^T P^T when that product takes the
+// keys {4j + r} as its K dimension.  So P never leaves registers.  Softmax is
+// online per query (max and sum exchanged between the four lanes of a query),
+// scores are (q.k * scale) * scale and masked keys are -inf, as in
+// transformer.cpp:112-143; the output is divided by the sum at the end.
+constexpr int kPrefillQ = 64;        // tokens per block
+constexpr int kPrefillKeys = 64;     // keys per LDS tile
+constexpr int kPrefillStride = 68;   // padded row of a K or V tile
+
+// One thread's share of a 64 x 64 K (and V) tile: float4 i, i + 256, ... .
+// Rows at or past `end` were never written (they may hold NaN, and a masked
+// key still multiplies its V row by 0): they are zeros.
+__device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end, v4f (&kr)[4],
+                                                  v4f (&vr)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + kBlock * j, row = f / 16, col = 4 * (f % 16);
+        const int key = k0 + row;
+        const bool ok = key < end;
+        const size_t at = (size_t)(ok ? key : 0) * 64 + col;
+        const v4f kv = *(const v4f*)(K + at), vv = *(const v4f*)(V + at);
+        const v4f zero = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        kr[j] = ok ? kv : zero;
+        vr[j] = ok ? vv : zero;
+    }
+}
+__device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[4], const v4f (&vr)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + kBlock * j, row = f / 16, col = 4 * (f % 16);
+        *(v4f*)(ks + row * kPrefillStride + col) = kr[j];
+        *(v4f*)(vs + row * kPrefillStride + col) = vr[j];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void attention_prefill_kernel(AttentionCall p) {
+    __shared__ float ks[kPrefillKeys * kPrefillStride];
+    __shared__ float vs[kPrefillKeys * kPrefillStride];
+    constexpr int dim = 64;
+    const int h = blockIdx.x, t0 = blockIdx.y * kPrefillQ;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, lj = lane >> 4;
+    const int kvh = h / (p.heads / p.kv_heads);
+    const int tw = t0 + 16 * wave;                    // this wave's first token
+    const int q_tok = tw + li;                        // this lane's query (score columns)
+    const int q_pos = p.position + q_tok;
+    const bool q_live = q_tok < p.tokens;
+    // Q^T operand: dims 4c + lj of query q_tok
+    float qv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+        qv[c] = q_live ? p.q_heads[((size_t)h * p.tokens + q_tok) * dim + 4 * c + lj] : 0.0f;
+    // keys the block needs: [first, end)
+    const int last_tok = min(t0 + kPrefillQ, p.tokens) - 1;
+    const int end = p.position + last_tok + 1;
+    int first = 0;
+    if (p.window) first = max(0, p.position + t0 + 1 - p.window);
+    first &= ~(kPrefillKeys - 1);
+    const float* K = p.keys + (size_t)kvh * p.capacity * dim;
+    const float* V = p.values + (size_t)kvh * p.capacity * dim;
+    v4f kr[4], vr[4];
+    prefill_tile_load(K, V, first, end, kr, vr);
+    v4f o[4];   // O^T: dims 16 dc + 4 lj + i, query li
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) o[dc] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    const float scale = p.scale;
+    for (int k0 = first; k0 < end; k0 += kPrefillKeys) {
+        __syncthreads();   // the previous tile is no longer read
+        prefill_tile_store(ks, vs, kr, vr);
+        __syncthreads();
+        if (k0 + kPrefillKeys < end) prefill_tile_load(K, V, k0 + kPrefillKeys, end, kr, vr);
+        // the keys this wave can see in this tile
+        const int wave_end = min(end, p.position + min(tw + 16, p.tokens));
+        for (int sub = 0; sub < kPrefillKeys && k0 + sub < wave_end; sub += 16) {
+            v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const float* krow = ks + (sub + li) * kPrefillStride + lj;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[4 * c], qv[c], sc, 0, 0, 0);
+            // lane: query q_tok, keys k0 + sub + 4 lj + r
+            float e[4];
+            float tile_max = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + sub + 4 * lj + r;
+                const bool ok = q_live && key <= q_pos && (p.window == 0 || key > q_pos - p.window);
+                e[r] = ok ? sc[r] * scale * scale : -INFINITY;
+                tile_max = fmaxf(tile_max, e[r]);
+            }
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
+            const float m_new = fmaxf(m, tile_max);
+            const float alpha = m_new == -INFINITY ? 1.0f : expf(m - m_new);
+            float tile_sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                e[r] = m_new == -INFINITY ? 0.0f : expf(e[r] - m_new);
+                tile_sum += e[r];
+            }
+            tile_sum += __shfl_xor(tile_sum, 16, kWave);
+            tile_sum += __shfl_xor(tile_sum, 32, kWave);
+            l = l * alpha + tile_sum;
+            m = m_new;
+#pragma unroll
+            for (int dc = 0; dc < 4; ++dc) o[dc] = o[dc] * alpha;
+            // O^T += V^T P^T over keys {4 j + r}: lane supplies V[4 lj + r][16 dc + li]
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* vrow = vs + (sub + 4 * lj + r) * kPrefillStride + li;
+#pragma unroll
+                for (int dc = 0; dc < 4; ++dc)
+                    o[dc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * dc], e[r], o[dc], 0, 0, 0);
+            }
+        }
+    }
+    if (q_live) {
+        float* out = p.out + ((size_t)q_tok * p.heads + h) * dim;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc) {
+            const v4f v = l > 0.0f ? v4f{o[dc][0] / l, o[dc][1] / l, o[dc][2] / l, o[dc][3] / l}
+                                   : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            *(v4f*)(out + 16 * dc + 4 * lj) = v;
+        }
+    }
+}
+
 __global__ void attention_merge_kernel(AttentionCall p, int splits) {
     const int h = blockIdx.x, t = blockIdx.y;
     const float* part = p.partial + ((size_t)t * p.heads + h) * splits * (p.dim + 2);
@@ -1333,6 +1469,11 @@ bool launch_attention(const AttentionCall& call, hipStream_t stream) {
             splits = (total + per_split - 1) / per_split;
         }
         if (splits == 1) per_split = total;
+    }
+    if (splits == 1 && call.tokens > 1 && call.dim == 64) {
+        attention_prefill_kernel<<<dim3(call.heads, (call.tokens + kPrefillQ - 1) / kPrefillQ), kBlock, 0, stream>>>(
+            call);
+        return true;
     }
     dim3 grid(call.heads, call.tokens, splits);
     attention_kernel<<<grid, kBlock, 0, stream>>>(call, per_split);

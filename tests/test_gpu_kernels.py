@@ -211,17 +211,23 @@ def test_rope_kv_matches_reference_formula(rt, oracle):
     assert bits_equal(values.numpy()[:, pos:pos + M], v)
 
 
-@pytest.mark.parametrize("tokens,position,window", [(1, 640, 0), (1, 4351, 0), (1, 700, 64), (37, 0, 0),
-                                                    (13, 21, 0), (16, 5, 7)])
-def test_attention_matches_oracle(rt, oracle, tokens, position, window):
+@pytest.mark.parametrize("tokens,position,window,heads,kv", [
+    (1, 640, 0, 14, 2), (1, 4351, 0, 14, 2), (1, 700, 64, 14, 2), (37, 0, 0, 14, 2), (13, 21, 0, 14, 2),
+    (16, 5, 7, 14, 2),
+    # prefill sizes: the TinyLlama prompt, a chunk after cached keys, a window
+    (512, 0, 0, 32, 4), (200, 300, 0, 32, 4), (130, 100, 64, 14, 2)])
+def test_attention_matches_oracle(rt, oracle, tokens, position, window, heads, kv):
     from leaf_amd.runtime import check, library
     rng = np.random.default_rng(tokens * 100 + position)
-    heads, kv, dim = 14, 2, 64
+    dim = 64
     total = position + tokens
-    cap = total + 3
+    cap = total + 70
     q = rng.standard_normal((heads, tokens, dim), dtype=np.float32)
     keys = rng.standard_normal((kv, cap, dim), dtype=np.float32)
     values = rng.standard_normal((kv, cap, dim), dtype=np.float32)
+    # cache rows past the visible keys were never written: NaN must not leak
+    keys[:, total:] = np.nan
+    values[:, total:] = np.nan
     dq, dk, dv = rt.DeviceArray.of(q), rt.DeviceArray.of(keys), rt.DeviceArray.of(values)
     out = rt.DeviceArray((tokens, heads * dim), np.float32)
     check(library().lh_attention(dq.ptr, dk.ptr, dv.ptr, cap, heads, kv, dim, tokens, position, window, out.ptr,
@@ -233,7 +239,9 @@ def test_attention_matches_oracle(rt, oracle, tokens, position, window):
         mask[t, begin:end] = 1
     scale = np.float32(1) / np.sqrt(np.sqrt(np.float32(dim)))
     ref = oracle.attention(q, keys, values, mask, heads, kv, tokens, total, cap, dim, float(scale))
-    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=2e-6)
+    got = out.numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=2e-6)
 
 
 def test_argmax_first_maximum(rt):
