@@ -126,12 +126,19 @@ lh_status linear_impl(const lh_weight* weight, const float* x, const int8_t* q, 
         c.y = y;
         c.acc_out = acc;
         c.force_path = force_path;
-        if (c.integer_activations && !q) {
-            // quantized copy of x (when the kernel does not quantize in registers)
-            const size_t bytes = ((tokens * c.w.cols + 255) / 256) * 256 + tokens * 4;
-            auto* base = static_cast<uint8_t*>(scratch_bytes(bytes));
-            c.xq_scratch = reinterpret_cast<int8_t*>(base);
-            c.xs_scratch = reinterpret_cast<float*>(base + ((tokens * c.w.cols + 255) / 256) * 256);
+        if (c.integer_activations) {
+            // quantized copy of x (when the kernel does not quantize in registers),
+            // then room for 8 split-K partial sums of the output (prefill GEMM)
+            const size_t q_bytes = q ? 0 : ((tokens * c.w.cols + 255) / 256) * 256;
+            const size_t s_bytes = q ? 0 : ((tokens * 4 + 255) / 256) * 256;
+            const size_t split = tokens > 4 ? 8 * tokens * c.w.rows : 0;
+            auto* base = static_cast<uint8_t*>(scratch_bytes(q_bytes + s_bytes + split * sizeof(int32_t) + 256));
+            if (!q) {
+                c.xq_scratch = reinterpret_cast<int8_t*>(base);
+                c.xs_scratch = reinterpret_cast<float*>(base + q_bytes);
+            }
+            c.split_scratch = split ? reinterpret_cast<int32_t*>(base + q_bytes + s_bytes) : nullptr;
+            c.split_capacity = split;
         }
         const int path = leafhip::launch_linear(c, as_stream(stream));
         if (path < 0) throw leafhip::Error(LH_ERROR_UNSUPPORTED, "Leaf decoder: unsupported linear configuration");

@@ -82,6 +82,8 @@ struct LinearCall {
     float* xs_scratch = nullptr;    // [tokens]
     float* norm_scratch = nullptr;  // [tokens, cols] when `norm` cannot be fused into the kernel
     int force_path = 0;             // 0 auto, 1 GEMV, 2 generic, 3 GEMM
+    int32_t* split_scratch = nullptr;   // split-K int32 sums for the W8A8 GEMM; may be null
+    size_t split_capacity = 0;          // int32 elements available in split_scratch
     PairEpilogue pair;              // single-token paired epilogue (y unused when set)
 };
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when

@@ -664,6 +664,131 @@ __global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const i
         }
 }
 
+// ----------------------------- W8A8 prefill, per-row scales: tiled MFMA ---
+// Y[t, n] = ((float)sum_k Xq[t, k] W[n, k] * s_x[t]) * s_w[n] + b[n] for
+// per-row weight scales (group = K, the export default) and K % 128 == 0.
+// A block owns 128 tokens x 128 weight rows; its four waves own 64 x 64 each
+// as 4 x 4 tiles of v_mfma_i32_16x16x64_i8 (operand layout as in
+// gemm_int8_kernel: lane l feeds row l % 16 with K bytes 16 (l / 16) .. +15 of
+// each 64-byte step).  K advances 128 bytes per stage: both 128 x 128 operand
+// tiles go to LDS (rows padded to 144 bytes, so a 16-lane group of operand
+// reads hits every bank once), double-buffered, and the next stage waits in
+// registers while this one feeds the MFMAs.  Two blocks share a CU (70 KB of
+// LDS each), so one block's loads overlap the other's MFMAs.  The integer sums are exact and
+// the epilogue is the CPU path's, so results are bit-identical to it.
+constexpr int kGemmTile = 128;                 // tokens and rows per block
+constexpr int kGemmStage = 128;                // K bytes per stage
+constexpr int kGemmRow = kGemmStage + 16;      // padded LDS row
+constexpr int kGemmLoads = kGemmTile * kGemmStage / 16 / kBlock;   // 16-byte loads per thread per operand
+
+__device__ __forceinline__ void gemm_stage_load(const int8_t* xq, const int8_t* W, int K, int tokens, int N, int m0,
+                                                int n0, int k0, v4i (&ra)[kGemmLoads], v4i (&rb)[kGemmLoads]) {
+#pragma unroll
+    for (int j = 0; j < kGemmLoads; ++j) {
+        const int f = threadIdx.x + kBlock * j, row = f / (kGemmStage / 16), col = (f % (kGemmStage / 16)) * 16;
+        // Rows past the token or weight count read row 0 instead: their
+        // sums are never stored, and no select waits on the load here.
+        const int t = m0 + row, n = n0 + row;
+        ra[j] = *(const v4i*)(xq + (size_t)(t < tokens ? t : 0) * K + k0 + col);
+        rb[j] = __builtin_nontemporal_load((const v4i*)(W + (size_t)(n < N ? n : 0) * K + k0 + col));
+    }
+}
+__device__ __forceinline__ void gemm_stage_store(int8_t* la, int8_t* lb, const v4i (&ra)[kGemmLoads],
+                                                 const v4i (&rb)[kGemmLoads]) {
+#pragma unroll
+    for (int j = 0; j < kGemmLoads; ++j) {
+        const int f = threadIdx.x + kBlock * j, row = f / (kGemmStage / 16), col = (f % (kGemmStage / 16)) * 16;
+        *(v4i*)(la + row * kGemmRow + col) = ra[j];
+        *(v4i*)(lb + row * kGemmRow + col) = rb[j];
+    }
+}
+
+// Split K (blockIdx.z = split of `splits`, each `split_stages` stages long):
+// with `partial` set, a block stores its int32 sums to partial[split][t][n]
+// and gemm_w8a8_split_epilogue adds the splits (exactly, in split order) and
+// applies the epilogue; without it, the block applies the epilogue itself.
+__global__ __launch_bounds__(kBlock, 2) void gemm_w8a8_tile_kernel(WeightView w, const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ xs, int tokens,
+                                                               float* __restrict__ y, int epilogue,
+                                                               int32_t* __restrict__ acc_out, int split_stages,
+                                                               int32_t* __restrict__ partial) {
+    __shared__ __align__(16) int8_t lds[2][2][kGemmTile * kGemmRow];   // [buffer][activations | weights]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, N = w.rows;
+    const int m0 = blockIdx.y * kGemmTile, n0 = blockIdx.x * kGemmTile;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 15, lk = (lane >> 4) * 16;
+    const int8_t* W = (const int8_t*)w.data;
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    v4i ra[kGemmLoads], rb[kGemmLoads];
+    const int stages = split_stages;
+    const int kb = blockIdx.z * split_stages * kGemmStage;   // this split's first K byte
+    gemm_stage_load(xq, W, K, tokens, N, m0, n0, kb, ra, rb);
+    gemm_stage_store(lds[0][0], lds[0][1], ra, rb);
+    __syncthreads();
+    for (int s = 0; s < stages; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < stages) gemm_stage_load(xq, W, K, tokens, N, m0, n0, kb + (s + 1) * kGemmStage, ra, rb);
+        const int8_t* A = lds[buf][0];
+        const int8_t* B = lds[buf][1];
+#pragma unroll
+        for (int kk = 0; kk < kGemmStage / 64; ++kk) {
+            v4i af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *(const v4i*)(A + (wm + 16 * i + li) * kGemmRow + 64 * kk + lk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = *(const v4i*)(B + (wn + 16 * j + li) * kGemmRow + 64 * kk + lk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        // the other buffer was last read before the previous barrier
+        if (s + 1 < stages) gemm_stage_store(lds[buf ^ 1][0], lds[buf ^ 1][1], ra, rb);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + wn + 16 * j + li;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
+                if (t < tokens && n < N) {
+                    if (partial) {
+                        partial[((size_t)blockIdx.z * tokens + t) * N + n] = acc[i][j][r];
+                    } else {
+                        if (acc_out) acc_out[(size_t)t * N + n] = acc[i][j][r];
+                        const float res = fmaf((float)acc[i][j][r] * xs[t], w.scales[n], 0.0f);
+                        store_out(y, (size_t)t * N + n, res, bias_at(w, n), epilogue);
+                    }
+                }
+            }
+        }
+}
+
+__global__ __launch_bounds__(kBlock) void gemm_w8a8_split_epilogue(WeightView w, const float* __restrict__ xs,
+                                                                  int tokens, const int32_t* __restrict__ partial,
+                                                                  int splits, float* __restrict__ y, int epilogue,
+                                                                  int32_t* __restrict__ acc_out) {
+    const int N = w.rows;
+    const size_t count = (size_t)tokens * N;
+    for (size_t i = blockIdx.x * (size_t)kBlock + threadIdx.x; i < count; i += (size_t)gridDim.x * kBlock) {
+        int acc = 0;
+        for (int s = 0; s < splits; ++s) acc += partial[s * count + i];
+        const int t = (int)(i / N), n = (int)(i % N);
+        if (acc_out) acc_out[i] = acc;
+        const float res = fmaf((float)acc * xs[t], w.scales[n], 0.0f);
+        store_out(y, i, res, bias_at(w, n), epilogue);
+    }
+}
+
 // ------------------------------------------------ FP prefill: f32 MFMA ---
 // Y[t, n] = sum_k X[t, k] W[n, k] with v_mfma_f32_16x16x4_f32; weights of any
 // storage are widened (BF16) or dequantized (INT8 / INT4) as they are loaded.
@@ -1397,6 +1522,26 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         if (path == 1) {
             if (w.bits == 8) launch_gemv_int<8>(c, xq, xs, stream); else launch_gemv_int<4>(c, xq, xs, stream);
             return 1;
+        }
+        if (path == 3 && w.group == K && K % kGemmStage == 0) {
+            const int tiles = ceil_div(w.rows, kGemmTile) * ceil_div(c.tokens, kGemmTile);
+            const int stages = K / kGemmStage;
+            // Split K until the grid covers the CUs twice (two blocks per CU),
+            // each split a whole number of stages, when a workspace is given.
+            int splits = 1;
+            while (c.split_scratch && tiles * splits < 512 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 2 &&
+                   (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
+                splits *= 2;
+            dim3 grid(ceil_div(w.rows, kGemmTile), ceil_div(c.tokens, kGemmTile), splits);
+            int32_t* partial = splits > 1 ? c.split_scratch : nullptr;
+            gemm_w8a8_tile_kernel<<<grid, kBlock, 0, stream>>>(w, xq, xs, c.tokens, c.y, c.epilogue, c.acc_out,
+                                                              stages / splits, partial);
+            if (partial) {
+                const int blocks = std::min(ceil_div((size_t)c.tokens * w.rows, kBlock), 4096);
+                gemm_w8a8_split_epilogue<<<blocks, kBlock, 0, stream>>>(w, xs, c.tokens, partial, splits, c.y,
+                                                                        c.epilogue, c.acc_out);
+            }
+            return 3;
         }
         if (path == 3) {
             dim3 grid(ceil_div(w.rows, 64), ceil_div(c.tokens, 64));

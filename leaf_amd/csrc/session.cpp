@@ -133,6 +133,9 @@ void Session::plan(uint32_t tokens, bool all_logits) {
         grow<int8_t>(xq_, P * widest);
         grow<float>(xs_, P);
         grow<float>(scaled_, P * widest);
+        // split-K sums of the W8A8 prefill GEMM: up to 8 splits of a
+        // hidden-wide output (wider outputs split less or not at all)
+        if (model.activation_bits == 8 && tokens > 4) grow<int32_t>(split_, P * 8 * c.hidden);
         grow<uint32_t>(ids_, P);
         if (host_ids_) (void)hipHostFree(host_ids_);
         hip_check(hipHostMalloc((void**)&host_ids_, P * sizeof(uint32_t)), "hipHostMalloc");
@@ -169,6 +172,8 @@ void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, 
     call.xq_scratch = xq_.as<int8_t>();
     call.xs_scratch = xs_.as<float>();
     call.norm_scratch = normed_.as<float>();
+    call.split_scratch = split_.as<int32_t>();
+    call.split_capacity = split_.bytes / sizeof(int32_t);
     if (l.input_scale) {
         // SmoothQuant input factors (decoder.cpp:1008-1019) before quantization.
         launch_scale_columns(x, tokens, l.view.cols, l.input_scale, scaled_.as<float>(), stream());

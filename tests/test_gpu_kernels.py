@@ -93,6 +93,20 @@ def test_w8a8_prefill_gemm_512_tokens_bit_exact(rt, oracle):
     assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, None, x))
 
 
+@pytest.mark.parametrize("M,K,N", [(300, 5632, 200), (130, 2048, 2560), (512, 2048, 1408), (17, 768, 129)])
+def test_w8a8_tiled_gemm_edges_bit_exact(rt, oracle, M, K, N):
+    # 128 x 128 tiles cut by the token and row counts; K from 768 to 5632
+    rng = np.random.default_rng(M * 31 + N)
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, 8, K)
+    b = rng.standard_normal(N, dtype=np.float32)
+    x = activations(rng, M, K)
+    y, acc = run_int_linear(rt, wq, ws, b, x, 8, K)
+    q, _ = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(8, N, K, K, wq, q))
+    assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, b, x))
+
+
 @pytest.mark.parametrize("bits,group,K,N,M", [(8, 64, 256, 9, 1), (8, 64, 256, 9, 5), (8, 64, 512, 70, 67),
                                               (8, 2, 100, 7, 3), (4, 32, 256, 6, 1), (4, 32, 896, 40, 3),
                                               (4, 896, 896, 40, 1), (8, 100, 100, 7, 1), (4, 2, 64, 3, 2)])
