@@ -671,14 +671,15 @@ __global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const i
 // as 4 x 4 tiles of v_mfma_i32_16x16x64_i8 (operand layout as in
 // gemm_int8_kernel: lane l feeds row l % 16 with K bytes 16 (l / 16) .. +15 of
 // each 64-byte step).  K advances 128 bytes per stage: both 128 x 128 operand
-// tiles go to LDS (rows padded to 144 bytes, so a 16-lane group of operand
-// reads hits every bank once), double-buffered, and the next stage waits in
-// registers while this one feeds the MFMAs.  Two blocks share a CU (70 KB of
-// LDS each), so one block's loads overlap the other's MFMAs.  The integer sums are exact and
-// the epilogue is the CPU path's, so results are bit-identical to it.
+// tiles go to LDS (rows padded to 160 bytes: the hardware counter reads no
+// bank conflicts there, against one per LDS cycle at 144), double-buffered,
+// and the next stage waits in registers while this one feeds the MFMAs.  Two
+// blocks share a CU (80 KB of LDS each), so one block's loads overlap the
+// other's MFMAs.  The integer sums are exact and the epilogue is the CPU
+// path's, so results are bit-identical to it.
 constexpr int kGemmTile = 128;                 // tokens and rows per block
 constexpr int kGemmStage = 128;                // K bytes per stage
-constexpr int kGemmRow = kGemmStage + 16;      // padded LDS row
+constexpr int kGemmRow = kGemmStage + 32;      // padded LDS row (measured free of bank conflicts)
 constexpr int kGemmLoads = kGemmTile * kGemmStage / 16 / kBlock;   // 16-byte loads per thread per operand
 
 __device__ __forceinline__ void gemm_stage_load(const int8_t* xq, const int8_t* W, int K, int tokens, int N, int m0,
@@ -1525,12 +1526,13 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         }
         if (path == 3 && w.group == K && K % kGemmStage == 0) {
             const int tiles = ceil_div(w.rows, kGemmTile) * ceil_div(c.tokens, kGemmTile);
-            const int stages = K / kGemmStage;
+            const int steps = K / 64;
             // Split K until the grid covers the CUs twice (two blocks per CU),
             // each split a whole number of stages, when a workspace is given.
             int splits = 1;
-            while (c.split_scratch && tiles * splits < 512 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 2 &&
-                   (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
+            const int stages = steps / (kGemmStage / 64);
+            while (c.split_scratch && tiles * splits < 512 && stages % (2 * splits) == 0 &&
+                   stages / (2 * splits) >= 2 && (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
                 splits *= 2;
             dim3 grid(ceil_div(w.rows, kGemmTile), ceil_div(c.tokens, kGemmTile), splits);
             int32_t* partial = splits > 1 ? c.split_scratch : nullptr;
