@@ -35,6 +35,7 @@ struct StepLayer {
 struct StepParams {
     int layers = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, rotary = 0, vocab = 0;
     int window = 0, capacity = 0, activation = 0;
+    int item_heads = 1;                 // least query heads per exchange wave in an attention item (1, 2, 4 or 8)
     float epsilon = 0, embedding_scale = 1, attention_scale = 1;
     const StepLayer* layer = nullptr;   // device array [layers]
     WeightView embedding;               // int8 per row or f32

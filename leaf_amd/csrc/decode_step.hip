@@ -62,6 +62,7 @@ constexpr int kWaves = kT / kWave;                           // 8: two per SIMD,
 constexpr int kA = 2;                                        // exchange waves
 constexpr int kAT = kA * kWave;                              // exchange lanes
 constexpr int kB = kWaves - kA;                              // weight waves
+static_assert(kA == 2, "the exchange waves work as a pair");
 constexpr int kKCH = kStepMaxHidden / 16 / kWave;            // 16-byte chunks per lane, hidden-wide int8 row
 constexpr int kKCF = kStepMaxFfn / 16 / kWave;               // ... ffn-wide int8 row
 constexpr int kNH = (kStepMaxHidden + kAT - 1) / kAT;        // hidden values per exchange lane
@@ -88,17 +89,17 @@ struct __align__(16) Shared {
     float h_in[kStepMaxHidden];     // layer input (residual of o_proj)
     float h_mid[kStepMaxHidden];    // after o_proj (residual of down_proj)
     float xf[kStepMaxHidden];       // normalized FP32 input of the head
+    float gamma_in[kNH * kAT];      // gamma of the next input (or final) RMSNorm, as exchange-lane runs
     float k[kStepSpanKeys * kKStride];
     float v[kStepSpanKeys * kStepDim];
     float q[kStepMaxGroup * kStepDim];
     float e[kStepMaxGroup * kStepSpanKeys];
     float sx[2];                    // activation scale per xq buffer
-    float red[2 * kA];              // exchange-wave reductions: [parity][wave]
+    u64 pair[kA][2];                // a_trade words: [wave][sequence parity]
     float best_v[kWaves];
     int best_i[kWaves];
-    int ready;                      // last phase whose input the exchange waves posted
+    int ready[kA];                  // last phase whose input each exchange wave posted
     int published;                  // phase outputs this block's weight waves published (kB per phase)
-    int a_count;                    // exchange-wave barrier arrivals
     int abort;
 };
 
@@ -153,6 +154,12 @@ __device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[8]) {
 }
 __device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[4]) {
     asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+}
+__device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[2]) {
+    asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]));
+}
+__device__ __forceinline__ void all_loaded(const v4f& a, const v4f (&b)[1]) {
+    asm volatile("" ::"v"(a), "v"(b[0]));
 }
 
 __device__ __forceinline__ const StepLayer& layer_at(const Shared& s, int L) {
@@ -310,48 +317,109 @@ __device__ __forceinline__ bool await_one(const u64* p, bool wanted, unsigned ep
     return true;
 }
 
+// Span partials of one query head (span j at base + j * stride words: max,
+// sum, then the dim outputs).  Once they all carry `epoch`: ml = (max, sum)
+// of span `lane` (lanes < spans), os[j] = output element `lane` of span
+// s0 + j (j < spans - s0).  One buffer read takes all of them and repeats
+// until every word is there: only the merge waves (one per query head) poll
+// this way, and a full re-read costs less than watching a single word first,
+// which adds a round trip.  Words of spans past the last are read from the
+// last span and ignored.
+template <int NB>
+__device__ __forceinline__ bool await_partials(const u64* base, int stride, int spans, int s0, int lane,
+                                               unsigned epoch, v2f& ml, float (&os)[NB], const StepParams& P) {
+    const __amdgpu_buffer_rsrc_t view = exchange_view(base);
+    const int own = min(lane, spans - 1);
+    unsigned spin = 0;
+    for (;;) {
+        asm volatile("" ::: "memory");
+        const v4u m = __builtin_amdgcn_raw_buffer_load_b128(view, 8 * own * stride, 0, kLoadSc1);
+        u64 w[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(view, 8 * (2 + lane),
+                                                              8 * stride * min(s0 + j, spans - 1), kLoadSc1);
+            w[j] = (u64(v.y) << 32) | v.x;
+        }
+        bool ready = lane >= spans || (m.y == epoch && m.w == epoch);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) ready = ready && (s0 + j >= spans || unsigned(w[j] >> 32) == epoch);
+        if (__all(ready)) {
+            ml = v2f{__uint_as_float(m.x), __uint_as_float(m.z)};
+#pragma unroll
+            for (int j = 0; j < NB; ++j) os[j] = __uint_as_float(unsigned(w[j]));
+            return true;
+        }
+        if (++spin >= kSpinLimit || ((spin & 255u) == 255u && aborted(P.abort_flag))) {
+            raise_abort(P);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // ------------------------------------------------------ exchange waves ---
-// Barrier of the exchange waves (an LDS arrival counter).  Returns false
-// when the kernel is being abandoned.
-__device__ __forceinline__ bool a_sync(Shared& s, int& round) {
+// The two exchange waves trade one value: each posts it, tagged with the
+// call's sequence number, in its own LDS word and reads the other's.  A wave
+// that arrives first waits only for that word (no shared counter, no
+// arrival count to poll), and both combine the two values themselves.  Each
+// wave's earlier LDS writes are complete before its word is posted, so this
+// is also the pair's barrier.  Returns false (abort flag raised in LDS) on
+// timeout or when the block is being abandoned.
+__device__ __forceinline__ bool a_trade(float mine, float& theirs, Shared& s, int& round) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    ++round;
     lds_done();
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&s.a_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    round += kA;
-    for (unsigned spin = 0; lds_load(&s.a_count) < round; ++spin) {
-        if (spin > kSpinLimit) return false;
+    if ((threadIdx.x & 63) == 0)
+        __hip_atomic_store(&s.pair[w][round & 1], tagged(unsigned(round), mine), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    const u64* other = &s.pair[w ^ 1][round & 1];
+    for (unsigned spin = 0;; ++spin) {
+        const u64 v = __hip_atomic_load(other, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (unsigned(v >> 32) == unsigned(round)) {
+            theirs = __uint_as_float(unsigned(v));
+            break;
+        }
+        if (spin > kSpinLimit || lds_load(&s.abort)) {
+            lds_store(&s.abort, 1);
+            return false;
+        }
         __builtin_amdgcn_s_sleep(0);
     }
     asm volatile("" ::: "memory");
     return true;
 }
 
-// The exchange waves agree on `ok`; false means all of them leave the kernel.
-__device__ __forceinline__ bool a_agree(bool ok, Shared& s, int& round) {
-    if (!__all(ok) && (threadIdx.x & 63) == 0) lds_store(&s.abort, 1);
-    if (!a_sync(s, round)) return false;
-    return lds_load(&s.abort) == 0;
+__device__ __forceinline__ bool a_sync(Shared& s, int& round) {
+    float unused;
+    return a_trade(0.0f, unused, s, round);
 }
 
-// Sums (or maxes) over the exchange lanes; every exchange wave gets the same bits.
-__device__ __forceinline__ float a_sum(float v, Shared& s, int& round, int& parity) {
-    v = dpp_sum_f32(v);
-    if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
-    a_sync(s, round);
-    float r = s.red[kA * parity];
-#pragma unroll
-    for (int w = 1; w < kA; ++w) r += s.red[kA * parity + w];
-    parity ^= 1;
-    return r;
+// Every exchange wave has `ok`; otherwise this wave leaves the kernel with the
+// block's abort flag raised (the other exchange wave and the weight waves see
+// it in their next wait, other blocks see the device flag).
+__device__ __forceinline__ bool a_check(bool ok, Shared& s, const StepParams& P) {
+    if (__all(ok)) return true;
+    lds_store(&s.abort, 1);
+    raise_abort(P);
+    return false;
 }
-__device__ __forceinline__ float a_max(float v, Shared& s, int& round, int& parity) {
+
+// Sums (or maxes) over the exchange lanes; both exchange waves get the same
+// bits (IEEE addition and fmaxf are commutative).
+__device__ __forceinline__ bool a_sum(float& v, Shared& s, int& round) {
+    v = dpp_sum_f32(v);
+    float other;
+    if (!a_trade(v, other, s, round)) return false;
+    v += other;
+    return true;
+}
+__device__ __forceinline__ bool a_max(float& v, Shared& s, int& round) {
     v = dpp_max_f32(v);
-    if ((threadIdx.x & 63) == 0) s.red[kA * parity + (threadIdx.x >> 6)] = v;
-    a_sync(s, round);
-    float r = s.red[kA * parity];
-#pragma unroll
-    for (int w = 1; w < kA; ++w) r = fmaxf(r, s.red[kA * parity + w]);
-    parity ^= 1;
-    return r;
+    float other;
+    if (!a_trade(v, other, s, round)) return false;
+    v = fmaxf(v, other);
+    return true;
 }
 
 // Waits until this block's weight waves issued their stores of `phases`
@@ -367,37 +435,38 @@ __device__ __forceinline__ bool wait_published(Shared& s, int phases) {
     return true;
 }
 
-// Posts phase `phase`: every exchange wave has finished writing its input.
-__device__ __forceinline__ void post(Shared& s, int phase, int& round) {
-    a_sync(s, round);
-    if (threadIdx.x == 0) lds_store(&s.ready, phase);
+// Posts phase `phase` for this exchange wave: it has finished writing its
+// part of the phase's input.  The weight waves start once both posted.
+__device__ __forceinline__ void post(Shared& s, int phase) {
+    lds_done();
+    if ((threadIdx.x & 63) == 0) lds_store(&s.ready[threadIdx.x >> 6], phase);
 }
 
 // RMSNorm of the n values held as runs (decoder.cpp:706-727).
 template <int N>
-__device__ __forceinline__ void rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
-                                              Shared& s, int& round, int& parity) {
+__device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
+                                              Shared& s, int& round) {
     const int live = n / kRun - a;
     float sq = 0.0f;
 #pragma unroll
     for (int i = 0; i < N; ++i) sq += (i / kRun) * kAT < live ? x[i] * x[i] : 0.0f;
-    sq = a_sum(sq, s, round, parity);
+    if (!a_sum(sq, s, round)) return false;
     const float scale = 1.0f / sqrtf(sq / (float)n + eps);
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
+    return true;
 }
 
 // Per-token symmetric int8 quantization into s.xq[buf] (decoder.cpp:1028-1043).
 // Runs past n land in the buffer's tail, which no reader uses.
 template <int N>
-__device__ __forceinline__ void quantize_into(const float (&x)[N], int n, int buf, int a, Shared& s, int& round,
-                                              int& parity) {
+__device__ __forceinline__ bool quantize_into(const float (&x)[N], int n, int buf, int a, Shared& s, int& round) {
     static_assert(N % kRun == 0 && kRun == 2, "runs of two");
     const int live = n / kRun - a;
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / kRun) * kAT < live ? fabsf(x[i]) : 0.0f);
-    amax = a_max(amax, s, round, parity);
+    if (!a_max(amax, s, round)) return false;
     const float sx = fmaxf(amax / 127.0f, 1e-12f);
     const float multiplier = 1.0f / sx;
 #pragma unroll
@@ -407,6 +476,7 @@ __device__ __forceinline__ void quantize_into(const float (&x)[N], int n, int bu
             (uint16_t)((quantize_one(v[0], multiplier) & 255) | ((quantize_one(v[1], multiplier) & 255) << 8));
     }
     if (a == 0) s.sx[buf] = sx;
+    return true;
 }
 
 // This lane's runs into dst (natural element order; dst holds kAT * N floats).
@@ -416,6 +486,18 @@ __device__ __forceinline__ void store_runs(float* dst, const float (&x)[N], int 
 #pragma unroll
     for (int g = 0; g < N / kRun; ++g)
         *reinterpret_cast<v2f*>(dst + kRun * run_of(g, a)) = v2f{x[kRun * g], x[kRun * g + 1]};
+}
+
+// This lane's runs out of src (natural element order), as store_runs wrote them.
+template <int N>
+__device__ __forceinline__ void load_runs(float (&x)[N], const float* src, int a) {
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g) {
+        const v2f v = *reinterpret_cast<const v2f*>(src + kRun * run_of(g, a));
+        x[kRun * g] = v[0];
+        x[kRun * g + 1] = v[1];
+    }
 }
 
 // gamma for this lane's runs; runs past n read the last one (their x are 0).
@@ -519,7 +601,7 @@ __device__ __forceinline__ void note_published(Shared& s) {
 // Waits (weight waves) until the exchange waves posted `phase`.
 __device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
     for (unsigned spin = 0;; ++spin) {
-        if (lds_load(&s.ready) >= phase) break;
+        if (min(lds_load(&s.ready[0]), lds_load(&s.ready[1])) >= phase) break;
         if (lds_load(&s.abort) || spin > 64 * kSpinLimit) return false;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -557,27 +639,29 @@ struct Ownership {
 };
 
 // Attention over this block's span of keys (K rows in s.k, V rows in s.v,
-// q of the group's heads in s.q) for the wave's query heads aw, aw + kA, ...
-// (HPW of them; heads past the group repeat the last one, branch-free, so all
-// heads' LDS reads overlap).  Publishes per head: max score, sum of
+// q of the group's heads in s.q) for the wave's query heads h0 + aw,
+// h0 + aw + kA, ... below h_end (HPW of them; heads past h_end repeat the
+// last one, branch-free, so all heads' LDS reads overlap).  Fewer heads per
+// wave leave registers for more LDS reads in flight: the loops are unrolled
+// 8 / HPW times.  Publishes per head: max score, sum of
 // exp(score - max), and the unnormalized output sum_k exp(s_k - max) v_k.
 // Every staged row is finite: rows past the span hold key 0's values and get
 // weight 0.
 template <int HPW>
-__device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, int lane, int aw, int group, int keys,
-                                               u64* parts, unsigned epoch) {
+__device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, int lane, int aw, int h0, int h_end,
+                                               int keys, u64* parts, unsigned epoch) {
     constexpr int dim = kStepDim;
     // scores: lane = key, four dims of its K row at a time
     float sum[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) sum[h] = 0.0f;
-#pragma unroll 2
+#pragma unroll(8 / HPW)
     for (int d4 = 0; d4 < dim / 4; ++d4) {
         const v4f kv = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
         v4f qv[HPW];
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
-            qv[h] = *reinterpret_cast<const v4f*>(s.q + min(aw + kA * h, group - 1) * dim + 4 * d4);
+            qv[h] = *reinterpret_cast<const v4f*>(s.q + min(h0 + aw + kA * h, h_end - 1) * dim + 4 * d4);
         all_loaded(kv, qv);
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
@@ -587,10 +671,10 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
     float m[HPW], l[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
-        const int gh = aw + kA * h;
+        const int gh = h0 + aw + kA * h;
         m[h] = -INFINITY;
         l[h] = 0.0f;
-        if (gh < group) {
+        if (gh < h_end) {
             const float sc = lane < keys ? sum[h] * P.attention_scale * P.attention_scale : -INFINITY;
             m[h] = dpp_max_f32(sc);
             const float e = lane < keys ? expf(sc - m[h]) : 0.0f;
@@ -604,7 +688,7 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
 #pragma unroll
     for (int h = 0; h < HPW; ++h) o[h] = 0.0f;
     const int keys4 = (keys + 3) & ~3;
-#pragma unroll 2
+#pragma unroll(8 / HPW)
     for (int kk = 0; kk < keys4; kk += 4) {
         v4f v;
 #pragma unroll
@@ -612,7 +696,7 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
         v4f e4[HPW];
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
-            e4[h] = *reinterpret_cast<const v4f*>(s.e + min(aw + kA * h, group - 1) * kStepSpanKeys + kk);
+            e4[h] = *reinterpret_cast<const v4f*>(s.e + min(h0 + aw + kA * h, h_end - 1) * kStepSpanKeys + kk);
         all_loaded(v, e4);
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
@@ -621,8 +705,8 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
     }
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
-        const int gh = aw + kA * h;
-        if (gh < group) {
+        const int gh = h0 + aw + kA * h;
+        if (gh < h_end) {
             u64* part = parts + (size_t)gh * (dim + 2);
             publish(part + 2 + lane, epoch, o[h]);
             if (lane == 0) {
@@ -642,15 +726,22 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     const int qw = P.heads * dim, kvw = P.kv_heads * dim;
     const int group = P.heads / P.kv_heads;
     const int pos = P.position;
-    int round = 0, parity = 0;
+    int round = 0;
     auto epoch = [&](int layer, int phase) { return P.epoch + (unsigned)(layer * 8 + phase); };
 
-    // this block's attention item: (KV head, span of keys)
+    // this block's attention item: (KV head, span of keys, slice of the
+    // group's query heads).  Slices are as narrow as the grid allows (hpw
+    // heads per exchange wave): an item's time grows with its heads.
     const int end = pos + 1;
     const int begin = (P.window > 0 && end > P.window) ? end - P.window : 0;
     const int spans = (end - begin + kStepSpanKeys - 1) / kStepSpanKeys;
-    const bool has_item = b < P.kv_heads * spans;
-    const int item_g = has_item ? b / spans : 0, item_s = has_item ? b % spans : 0;
+    int hpw = 1;
+    while (hpw < kHeadsA && hpw < P.item_heads) hpw *= 2;
+    while (hpw < kHeadsA && P.kv_heads * spans * ((group + kA * hpw - 1) / (kA * hpw)) > G) hpw *= 2;
+    const int slices = (group + kA * hpw - 1) / (kA * hpw);
+    const bool has_item = b < P.kv_heads * spans * slices;
+    const int item_g = has_item ? b / (spans * slices) : 0, item_s = has_item ? b / slices % spans : 0;
+    const int item_h0 = has_item ? b % slices * kA * hpw : 0, item_h1 = min(group, item_h0 + kA * hpw);
     const int k0 = begin + item_s * kStepSpanKeys, k1 = min(end, k0 + kStepSpanKeys);
     const int cached_end = min(k1, pos), keys = k1 - k0;
     const bool new_key = pos >= k0 && pos < k1;
@@ -658,6 +749,14 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     const bool merge_block = (G - 1 - b) * kA < P.heads;
 
     float x[kNH];
+    {
+        // The input norm's gamma waits in LDS (each lane reads back its own
+        // runs): a cold read of it after the layer input lands would add a
+        // memory round trip to every layer.
+        float gamma[kNH];
+        fetch_gamma(gamma, layer_at(s, 0).input_gamma, H, a);
+        store_runs(s.gamma_in, gamma, a);
+    }
     {
         const uint32_t id = ldg(P.token);
 #pragma unroll
@@ -676,7 +775,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         const float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
         const float* Vc = Kc + (size_t)P.kv_heads * P.capacity * dim;
         float gamma[kNH];
-        fetch_gamma(gamma, Ly.input_gamma, H, a);
+        load_runs(gamma, s.gamma_in, a);
 
         // ---- layer input (x, polled at the end of the previous layer) -> RMSNorm -> int8 for q|k|v
         stamp(P.trace, b, 64 * L + 1);
@@ -693,9 +792,8 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
         }
         store_runs(s.h_in, x, a);
-        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
-        quantize_into(x, H, 0, a, s, round, parity);
-        post(s, 4 * L + 0, round);
+        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        post(s, 4 * L + 0);
         stamp(P.trace, b, 64 * L + 2);
         if (has_item) {
             // the cached keys and values, loaded during the norm, into LDS
@@ -721,7 +819,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             const bool ok_q = wait_published(s, 4 * L + 1) &&
                               await_runs<kNQ - 1, 0, false>(P.x_qkv + q_base, group * dim, epoch(L, 1), got, a, P);
             const bool ok_kv = ok_q && await_one(P.x_qkv + kv_word, has_kv, epoch(L, 1), kv_got, P);
-            if (!a_agree(ok_kv, s, round)) return false;
+            if (!a_check(ok_kv, s, P)) return false;
             stamp(P.trace, b, 64 * L + 3);
             store_runs(s.q, got, a);
             if (has_kv) {
@@ -733,8 +831,10 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             stamp(P.trace, b, 64 * L + 56);
             if (P.trace && threadIdx.x == 0) stg(P.trace + (size_t)b * kStepTracePoints + 64 * L + 61, (unsigned long long)__builtin_amdgcn_s_memtime());
             u64* parts = P.x_part + (size_t)(item_g * spans + item_s) * group * (dim + 2);
-            if (group <= 4 * kA) attention_item<4>(P, s, lane, aw, group, keys, parts, epoch(L, 2));
-            else attention_item<kHeadsA>(P, s, lane, aw, group, keys, parts, epoch(L, 2));
+            if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
+            else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
+            else if (hpw == 4) attention_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
+            else attention_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
             stamp(P.trace, b, 64 * L + 57);
         }
         if (merge_block) {
@@ -746,22 +846,18 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
                 const int g = mh / group, gh = mh % group;
                 const size_t stride = (size_t)group * (dim + 2);
                 const u64* base = P.x_part + ((size_t)g * spans * group + gh) * (dim + 2);
-                // wait for every span's (max, sum) pair (lane s: span s),
-                // then read the outputs kMergeBatch spans per round trip
-                float ml[2];
-                unsigned spin = 0;
-                if (lane < spans) ok = spin_until(base + lane * stride + 1, epoch(L, 2), spin, P);
-                auto ml_index = [&](int i) { return lane < spans ? (int)(lane * stride) + i : -1; };
-                ok = __all(ok) && await(base, ml_index, epoch(L, 2), ml, P);
+                // One read takes every (max, sum) pair and the first
+                // kMergeBatch spans' outputs; later batches are read as needed.
+                v2f ml;
+                float os[kMergeBatch];
+                ok = await_partials(base, (int)stride, spans, 0, lane, epoch(L, 2), ml, os, P);
                 const float ms = lane < spans ? ml[0] : -INFINITY;
                 const float mx = dpp_max_f32(ms);
                 const float weight = lane < spans ? expf(ms - mx) : 0.0f;
                 const float total = dpp_sum_f32(lane < spans ? ml[1] * weight : 0.0f);
                 float acc = 0.0f;
                 for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
-                    float os[kMergeBatch];
-                    auto o_index = [&](int j) { return s0 + j < spans ? (int)((s0 + j) * stride + 2 + lane) : -1; };
-                    ok = await(base, o_index, epoch(L, 2), os, P);
+                    if (s0 > 0) ok = await_partials(base, (int)stride, spans, s0, lane, epoch(L, 2), ml, os, P);
 #pragma unroll
                     for (int j = 0; j < kMergeBatch; ++j) {
                         const float wj = __builtin_bit_cast(
@@ -771,7 +867,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
                 }
                 if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), total > 0.0f ? acc / total : 0.0f);
             }
-            if (!a_agree(ok, s, round)) return false;
+            if (!a_check(ok, s, P)) return false;
             stamp(P.trace, b, 64 * L + 60);
         }
         stamp(P.trace, b, 64 * L + 4);
@@ -779,21 +875,25 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // ---- attention output -> int8 for o_proj
         {
             float xa[kNH];
-            if (!a_agree(await_runs<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, round)) return false;
+            if (!a_check(await_runs<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, P)) return false;
             stamp(P.trace, b, 64 * L + 5);
-            quantize_into(xa, qw, 1, a, s, round, parity);
-            post(s, 4 * L + 1, round);
+            if (!quantize_into(xa, qw, 1, a, s, round)) return false;
+            post(s, 4 * L + 1);
         }
         // ---- after o_proj -> RMSNorm -> int8 for gate|up
         fetch_gamma(gamma, Ly.post_gamma, H, a);
-        if (!a_agree(wait_published(s, 4 * L + 2) && await_runs<kNH, 0, false>(P.x_mid, H, epoch(L, 4), x, a, P), s,
-                     round))
-            return false;
+        {
+            // the next norm's gamma (the next layer's input norm, or the final one)
+            float next[kNH];
+            fetch_gamma(next, L + 1 < P.layers ? layer_at(s, L + 1).input_gamma : P.final_gamma, H, a);
+            if (!a_check(wait_published(s, 4 * L + 2) && await_runs<kNH, 0, false>(P.x_mid, H, epoch(L, 4), x, a, P), s, P))
+                return false;
+            store_runs(s.gamma_in, next, a);
+        }
         stamp(P.trace, b, 64 * L + 6);
         store_runs(s.h_mid, x, a);
-        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
-        quantize_into(x, H, 0, a, s, round, parity);
-        post(s, 4 * L + 2, round);
+        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        post(s, 4 * L + 2);
         // ---- SiLU-gated activation -> int8 for down_proj
         {
             float xd[kNF];
@@ -801,32 +901,30 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             stamp(P.trace, b, 64 * L + 61);
             ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
             stamp(P.trace, b, 64 * L + 62);
-            if (!a_agree(ok, s, round)) return false;
+            if (!a_check(ok, s, P)) return false;
             stamp(P.trace, b, 64 * L + 7);
-            quantize_into(xd, F, 1, a, s, round, parity);
-            post(s, 4 * L + 3, round);
+            if (!quantize_into(xd, F, 1, a, s, round)) return false;
+            post(s, 4 * L + 3);
         }
         // ---- the next layer's input (the last layer's feeds the head below)
         if (L + 1 < P.layers) {
             stamp(P.trace, b, 64 * (L + 1) + 0);
-            if (!a_agree(wait_published(s, 4 * L + 4) && await_runs<kNH, 0, false>(P.x_hidden, H, epoch(L, 6), x, a, P),
-                         s, round))
+            if (!a_check(wait_published(s, 4 * L + 4) && await_runs<kNH, 0, false>(P.x_hidden, H, epoch(L, 6), x, a, P), s, P))
                 return false;
         }
     }
     // ---- final RMSNorm -> FP32 input of the head
     {
         float gamma[kNH];
-        fetch_gamma(gamma, P.final_gamma, H, a);
+        load_runs(gamma, s.gamma_in, a);
         stamp(P.trace, b, 64 * P.layers + 0);
-        if (!a_agree(wait_published(s, 4 * P.layers) &&
-                         await_runs<kNH, 0, false>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P),
-                     s, round))
+        if (!a_check(wait_published(s, 4 * P.layers) &&
+                         await_runs<kNH, 0, false>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, P))
             return false;
         stamp(P.trace, b, 64 * P.layers + 1);
-        rms_normalize(x, H, gamma, P.epsilon, a, s, round, parity);
+        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round)) return false;
         store_runs(s.xf, x, a);
-        post(s, 4 * P.layers, round);
+        post(s, 4 * P.layers);
     }
     return true;
 }
@@ -1026,10 +1124,10 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     const int G = gridDim.x, b = blockIdx.x;
     const int H = P.hidden;
     if (t == 0) {
-        s.ready = -1;
+        s.ready[0] = s.ready[1] = -1;
         s.published = 0;
-        s.a_count = 0;
         s.abort = 0;
+        s.pair[0][0] = s.pair[0][1] = s.pair[1][0] = s.pair[1][1] = 0;
     }
     {
         const int words = P.layers * (int)(sizeof(StepLayer) / 16);
@@ -1039,8 +1137,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     }
     __syncthreads();
     const bool ok = wave < kA ? exchange_role(P, s) : weight_role(P, s);
-    if (!ok) return;                            // both roles leave together (abort flag in LDS)
-    __syncthreads();
+    if (__syncthreads_or(!ok)) return;          // every wave leaves when one gave up (abort flags raised)
 
     // ---------------- FP32 LM head and greedy argmax (all waves)
     const int V = P.vocab;

@@ -393,6 +393,9 @@ void Session::step_prepare() {
     step_bytes_ = bytes;
     step_kv_bytes_ = 2.0 * 4.0 * c.layers * c.kv_heads * c.head_dim;
     step_blocks_ = blocks;
+    // LEAF_DECODE_STEP_ITEM_HEADS=<n>: at least n query heads per exchange
+    // wave in each attention item (wider items, fewer blocks; for tests).
+    if (const char* heads = std::getenv("LEAF_DECODE_STEP_ITEM_HEADS")) p.item_heads = std::max(1, std::atoi(heads));
     // LEAF_DECODE_STEP_TRACE=<file>: append every step's phase timeline
     // (blocks x kStepTracePoints u64 stamps of the 100 MHz device clock).
     if (const char* trace = std::getenv("LEAF_DECODE_STEP_TRACE")) {

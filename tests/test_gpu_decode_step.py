@@ -116,6 +116,16 @@ def test_step_matches_oracle_across_span_boundaries(rt, oracle, small):
     assert profile.get("decode_step", {}).get("launches") == 80, profile
 
 
+@pytest.mark.parametrize("item_heads", [2, 4, 8])
+def test_step_with_wider_attention_items(rt, oracle, small, monkeypatch, item_heads):
+    # Long contexts give each attention item more query heads (fewer, wider
+    # items when heads x spans outgrow the grid); forced here at a short one.
+    monkeypatch.setenv("LEAF_DECODE_STEP_ITEM_HEADS", str(item_heads))
+    worst, _, profile = run_steps(rt, oracle, small, 70, 30, seed=6)
+    assert worst <= W8A8_LOGIT_TOLERANCE
+    assert profile.get("decode_step", {}).get("launches") == 30, profile
+
+
 def test_step_at_full_tinyllama_width(rt, oracle, wide):
     worst, _, profile = run_steps(rt, oracle, wide, 300, 12, seed=4)
     print(f"decode step (2048/5632/32:4): worst relative logit error {worst:.2e}")
