@@ -18,8 +18,13 @@ Beside it:
                 >= 1 GiB of weight copies so the 256 MiB MALL cannot serve them;
   cpu_baseline  the reference CPU engine (oracle/_ref/leaf_decoder, built from the
                 reference sources) on this host, on a bounded sample.
+  traffic       HBM bytes per launch of the dominant kernel from two rocprofv3
+                counter passes (FETCH_SIZE, WRITE_SIZE), each scaled by what the
+                same counter reads for a copy of known size (leaf_amd/bin/hbm_copy);
+                derived once with --derive-traffic and kept in profiles/.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py --derive-traffic DIR   # DIR holds the four counter runs (see profiles/)
 """
 from __future__ import annotations
 
@@ -38,6 +43,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, datasheet
+TRAFFIC_FILE = ROOT / "profiles" / "decode_step_tinyllama_w8a8_traffic.json"
+COPY_BYTES = 1 << 30           # hbm_copy 1024: reads and writes this many bytes per launch
 PROMPT_TOKENS = 512
 SEED = 20261201
 METRIC = "decode tok/s + GEMV HBM GB/s (% peak), TinyLlama-shape W8A8, batch 1"
@@ -177,6 +184,37 @@ def cpu_baseline(path: Path, budget_s: float = 30.0) -> dict | None:
             "sample": f"oracle decoder, 16-token prompt + {steps} decode steps"}
 
 
+def _counter_means(csv_path: Path) -> dict:
+    """Mean counter value (KiB) per kernel name in one rocprofv3 counter_collection.csv."""
+    import csv
+    sums: dict = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            total, count = sums.get(row["Kernel_Name"], (0.0, 0))
+            sums[row["Kernel_Name"]] = (total + float(row["Counter_Value"]), count + 1)
+    return {name: total / count for name, (total, count) in sums.items()}
+
+
+def derive_traffic(base: Path, kernel: str = "decode_step_kernel") -> dict:
+    """HBM bytes per launch of `kernel` from rocprofv3 --pmc runs under `base`:
+    pmc_copy_{FETCH,WRITE}_SIZE (hbm_copy 1024 5) and pmc_step_{FETCH,WRITE}_SIZE
+    (the leaf_decoder generation).  Each counter is scaled by the bytes a copy of
+    COPY_BYTES moves per unit of that counter."""
+    out = {"kernel": kernel}
+    total = 0.0
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copy = _counter_means(next((base / f"pmc_copy_{counter}").glob("*counter_collection.csv")))
+        copy_kib = next(v for k, v in copy.items() if "hbm_copy_kernel" in k)
+        scale = COPY_BYTES / copy_kib                    # bytes per counted KiB
+        step = _counter_means(next((base / f"pmc_step_{counter}").glob("*counter_collection.csv")))
+        step_kib = next(v for k, v in step.items() if kernel in k)
+        out[counter] = {"kib_per_launch": round(step_kib, 1), "copy_kib": round(copy_kib, 1),
+                        "bytes_per_kib": round(scale, 3), "bytes": round(step_kib * scale)}
+        total += step_kib * scale
+    out["bytes_per_launch"] = round(total)
+    return out
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -184,7 +222,13 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemv", action="store_true")
+    parser.add_argument("--derive-traffic", type=Path, default=None)
     args = parser.parse_args()
+    if args.derive_traffic is not None:
+        traffic = derive_traffic(args.derive_traffic)
+        TRAFFIC_FILE.write_text(json.dumps(traffic, indent=1) + "\n")
+        print(json.dumps(traffic))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
@@ -206,6 +250,9 @@ def main() -> int:
     avg_ms = g["ms"] / launches
     bytes_per_launch = g["bytes"] / launches
     achieved = bytes_per_launch / avg_ms / 1e6 if avg_ms > 0 else 0.0
+    traffic = None
+    if TRAFFIC_FILE.exists() and "decode_step" in kernel:
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
     gemv = None
     if not args.no_gemv:
         log("GEMV microbenchmark ...")
@@ -226,7 +273,7 @@ def main() -> int:
                    "prefill_ms": round(d["prefill_ms"], 2)},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(bytes_per_launch),
                      "launches": g["launches"]},
         "device_ms_per_step": device_ms,

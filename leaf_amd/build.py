@@ -1,4 +1,4 @@
-"""Build libleafhip.so (and the leaf_decoder executable) for gfx950 with hipcc.
+"""Build libleafhip.so (and the leaf_decoder and hbm_copy executables) for gfx950 with hipcc.
 
     python -m leaf_amd.build            # compile everything in-tree
 
@@ -69,6 +69,15 @@ def build(verbose: bool = False) -> Path:
         if result.returncode != 0:
             raise RuntimeError(f"building leaf_decoder failed:\n{result.stderr}")
         exe_tmp.replace(EXECUTABLE)
+    if (CSRC / "hbm_copy.hip").exists():
+        # the copy of known size that calibrates the profiler's byte counters
+        probe = PACKAGE / "bin" / "hbm_copy"
+        probe.parent.mkdir(exist_ok=True)
+        cmd = [hipcc(), *HIPFLAGS, str(CSRC / "hbm_copy.hip"), "-o", str(probe.with_suffix(".tmp"))]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"building hbm_copy failed:\n{result.stderr}")
+        probe.with_suffix(".tmp").replace(probe)
     if verbose:
         print(f"built {LIBRARY}")
     return LIBRARY
