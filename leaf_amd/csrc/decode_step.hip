@@ -374,17 +374,19 @@ __device__ __forceinline__ bool a_trade(float mine, float& theirs, Shared& s, in
         __hip_atomic_store(&s.pair[w][round & 1], tagged(unsigned(round), mine), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
     const u64* other = &s.pair[w ^ 1][round & 1];
+    // A tight poll (one LDS round trip per try): the other wave usually
+    // posts within a few hundred cycles.  The abort flag is checked every
+    // 64 tries only.
     for (unsigned spin = 0;; ++spin) {
         const u64 v = __hip_atomic_load(other, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (unsigned(v >> 32) == unsigned(round)) {
             theirs = __uint_as_float(unsigned(v));
             break;
         }
-        if (spin > kSpinLimit || lds_load(&s.abort)) {
+        if ((spin & 63u) == 63u && (spin > 16 * kSpinLimit || lds_load(&s.abort))) {
             lds_store(&s.abort, 1);
             return false;
         }
-        __builtin_amdgcn_s_sleep(0);
     }
     asm volatile("" ::: "memory");
     return true;
@@ -611,9 +613,10 @@ __device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
 
 // Phase timeline: the first thread of each role stamps the 100 MHz device
 // clock at phase boundaries into trace[block][point]: points 64 * layer + k
-// (k < 8 exchange waves, 8 + 8 * w + j weight wave w, 56-62 inside attention
-// and the ffn-vector read), then the head's.  Off (null)
-// outside diagnostics.
+// (k < 8 exchange wave 0, 8 + 8 * w + j weight wave w, 56, 57, 60 inside
+// attention, 58, 59, 61, 63 exchange wave 1's arrivals of x_attn, x_mid,
+// the layer input and x_act), then the head's.  Off (null) outside
+// diagnostics.
 __device__ __forceinline__ void stamp(unsigned long long* trace, int block, int point, int thread = 0) {
     if (trace && threadIdx.x == thread)
         stg(trace + (size_t)block * kStepTracePoints + point, (unsigned long long)__builtin_amdgcn_s_memrealtime());
@@ -779,6 +782,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
 
         // ---- layer input (x, polled at the end of the previous layer) -> RMSNorm -> int8 for q|k|v
         stamp(P.trace, b, 64 * L + 1);
+        stamp(P.trace, b, 64 * L + 61, kWave);
         // cached keys and values of this block's span (rows past the cached
         // ones load key 0 again; they are overwritten or never read)
         v4u kv_pre[2 * kNK] = {};
@@ -829,7 +833,6 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
             if (!a_sync(s, round)) return false;
             stamp(P.trace, b, 64 * L + 56);
-            if (P.trace && threadIdx.x == 0) stg(P.trace + (size_t)b * kStepTracePoints + 64 * L + 61, (unsigned long long)__builtin_amdgcn_s_memtime());
             u64* parts = P.x_part + (size_t)(item_g * spans + item_s) * group * (dim + 2);
             if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
             else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
@@ -877,6 +880,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             float xa[kNH];
             if (!a_check(await_runs<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, P)) return false;
             stamp(P.trace, b, 64 * L + 5);
+            stamp(P.trace, b, 64 * L + 58, kWave);
             if (!quantize_into(xa, qw, 1, a, s, round)) return false;
             post(s, 4 * L + 1);
         }
@@ -891,6 +895,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             store_runs(s.gamma_in, next, a);
         }
         stamp(P.trace, b, 64 * L + 6);
+        stamp(P.trace, b, 64 * L + 59, kWave);
         store_runs(s.h_mid, x, a);
         if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
         post(s, 4 * L + 2);
@@ -898,9 +903,8 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         {
             float xd[kNF];
             bool ok = wait_published(s, 4 * L + 3);
-            stamp(P.trace, b, 64 * L + 61);
             ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
-            stamp(P.trace, b, 64 * L + 62);
+            stamp(P.trace, b, 64 * L + 63, kWave);
             if (!a_check(ok, s, P)) return false;
             stamp(P.trace, b, 64 * L + 7);
             if (!quantize_into(xd, F, 1, a, s, round)) return false;
