@@ -99,6 +99,7 @@ struct __align__(16) Shared {
     float best_v[kWaves];
     int best_i[kWaves];
     int ready[kA];                  // last phase whose input each exchange wave posted
+    int received[kA];               // last phase whose input vector each exchange wave has read
     int published;                  // phase outputs this block's weight waves published (kB per phase)
     int abort;
 };
@@ -437,6 +438,11 @@ __device__ __forceinline__ bool wait_published(Shared& s, int phases) {
     return true;
 }
 
+// Notes that this exchange wave has read the input vector of `phase`.
+__device__ __forceinline__ void note_received(Shared& s, int phase) {
+    if ((threadIdx.x & 63) == 0) lds_store(&s.received[threadIdx.x >> 6], phase);
+}
+
 // Posts phase `phase` for this exchange wave: it has finished writing its
 // part of the phase's input.  The weight waves start once both posted.
 __device__ __forceinline__ void post(Shared& s, int phase) {
@@ -600,16 +606,23 @@ __device__ __forceinline__ void note_published(Shared& s) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&s.published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Waits (weight waves) until the exchange waves posted `phase`.
-__device__ __forceinline__ bool wait_ready(Shared& s, int phase) {
+// Waits (weight waves) until both exchange waves' flags reach `phase`.
+__device__ __forceinline__ bool wait_flags(Shared& s, const int (&flag)[kA], int phase) {
     for (unsigned spin = 0;; ++spin) {
-        if (min(lds_load(&s.ready[0]), lds_load(&s.ready[1])) >= phase) break;
+        if (min(lds_load(&flag[0]), lds_load(&flag[1])) >= phase) break;
         if (lds_load(&s.abort) || spin > 64 * kSpinLimit) return false;
         __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
     return true;
 }
+// ... until the exchange waves posted the int8 input of `phase`.
+__device__ __forceinline__ bool wait_ready(Shared& s, int phase) { return wait_flags(s, s.ready, phase); }
+// ... until they have read the input vector of `phase` (its hop is over).
+// The weight waves issue a phase's next-layer loads only then: a burst of
+// weight loads in flight slows the exchange reads of a hop down, while the
+// norm and quantization that follow the hop need no memory.
+__device__ __forceinline__ bool wait_received(Shared& s, int phase) { return wait_flags(s, s.received, phase); }
 
 // Phase timeline: the first thread of each role stamps the 100 MHz device
 // clock at phase boundaries into trace[block][point]: points 64 * layer + k
@@ -879,6 +892,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         {
             float xa[kNH];
             if (!a_check(await_runs<kNH>(P.x_attn, qw, epoch(L, 3), xa, a, P), s, P)) return false;
+            note_received(s, 4 * L + 1);
             stamp(P.trace, b, 64 * L + 5);
             stamp(P.trace, b, 64 * L + 58, kWave);
             if (!quantize_into(xa, qw, 1, a, s, round)) return false;
@@ -892,6 +906,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             fetch_gamma(next, L + 1 < P.layers ? layer_at(s, L + 1).input_gamma : P.final_gamma, H, a);
             if (!a_check(wait_published(s, 4 * L + 2) && await_runs<kNH, 0, false>(P.x_mid, H, epoch(L, 4), x, a, P), s, P))
                 return false;
+            note_received(s, 4 * L + 2);
             store_runs(s.gamma_in, next, a);
         }
         stamp(P.trace, b, 64 * L + 6);
@@ -906,6 +921,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
             stamp(P.trace, b, 64 * L + 63, kWave);
             if (!a_check(ok, s, P)) return false;
+            note_received(s, 4 * L + 3);
             stamp(P.trace, b, 64 * L + 7);
             if (!quantize_into(xd, F, 1, a, s, round)) return false;
             post(s, 4 * L + 3);
@@ -915,6 +931,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             stamp(P.trace, b, 64 * (L + 1) + 0);
             if (!a_check(wait_published(s, 4 * L + 4) && await_runs<kNH, 0, false>(P.x_hidden, H, epoch(L, 6), x, a, P), s, P))
                 return false;
+            note_received(s, 4 * L + 4);
         }
     }
     // ---- final RMSNorm -> FP32 input of the head
@@ -925,6 +942,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         if (!a_check(wait_published(s, 4 * P.layers) &&
                          await_runs<kNH, 0, false>(P.x_hidden, H, epoch(P.layers - 1, 6), x, a, P), s, P))
             return false;
+        note_received(s, 4 * P.layers);
         stamp(P.trace, b, 64 * P.layers + 1);
         if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round)) return false;
         store_runs(s.xf, x, a);
@@ -1059,6 +1077,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
+        if (!wait_received(s, 4 * L + 1)) return false;
         load_qkv(next, more);
         // ---- o_proj + residual
         if (!wait_ready(s, 4 * L + 1)) return false;
@@ -1077,6 +1096,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
+        if (!wait_received(s, 4 * L + 2)) return false;
         load_o(next, more);
         // ---- gate|up + SiLU gate
         if (!wait_ready(s, 4 * L + 2)) return false;
@@ -1098,6 +1118,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
+        if (!wait_received(s, 4 * L + 3)) return false;
         load_gate_up(next, more);
         // ---- down_proj + residual
         if (!wait_ready(s, 4 * L + 3)) return false;
@@ -1116,6 +1137,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 15 + 8 * bw, kAT + kWave * bw);
+        if (!wait_received(s, 4 * L + 4)) return false;
         load_down(next, more);
     }
     return wait_ready(s, 4 * P.layers);
@@ -1129,6 +1151,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     const int H = P.hidden;
     if (t == 0) {
         s.ready[0] = s.ready[1] = -1;
+        s.received[0] = s.received[1] = -1;
         s.published = 0;
         s.abort = 0;
         s.pair[0][0] = s.pair[0][1] = s.pair[1][0] = s.pair[1][1] = 0;
