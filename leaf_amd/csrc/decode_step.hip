@@ -113,6 +113,7 @@ constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
 constexpr int kDppMirror = 0x140;      // row_mirror
+constexpr int kDppRor8 = 0x128;        // row_ror:8 (lane i of a 16-lane row reads lane (i + 8) mod 16)
 template <int Ctrl>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xF, 0xF, false);
@@ -521,19 +522,25 @@ __device__ __forceinline__ void fetch_gamma(float (&g)[N], const float* gamma, i
 }
 
 // -------------------------------------------------------- weight waves ---
+// A row no wave of this block reads for real (not owned, or past the last
+// layer) is still loaded, so that every phase issues the same loads on every
+// path: that keeps the compiler's in-order wait counts exact across the
+// layer loop (with a path that skips loads it must assume the worst and waits
+// for every load in flight, next-layer prefetches included).  Such loads read
+// one 16-byte chunk of row blockIdx.x, so the blocks spread them over
+// different lines and memory channels.
+__device__ __forceinline__ int spare_row(const WeightView& m) {
+    return min((int)blockIdx.x, m.rows - 1);
+}
+
 // One int8 row of `m` into registers: lane holds chunks lane + 64 j.  Slots
 // past the row end reload its last chunk (same cache line as a neighbour's
 // load, so no extra traffic); row_dot ignores them.  Branch-free, so every
-// load of a phase is in flight at once.  A row the wave does not need (live
-// false: not owned, or past the last layer) is still loaded, from one 16-byte
-// chunk the whole wave shares: every phase then issues the same loads on
-// every path, which keeps the compiler's in-order wait counts exact across
-// the layer loop (with a path that skips loads it must assume the worst and
-// waits for every load in flight, next-layer prefetches included).
+// load of a phase is in flight at once.
 template <int KC>
 __device__ __forceinline__ void load_row(v4u (&w)[KC], const WeightView& m, int row, int lane, bool live) {
     const int last = m.cols / 16 - 1;
-    const uint8_t* base = static_cast<const uint8_t*>(m.data) + (size_t)(live ? row : 0) * m.cols;
+    const uint8_t* base = static_cast<const uint8_t*>(m.data) + (size_t)(live ? row : spare_row(m)) * m.cols;
 #pragma unroll
     for (int j = 0; j < KC; ++j) w[j] = ldg_stream(base + 16 * (live ? min(lane + kWave * j, last) : 0));
 }
@@ -555,6 +562,64 @@ __device__ __forceinline__ int row_dot(const v4u (&w)[KC], const int8_t* xq, int
     return dpp_sum_i32(acc);
 }
 
+// This lane's part of the exact int32 dot of a register-held row with the
+// int8 input chunks xc (chunk lane + 64 j of the input, read once per phase).
+template <int KC>
+__device__ __forceinline__ int row_part(const v4u (&w)[KC], const v4u (&xc)[KC], int chunks, int lane) {
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+        int a = dot4((int)w[j].x, (int)xc[j].x, 0);
+        a = dot4((int)w[j].y, (int)xc[j].y, a);
+        a = dot4((int)w[j].z, (int)xc[j].z, a);
+        a = dot4((int)w[j].w, (int)xc[j].w, a);
+        acc += lane + kWave * j < chunks ? a : 0;
+    }
+    return acc;
+}
+
+// Totals of eight rows' lane parts v[0..7], transposed: every lane of the
+// 8-lane group l / 8 ends with the total of v[l / 8].  The rows fold pairwise
+// across the wave halves (v[j] with v[j + 4], permlane32 swap), then across
+// 16-lane rows (permlane16 swap), then within each 16-lane row (row_ror 8 with
+// lane selects), then within the 8-lane groups (half-row mirror and quad
+// permutes): 22 lane moves and adds instead of a full reduction per row.
+// Integer sums, so the totals are exact whatever the order.
+__device__ __forceinline__ int sum8_transposed(const int (&v)[8], int lane) {
+    int u[4], w[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)v[j], (unsigned)v[j + 4], false, false);
+        u[j] = (int)p[0] + (int)p[1];   // lanes 0-31: v[j] folded; lanes 32-63: v[j + 4] folded
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)u[j], (unsigned)u[j + 2], false, false);
+        w[j] = (int)p[0] + (int)p[1];   // 16-lane rows 0..3: v[j], v[j + 2], v[j + 4], v[j + 6]
+    }
+    const bool high = (lane & 8) != 0;
+    int g = (high ? w[1] : w[0]) + dpp<kDppRor8>(high ? w[0] : w[1]);   // 8-lane group k: v[k]
+    g += dpp<kDppHalfMirror>(g);
+    g += dpp<kDppXor2>(g);
+    g += dpp<kDppXor1>(g);
+    return g;
+}
+
+// Totals of two rows' lane parts: lanes 0-31 end with the total of v0,
+// lanes 32-63 with that of v1 (permlane32 and permlane16 swaps, then four
+// DPP steps within each 16-lane row).  Exact integer sums.
+__device__ __forceinline__ int sum2_transposed(int v0, int v1) {
+    const auto p = __builtin_amdgcn_permlane32_swap((unsigned)v0, (unsigned)v1, false, false);
+    const int u = (int)p[0] + (int)p[1];
+    const auto q = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+    int g = (int)q[0] + (int)q[1];   // 16-lane rows 0, 1: v0 folded to 16 lanes; rows 2, 3: v1
+    g += dpp<kDppRor8>(g);
+    g += dpp<kDppHalfMirror>(g);
+    g += dpp<kDppXor2>(g);
+    g += dpp<kDppXor1>(g);
+    return g;
+}
+
 // ((float)acc * s_x) * s_w + b  (decoder.cpp:568, 1229), separate roundings.
 __device__ __forceinline__ float dequant(int acc, float sx, float sw, float bias) {
     const float term = (float)acc * sx;
@@ -565,8 +630,8 @@ __device__ __forceinline__ float dequant(int acc, float sx, float sw, float bias
 struct RowScale {
     float scale = 0.0f, bias = 0.0f;
     __device__ __forceinline__ void fetch(const WeightView& m, int r, bool live) {
-        scale = ldg(m.scales + (live ? r : 0));
-        bias = ldg(m.bias + (live ? r : 0));
+        scale = ldg(m.scales + (live ? r : spare_row(m)));
+        bias = ldg(m.bias + (live ? r : spare_row(m)));
     }
 };
 
@@ -957,7 +1022,9 @@ struct LayerRows {
     v4u o[kOR][kKCH];
     v4u g[kGP][2][kKCH];
     v4u d[kOR][kKCF];
-    RowScale qs[kQP][2], os[kOR], gs[kGP][2], ds[kOR];
+    RowScale qs[kQP][2];
+    RowScale os, ds;   // per lane: o / down row k = lane / 32 of this wave
+    RowScale gs;   // per lane: the gate|up row whose total this lane's 8-lane group holds
 };
 
 __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
@@ -992,6 +1059,17 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     for (int k = 0; k < kOR; ++k) has_r[k] = own.r_first + bw + kB * k < own.r_end;
 #pragma unroll
     for (int k = 0; k < kGP; ++k) has_g[k] = own.g_first + bw + kB * k < own.g_end;
+    static_assert(kGP == 4, "gate|up totals are reduced eight rows at a time");
+    static_assert(kOR == 2, "o and down totals are reduced two rows at a time");
+    // This lane's o / down row after sum2_transposed: lanes 0-31 hold row 0
+    // of the wave, lanes 32-63 row 1.
+    const int r_row = own.r_first + bw + kB * (lane >> 5);
+    const bool r_live = r_row < own.r_end;
+    // This lane's gate|up row after sum8_transposed: 8-lane groups 0-3 hold
+    // the gate rows of pairs 0-3, groups 4-7 their up rows.
+    const int g_pair = own.g_first + bw + kB * ((lane >> 3) & 3);
+    const bool g_live = g_pair < own.g_end;
+    const int g_row = (lane < 32 ? 0 : F) + g_pair;
 
     LayerRows w;
     // Loads of one phase's rows; `more` false loads nothing useful (the last
@@ -1010,8 +1088,8 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         for (int k = 0; k < kOR; ++k) {
             const int row = own.r_first + bw + kB * k;
             load_row(w.o[k], Ly.o, row, lane, has_r[k] && more);
-            w.os[k].fetch(Ly.o, row, has_r[k] && more);
         }
+        w.os.fetch(Ly.o, r_row, r_live && more);
     };
     auto load_gate_up = [&](const StepLayer& Ly, bool more) {
 #pragma unroll
@@ -1019,17 +1097,16 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
             const int p = own.g_first + bw + kB * k;
             load_row(w.g[k][0], Ly.gate_up, p, lane, has_g[k] && more);
             load_row(w.g[k][1], Ly.gate_up, F + p, lane, has_g[k] && more);
-            w.gs[k][0].fetch(Ly.gate_up, p, has_g[k] && more);
-            w.gs[k][1].fetch(Ly.gate_up, F + p, has_g[k] && more);
         }
+        w.gs.fetch(Ly.gate_up, g_row, g_live && more);
     };
     auto load_down = [&](const StepLayer& Ly, bool more) {
 #pragma unroll
         for (int k = 0; k < kOR; ++k) {
             const int row = own.r_first + bw + kB * k;
             load_row(w.d[k], Ly.down, row, lane, has_r[k] && more);
-            w.ds[k].fetch(Ly.down, row, has_r[k] && more);
         }
+        w.ds.fetch(Ly.down, r_row, r_live && more);
     };
     load_qkv(layer_at(s, 0), true);
     load_o(layer_at(s, 0), true);
@@ -1083,16 +1160,19 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         if (!wait_ready(s, 4 * L + 1)) return false;
         stamp(P.trace, b, 64 * L + 10 + 8 * bw, kAT + kWave * bw);
         {
+            // both rows' dots against one read of the input, one joint
+            // reduction; lane 32 k publishes row k
             const float sx = s.sx[1];
+            const int chunks = P.heads * dim / 16;
+            v4u xc[kKCH];
 #pragma unroll
-            for (int k = 0; k < kOR; ++k)
-                if (has_r[k]) {
-                    const int row = own.r_first + bw + kB * k;
-                    const int acc = row_dot(w.o[k], s.xq[1], P.heads * dim / 16, lane);
-                    if (lane == 0)
-                        publish(P.x_mid + row, epoch(L, 4),
-                                s.h_in[row] + dequant(acc, sx, w.os[k].scale, w.os[k].bias));
-                }
+            for (int j = 0; j < kKCH; ++j)
+                xc[j] = *reinterpret_cast<const v4u*>(s.xq[1] + 16 * min(lane + kWave * j, chunks - 1));
+            const int p0 = has_r[0] ? row_part(w.o[0], xc, chunks, lane) : 0;
+            const int p1 = has_r[1] ? row_part(w.o[1], xc, chunks, lane) : 0;
+            const int acc = sum2_transposed(p0, p1);
+            if ((lane & 31) == 0 && r_live)
+                publish(P.x_mid + r_row, epoch(L, 4), s.h_in[r_row] + dequant(acc, sx, w.os.scale, w.os.bias));
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
@@ -1102,19 +1182,27 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         if (!wait_ready(s, 4 * L + 2)) return false;
         stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
         {
+            // Eight row dots against one read of the input, one transposed
+            // reduction, then every pair's epilogue at once: lane 8 k (k < 4)
+            // combines pair k's gate with its up (brought over from lane 8 k + 32).
+            // Pairs this wave does not own are skipped (a wave-uniform test).
             const float sx = s.sx[0];
+            const int chunks = H / 16;
+            v4u xc[kKCH];
 #pragma unroll
-            for (int k = 0; k < kGP; ++k)
-                if (has_g[k]) {
-                    const int p = own.g_first + bw + kB * k;
-                    const int ag = row_dot(w.g[k][0], s.xq[0], H / 16, lane);
-                    const int au = row_dot(w.g[k][1], s.xq[0], H / 16, lane);
-                    if (lane == 0) {
-                        const float gate = dequant(ag, sx, w.gs[k][0].scale, w.gs[k][0].bias);
-                        const float up = dequant(au, sx, w.gs[k][1].scale, w.gs[k][1].bias);
-                        publish(P.x_act + p, epoch(L, 5), up * activate(P.activation, gate));
-                    }
-                }
+            for (int j = 0; j < kKCH; ++j)
+                xc[j] = *reinterpret_cast<const v4u*>(s.xq[0] + 16 * min(lane + kWave * j, chunks - 1));
+            int part[2 * kGP];
+#pragma unroll
+            for (int k = 0; k < kGP; ++k) {
+                part[k] = has_g[k] ? row_part(w.g[k][0], xc, chunks, lane) : 0;
+                part[kGP + k] = has_g[k] ? row_part(w.g[k][1], xc, chunks, lane) : 0;
+            }
+            const float mine = dequant(sum8_transposed(part, lane), sx, w.gs.scale, w.gs.bias);
+            const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
+                                                                             __float_as_uint(mine), false, false)[1]);
+            if (lane < 32 && (lane & 7) == 0 && g_live)
+                publish(P.x_act + g_pair, epoch(L, 5), up * activate(P.activation, mine));
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
@@ -1125,15 +1213,16 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 14 + 8 * bw, kAT + kWave * bw);
         {
             const float sx = s.sx[1];
+            const int chunks = F / 16;
+            v4u xc[kKCF];
 #pragma unroll
-            for (int k = 0; k < kOR; ++k)
-                if (has_r[k]) {
-                    const int row = own.r_first + bw + kB * k;
-                    const int acc = row_dot(w.d[k], s.xq[1], F / 16, lane);
-                    if (lane == 0)
-                        publish(P.x_hidden + row, epoch(L, 6),
-                                s.h_mid[row] + dequant(acc, sx, w.ds[k].scale, w.ds[k].bias));
-                }
+            for (int j = 0; j < kKCF; ++j)
+                xc[j] = *reinterpret_cast<const v4u*>(s.xq[1] + 16 * min(lane + kWave * j, chunks - 1));
+            const int p0 = has_r[0] ? row_part(w.d[0], xc, chunks, lane) : 0;
+            const int p1 = has_r[1] ? row_part(w.d[1], xc, chunks, lane) : 0;
+            const int acc = sum2_transposed(p0, p1);
+            if ((lane & 31) == 0 && r_live)
+                publish(P.x_hidden + r_row, epoch(L, 6), s.h_mid[r_row] + dequant(acc, sx, w.ds.scale, w.ds.bias));
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 15 + 8 * bw, kAT + kWave * bw);
