@@ -1111,7 +1111,6 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     load_qkv(layer_at(s, 0), true);
     load_o(layer_at(s, 0), true);
     load_gate_up(layer_at(s, 0), true);
-    load_down(layer_at(s, 0), true);
 
     for (int L = 0; L < P.layers; ++L) {
         float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
@@ -1154,6 +1153,9 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
+        // this layer's down rows: the attention that follows reads little
+        // from memory, and the norm and q|k|v phases are over
+        load_down(layer_at(s, L), true);
         if (!wait_received(s, 4 * L + 1)) return false;
         load_qkv(next, more);
         // ---- o_proj + residual
@@ -1226,8 +1228,6 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 15 + 8 * bw, kAT + kWave * bw);
-        if (!wait_received(s, 4 * L + 4)) return false;
-        load_down(next, more);
     }
     return wait_ready(s, 4 * P.layers);
 }
