@@ -1,0 +1,195 @@
+"""The benchmark configurations at their full shapes, on the GPU against the oracle.
+
+* GPT-2 small FP32 (12 x 768, 12 heads, vocab 50257): a 16-token seeded prompt
+  and 32 greedy tokens.  Every logit of the prefill and of each decode step
+  within LOGIT_TOLERANCE, and the GPU's own greedy run identical to the
+  oracle's.
+* TinyLlama-1.1B W8A8 (22 x 2048, 32/4 heads, SwiGLU 5632, FP32 head): a
+  512-token prompt, then 48 teacher-forced decode steps on the persistent
+  decode step, within a band the oracle measures on itself (see the test).
+* Qwen2.5-0.5B INT4 group 32 (24 x 896, 14/2 heads, vocab 151936, tied) and
+  SmolLM2-360M BF16 with accurate FP32 math (32 x 960, 15/5 heads): full
+  geometry against the oracle with 128-token prompts (the oracle's scalar
+  prefill of the configured 4096 / 2048 tokens takes minutes on the host);
+  their configured spans are checked on the GPU alone: the prompt's last
+  token decoded after a prefill of the rest must give the logits of the
+  one-shot prefill (decode attention over 4095 / 2047 cached keys against the
+  prefill attention kernel), and a prefill in chunks must give them too.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from leaf_amd import models
+from leaf_amd.artifact import write_artifact
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOLERANCE = 1e-3          # FP32 / BF16 / weight-only INT4: max-abs error / max |logit|
+
+
+def rel_error(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def rel_rmse(a, b):
+    return float(np.sqrt(np.mean((a - b) ** 2)) / max(np.sqrt(np.mean(b ** 2)), 1e-12))
+
+
+def decisive(reference, band):
+    top = np.sort(reference)[-2:]
+    return top[1] - top[0] > 2 * band * np.max(np.abs(reference))
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from leaf_amd import runtime
+    runtime.library()
+    return runtime
+
+
+@pytest.fixture(scope="module")
+def full_artifacts(tmp_path_factory):
+    root = tmp_path_factory.mktemp("full")
+    cache = {}
+
+    def get(family):
+        if family not in cache:
+            path = root / f"{family}.leaf"
+            write_artifact(path, models.PRESETS[family](), seed=20261202)
+            cache[family] = path
+        return cache[family]
+    return get
+
+
+def teacher_forced(dec, od, prompt, steps, tolerance):
+    """Prefill, then `steps` decode steps fed the oracle's greedy token; returns
+    the worst relative logit error and the tokens."""
+    a, b = dec.forward(prompt), od.forward(prompt)
+    worst = rel_error(a, b)
+    assert worst <= tolerance, f"prefill logits off by {worst:.2e}"
+    tokens = []
+    for step in range(steps):
+        tok = int(np.argmax(b))
+        assert int(np.argmax(a)) == tok, f"greedy token differs at step {step}"
+        tokens.append(tok)
+        a, b = dec.forward([tok]), od.forward([tok])
+        worst = max(worst, rel_error(a, b))
+        assert worst <= tolerance, f"decode step {step}: logits off by {worst:.2e}"
+    return worst, tokens
+
+
+def test_gpt2_small_full_logits_and_greedy_run(rt, oracle, full_artifacts):
+    path = full_artifacts("gpt2")
+    prompt = np.random.default_rng(1).integers(0, 50257, 16).astype(np.uint32)
+    dec = rt.Decoder(path, 32, "fast")
+    od = oracle.decoder(path, 32, False)
+    worst, forced = teacher_forced(dec, od, prompt, 32, LOGIT_TOLERANCE)
+    dec.reset()
+    od.reset()
+    tokens, _, _ = dec.generate(prompt, 32)
+    expected = od.generate(prompt, 32)
+    print(f"gpt2 full: worst relative logit error {worst:.2e} over the prefill and 32 decode steps")
+    assert tokens == expected
+    assert tokens[:len(forced)] == forced[:len(tokens)]
+    dec.close()
+
+
+def oracle_rows(oracle, path, prompt, tokens, norm_order):
+    """The oracle's last-row logits of the prefill and of one decode step per
+    token, with its RMSNorm square sum in the given order."""
+    oracle.set_norm_order(norm_order)
+    try:
+        od = oracle.decoder(path, 8, False)
+        rows = [od.forward(prompt)]
+        for tok in tokens:
+            rows.append(od.forward([tok]))
+        od.close()
+    finally:
+        oracle.set_norm_order(0)
+    return np.stack(rows)
+
+
+def test_tinyllama_w8a8_full_prefill_and_decode_steps(rt, oracle, full_artifacts):
+    """At 22 layers the int8 rounding flips of W8A8 compound: the oracle itself,
+    with nothing but its RMSNorm square sum taken pairwise instead of
+    sequentially, moves these logits by 6-9% of the largest |logit| (measured
+    at 512 keys).  That distance, measured here on the same inputs, is the
+    band: the GPU must stay within 1.5 times it, its greedy choice must match
+    wherever the oracle's top-2 margin is wider than twice it, and it must
+    agree with the oracle's greedy choice about as often as the pairwise-norm
+    oracle does (43 and 42 of 49 rows when this was written)."""
+    path = full_artifacts("tinyllama")
+    prompt = np.random.default_rng(2).integers(0, 32000, 512).astype(np.uint32)
+    steps = 48
+    od = oracle.decoder(path, 8, False)
+    ref = [od.forward(prompt)]
+    tokens = []
+    for _ in range(steps):
+        tokens.append(int(np.argmax(ref[-1])))
+        ref.append(od.forward([tokens[-1]]))
+    od.close()
+    ref = np.stack(ref)
+    alt = oracle_rows(oracle, path, prompt, tokens, 1)
+    band = max(rel_error(x, y) for x, y in zip(alt, ref))
+    band_rmse = max(rel_rmse(x, y) for x, y in zip(alt, ref))
+    dec = rt.Decoder(path, 8, "fast", max_context=700, max_prefill=512)
+    rows = [dec.forward(prompt)]
+    dec.set_profiling(True)
+    for tok in tokens:
+        rows.append(dec.forward([tok]))
+    launches = dec.profile().get("decode_step", {}).get("launches", 0)
+    dec.close()
+    worst = max(rel_error(x, y) for x, y in zip(rows, ref))
+    rmse = max(rel_rmse(x, y) for x, y in zip(rows, ref))
+    checked = 0
+    for i, (x, y) in enumerate(zip(rows, ref)):
+        if decisive(y, band):
+            assert int(np.argmax(x)) == int(np.argmax(y)), f"greedy token differs at row {i} with a decisive margin"
+            checked += 1
+    # how often the greedy choice survives inside the band: the oracle against
+    # itself, and the GPU against the oracle
+    same_alt = sum(int(np.argmax(x)) == int(np.argmax(y)) for x, y in zip(alt, ref))
+    same_gpu = sum(int(np.argmax(x)) == int(np.argmax(y)) for x, y in zip(rows, ref))
+    print(f"tinyllama full: oracle band {band:.2e} (RMSE {band_rmse:.2e}); GPU worst {worst:.2e} (RMSE {rmse:.2e}); "
+          f"greedy choice compared at {checked} of {steps + 1} rows; same argmax as the oracle in {same_gpu} rows "
+          f"(the oracle's pairwise-norm run: {same_alt}); {launches} persistent-step launches")
+    assert launches == steps
+    assert worst <= 1.5 * band
+    assert rmse <= 1.5 * band_rmse
+    assert same_gpu >= same_alt - 2, "the greedy choice departs from the oracle more often than a reorder does"
+
+
+@pytest.mark.parametrize("family,math", [("qwen", "fast"), ("smollm2", "accurate")])
+def test_full_geometry_against_oracle(rt, oracle, full_artifacts, family, math):
+    path = full_artifacts(family)
+    spec = models.PRESETS[family]()
+    prompt = np.random.default_rng(3).integers(0, spec.vocab, 128).astype(np.uint32)
+    dec = rt.Decoder(path, 32, math)
+    od = oracle.decoder(path, 32, math == "accurate")
+    worst, _ = teacher_forced(dec, od, prompt, 8, LOGIT_TOLERANCE)
+    dec.close()
+    print(f"{family} full geometry: worst relative logit error {worst:.2e} (tolerance {LOGIT_TOLERANCE:.0e})")
+
+
+@pytest.mark.parametrize("family,math,span", [("qwen", "fast", 4096), ("smollm2", "accurate", 2048)])
+def test_configured_span_decode_matches_prefill(rt, full_artifacts, family, math, span):
+    path = full_artifacts(family)
+    spec = models.PRESETS[family]()
+    prompt = np.random.default_rng(4).integers(0, spec.vocab, span).astype(np.uint32)
+    one = rt.Decoder(path, 32, math, max_context=span + 8, max_prefill=span)
+    whole = one.forward(prompt)
+    one.reset()
+    one.forward(prompt[:-1])
+    stepped = one.forward(prompt[-1:])
+    one.reset()
+    chunked = None
+    for pos in range(0, span, 512):
+        chunked = one.forward(prompt[pos:pos + 512])
+    one.close()
+    e_step, e_chunk = rel_error(stepped, whole), rel_error(chunked, whole)
+    print(f"{family} span {span}: decode-vs-prefill {e_step:.2e}, chunked-vs-one-shot {e_chunk:.2e}")
+    assert e_step <= LOGIT_TOLERANCE
+    assert e_chunk <= LOGIT_TOLERANCE
+    assert int(np.argmax(stepped)) == int(np.argmax(whole)) == int(np.argmax(chunked))
