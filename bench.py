@@ -16,6 +16,8 @@ Beside it:
                 of the same decode steps;
   gemv          standalone W8A8 GEMV at the TinyLlama shapes (M = 1), rotating
                 >= 1 GiB of weight copies so the 256 MiB MALL cannot serve them;
+  linear_w8a8   the same shapes at M = 4, 16, 128 and 512 tokens (the prefill
+                GEMM at 512): us per call, int8 TOPS against the 5.0 POPS peak;
   cpu_baseline  the reference CPU engine (oracle/_ref/leaf_decoder, built from the
                 reference sources) on this host, on a bounded sample.
   traffic       HBM bytes per launch of the dominant kernel from two rocprofv3
@@ -43,6 +45,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, datasheet
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, datasheet
 TRAFFIC_FILE = ROOT / "profiles" / "decode_step_tinyllama_w8a8_traffic.json"
 COPY_BYTES = 1 << 30           # hbm_copy 1024: reads and writes this many bytes per launch
 PROMPT_TOKENS = 512
@@ -142,6 +145,52 @@ def gemv_microbench(repeats: int = 20) -> dict:
     return results
 
 
+def linear_microbench(tokens=(4, 16, 128, 512), repeats: int = 3) -> dict:
+    """W8A8 linear at the TinyLlama shapes for M > 1 tokens: per-token int8
+    activations (quantized beforehand, as the decoder's norm epilogues leave
+    them), per-row int8 weights, the split-K epilogue included, rotating
+    >= 1 GiB of weight copies.  Reported per shape as microseconds per call,
+    int8 TOPS against the 5.0 POPS dense peak, and the bytes of the call
+    (N*K + 8N + M*K + 4M + 4MN) per microsecond."""
+    from leaf_amd import runtime
+    from leaf_amd.models import W8A8_LINEAR_SHAPES
+    rng = np.random.default_rng(SEED + 3)
+    shapes = sorted(set(W8A8_LINEAR_SHAPES))
+    layer_bytes = sum(k * n for k, n in W8A8_LINEAR_SHAPES)
+    copies = int(np.ceil(1.1 * (1 << 30) / layer_bytes))
+    weights = {}
+    for (K, N) in shapes:
+        data = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        scales = (rng.random(N, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+        weights[(K, N)] = [runtime.DeviceWeight(data, 8, K, scales, K) for _ in range(copies)]
+    out = {}
+    for M in tokens:
+        row = {}
+        for (K, N) in shapes:
+            q = runtime.DeviceArray.of(rng.integers(-127, 128, (M, K), dtype=np.int8))
+            xs = runtime.DeviceArray.of((rng.random(M, dtype=np.float32) * 1e-2 + 1e-3).astype(np.float32))
+            y = runtime.DeviceArray((M, N), np.float32)
+            ws = weights[(K, N)]
+            for w in ws[:3]:
+                runtime.linear_q(w, q, xs, M, y)
+            timer = runtime.Timer()
+            launches = 0
+            for _ in range(repeats):
+                for w in ws:
+                    runtime.linear_q(w, q, xs, M, y)
+                    launches += 1
+            ms = timer.stop() / launches
+            ops = 2.0 * M * N * K
+            traffic = N * K + 8 * N + M * K + 4 * M + 4 * M * N
+            row[f"{K}x{N}"] = {"us": round(ms * 1e3, 2), "TOPS": round(ops / ms / 1e9, 1),
+                               "frac_mfma": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
+                               "GBps": round(traffic / ms / 1e6, 1)}
+        out[f"M={M}"] = row
+    for s in weights.values():
+        s.clear()
+    return out
+
+
 def cpu_baseline(path: Path, budget_s: float = 30.0) -> dict | None:
     """Reference CPU engine (built from the reference sources) on this host."""
     from leaf_amd.artifact import write_tokens
@@ -222,6 +271,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemv", action="store_true")
+    parser.add_argument("--no-linear", action="store_true")
     parser.add_argument("--derive-traffic", type=Path, default=None)
     args = parser.parse_args()
     if args.derive_traffic is not None:
@@ -257,6 +307,10 @@ def main() -> int:
     if not args.no_gemv:
         log("GEMV microbenchmark ...")
         gemv = gemv_microbench()
+    linear = None
+    if not args.no_linear:
+        log("W8A8 linear microbenchmark ...")
+        linear = linear_microbench()
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline ...")
@@ -278,6 +332,7 @@ def main() -> int:
                      "launches": g["launches"]},
         "device_ms_per_step": device_ms,
         "gemv": gemv,
+        "linear_w8a8": linear,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
