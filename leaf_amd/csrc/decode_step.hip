@@ -1101,13 +1101,14 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         if (k0 == 0) w.gs.fetch(Ly.gate_up, g_row, g_live && more);
     };
-    auto load_down = [&](const StepLayer& Ly, bool more) {
+    auto load_down = [&](const StepLayer& Ly, bool more, int k0 = 0, int k1 = kOR) {
 #pragma unroll
         for (int k = 0; k < kOR; ++k) {
+            if (k < k0 || k >= k1) continue;
             const int row = own.r_first + bw + kB * k;
             load_row(w.d[k], Ly.down, row, lane, has_r[k] && more);
         }
-        w.ds.fetch(Ly.down, r_row, r_live && more);
+        if (k0 == 0) w.ds.fetch(Ly.down, r_row, r_live && more);
     };
     load_qkv(layer_at(s, 0), true);
     load_o(layer_at(s, 0), true);
@@ -1154,9 +1155,10 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
-        // this layer's down rows: the attention that follows reads little
-        // from memory, and the norm and q|k|v phases are over
-        load_down(layer_at(s, L), true);
+        // this layer's first down row: the attention that follows reads
+        // little from memory, and the norm and q|k|v phases are over (the
+        // second goes out with the o prefetch, after the x_mid hop)
+        load_down(layer_at(s, L), true, 0, 1);
         if (!wait_received(s, 4 * L + 1)) return false;
         load_qkv(next, more);
         // ---- o_proj + residual
@@ -1181,6 +1183,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
         if (!wait_received(s, 4 * L + 2)) return false;
         load_o(next, more);
+        load_down(layer_at(s, L), true, 1, kOR);
         // ---- gate|up + SiLU gate
         if (!wait_ready(s, 4 * L + 2)) return false;
         stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
