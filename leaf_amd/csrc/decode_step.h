@@ -51,6 +51,10 @@ struct StepParams {
     unsigned long long* x_attn = nullptr;       // merged attention output        [q]
     unsigned long long* x_act = nullptr;        // SiLU-gated MLP activation       [ffn]
     unsigned long long* x_part = nullptr;       // attention span partials [kv][spans][group][dim + 2]
+    // The same partials in plain device memory, for the XCD-local merge (null: off).  Items and
+    // merge waves of a head pair then sit on one XCD (block b runs on XCD b % 8), the items write
+    // with plain stores that stay in that XCD's L2 and the merge waves read them from there.
+    unsigned long long* x_part_local = nullptr;
     unsigned long long* x_best = nullptr;       // per-block argmax candidates [blocks][2]
     unsigned* counters = nullptr;               // [kv_heads] span arrivals (zero between uses)
     unsigned* abort_flag = nullptr;             // set when a wait times out (device copy, polled by blocks)

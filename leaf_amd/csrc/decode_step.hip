@@ -180,9 +180,15 @@ __device__ __forceinline__ u64 fetch(const u64* p) {
 __device__ __forceinline__ bool aborted(const unsigned* flag) {
     return __hip_atomic_load((const LEAF_GLOBAL unsigned*)flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
-__device__ __forceinline__ void raise_abort(const StepParams& P) {
-    __hip_atomic_store((LEAF_GLOBAL unsigned*)P.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (P.host_abort) *P.host_abort = 1u;
+__device__ __forceinline__ void raise_abort(const StepParams& P, unsigned why = 1u) {
+    __hip_atomic_store((LEAF_GLOBAL unsigned*)P.abort_flag, why, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (P.host_abort) *P.host_abort = why;
+}
+// Abort code: a block did not run on XCD blockIdx.x % 8, so the XCD-local
+// merge cannot work (the host turns it off and runs the step again).
+constexpr unsigned kAbortXcdMapping = 2u;
+__device__ __forceinline__ int xcc_id() {
+    return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)) & 15;   // hwreg(HW_REG_XCC_ID, 0, 16)
 }
 __device__ __forceinline__ int lds_load(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -730,7 +736,12 @@ struct Ownership {
 // weight 0.
 template <int HPW>
 __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, int lane, int aw, int h0, int h_end,
-                                               int keys, u64* parts, unsigned epoch) {
+                                               int keys, u64* parts, unsigned epoch, bool local) {
+    // plain stores (they stay in this XCD's L2) for the XCD-local merge
+    auto put = [&](u64* p, float v) {
+        if (local) __hip_atomic_store((LEAF_GLOBAL u64*)p, tagged(epoch, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+        else publish(p, epoch, v);
+    };
     constexpr int dim = kStepDim;
     // scores: lane = key, four dims of its K row at a time
     float sum[HPW];
@@ -789,10 +800,10 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
         const int gh = h0 + aw + kA * h;
         if (gh < h_end) {
             u64* part = parts + (size_t)gh * (dim + 2);
-            publish(part + 2 + lane, epoch, o[h]);
+            put(part + 2 + lane, o[h]);
             if (lane == 0) {
-                publish(part, epoch, m[h]);
-                publish(part + 1, epoch, l[h]);
+                put(part, m[h]);
+                put(part + 1, l[h]);
             }
         }
     }
@@ -820,14 +831,39 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     while (hpw < kHeadsA && hpw < P.item_heads) hpw *= 2;
     while (hpw < kHeadsA && P.kv_heads * spans * ((group + kA * hpw - 1) / (kA * hpw)) > G) hpw *= 2;
     const int slices = (group + kA * hpw - 1) / (kA * hpw);
-    const bool has_item = b < P.kv_heads * spans * slices;
-    const int item_g = has_item ? b / (spans * slices) : 0, item_s = has_item ? b / slices % spans : 0;
-    const int item_h0 = has_item ? b % slices * kA * hpw : 0, item_h1 = min(group, item_h0 + kA * hpw);
+    // XCD-local merge: head slices (kA heads, one merge block each) are dealt
+    // to the XCDs round robin, slice sigma to XCD sigma % 8; its span items
+    // and its merge block run on blocks of that XCD (block b on XCD b % 8,
+    // checked at kernel start), so the partials travel through that XCD's
+    // L2 instead of memory.  It needs one head per exchange wave, slices
+    // spread evenly over the XCDs, and room for their items on each XCD.
+    const int S = P.kv_heads * slices, per = S / 8;
+    const bool local = P.x_part_local && hpw == 1 && G % 8 == 0 && S % 8 == 0 && per * spans <= G / 8;
+    int sigma = -1, merge_sigma = -1;      // this block's item slice and merge slice (local mode)
+    bool has_item;
+    int item_g, item_s, item_h0;
+    if (local) {
+        const int x = b & 7, k = b >> 3;
+        has_item = k < per * spans;
+        sigma = has_item ? x + 8 * (k / spans) : 0;
+        item_g = sigma / slices;
+        item_s = has_item ? k % spans : 0;
+        item_h0 = sigma % slices * kA;
+        if (k >= G / 8 - per) merge_sigma = x + 8 * (G / 8 - 1 - k);
+    } else {
+        has_item = b < P.kv_heads * spans * slices;
+        item_g = has_item ? b / (spans * slices) : 0;
+        item_s = has_item ? b / slices % spans : 0;
+        item_h0 = has_item ? b % slices * kA * hpw : 0;
+    }
+    const int item_h1 = min(group, item_h0 + kA * hpw);
     const int k0 = begin + item_s * kStepSpanKeys, k1 = min(end, k0 + kStepSpanKeys);
     const int cached_end = min(k1, pos), keys = k1 - k0;
     const bool new_key = pos >= k0 && pos < k1;
     // merge blocks: the last ceil(heads / kA) blocks, one query head per wave
-    const bool merge_block = (G - 1 - b) * kA < P.heads;
+    // (local mode: the last `per` blocks of each XCD, one head slice each)
+    const bool merge_block = local ? merge_sigma >= 0 : (G - 1 - b) * kA < P.heads;
+    u64* const part_base = local ? P.x_part_local : P.x_part;
 
     float x[kNH];
     {
@@ -911,22 +947,23 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
             if (!a_sync(s, round)) return false;
             stamp(P.trace, b, 64 * L + 56);
-            u64* parts = P.x_part + (size_t)(item_g * spans + item_s) * group * (dim + 2);
-            if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
-            else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
-            else if (hpw == 4) attention_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
-            else attention_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2));
+            u64* parts = part_base + (size_t)(item_g * spans + item_s) * group * (dim + 2);
+            if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), local);
+            else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+            else if (hpw == 4) attention_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+            else attention_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
             stamp(P.trace, b, 64 * L + 57);
         }
         if (merge_block) {
             // this wave's query head mh: combine its spans (lane s holds span
             // s's max and sum; lane d accumulates output element d)
             bool ok = true;
-            const int mh = (G - 1 - b) * kA + aw;
-            if (mh < P.heads) {
+            const int mh = local ? merge_sigma / slices * group + merge_sigma % slices * kA + aw : (G - 1 - b) * kA + aw;
+            const bool mine = local ? merge_sigma % slices * kA + aw < group : mh < P.heads;
+            if (mine) {
                 const int g = mh / group, gh = mh % group;
                 const size_t stride = (size_t)group * (dim + 2);
-                const u64* base = P.x_part + ((size_t)g * spans * group + gh) * (dim + 2);
+                const u64* base = part_base + ((size_t)g * spans * group + gh) * (dim + 2);
                 // One read takes every (max, sum) pair and the first
                 // kMergeBatch spans' outputs; later batches are read as needed.
                 v2f ml;
@@ -1261,6 +1298,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         for (int i = t; i < words; i += kT) dst[i] = ldg(src + i);
     }
     __syncthreads();
+    if (P.x_part_local && t == 0 && xcc_id() != (b & 7)) raise_abort(P, kAbortXcdMapping);
     const bool ok = wave < kA ? exchange_role(P, s) : weight_role(P, s);
     if (__syncthreads_or(!ok)) return;          // every wave leaves when one gave up (abort flags raised)
 

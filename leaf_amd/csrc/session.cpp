@@ -358,6 +358,14 @@ void Session::step_prepare() {
     p.x_act = w; w += ffn_words;
     p.x_part = w; w += part;
     p.x_best = w; w += 2 * size_t(blocks);
+    // XCD-local copy of the span partials (plain device memory); see
+    // StepParams::x_part_local.  LEAF_DECODE_STEP_LOCAL_MERGE=0 turns it off.
+    const char* local = std::getenv("LEAF_DECODE_STEP_LOCAL_MERGE");
+    if (!(local && std::string(local) == "0")) {
+        step_part_local_.allocate(part * 8);
+        hip_check(hipMemset(step_part_local_.ptr, 0, step_part_local_.bytes), "hipMemset");
+        p.x_part_local = step_part_local_.as<unsigned long long>();
+    }
     p.counters = reinterpret_cast<unsigned*>(w);
     p.abort_flag = p.counters + c.kv_heads;
     hip_check(hipHostMalloc((void**)&step_host_abort_, sizeof(unsigned), hipHostMallocMapped), "hipHostMalloc");
@@ -424,6 +432,8 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
     if (++step_launch_ >= (1u << 20)) {
         // Epoch tags would repeat: start the exchange words from zero again.
         hip_check(hipMemsetAsync(step_exchange_.ptr, 0, step_exchange_.bytes, s), "hipMemsetAsync");
+        if (step_part_local_.ptr)
+            hip_check(hipMemsetAsync(step_part_local_.ptr, 0, step_part_local_.bytes, s), "hipMemsetAsync");
         step_launch_ = 1;
     }
     StepParams p = step_;
@@ -446,9 +456,18 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
     if (*step_host_abort_) {
         // A wait timed out: counters and exchange words may be mid-round.
         // Start the next step from zeroed state.
+        const unsigned why = *step_host_abort_;
         *step_host_abort_ = 0;
         hip_check(hipMemset(step_exchange_.ptr, 0, step_exchange_.bytes), "hipMemset");
+        if (step_part_local_.ptr) hip_check(hipMemset(step_part_local_.ptr, 0, step_part_local_.bytes), "hipMemset");
         step_token_valid_ = false;
+        if (why == 2 && step_.x_part_local) {
+            // A block ran off XCD blockIdx % 8: the XCD-local merge is off
+            // from now on, and the step (which wrote nothing but its own
+            // layers' KV rows for this position) runs again.
+            step_.x_part_local = nullptr;
+            return decode_step(id, host_logits, argmax);
+        }
         check(false, "decode step timed out waiting for another block", LH_ERROR_DEVICE);
     }
     if (!step_trace_path_.empty()) {
