@@ -55,6 +55,7 @@ struct StepParams {
     // merge waves of a head pair then sit on one XCD (block b runs on XCD b % 8), the items write
     // with plain stores that stay in that XCD's L2 and the merge waves read them from there.
     unsigned long long* x_part_local = nullptr;
+    int xcd_check_flip = 0;                     // tests: nonzero makes the XCD check fail (forces the fallback)
     unsigned long long* x_best = nullptr;       // per-block argmax candidates [blocks][2]
     unsigned* counters = nullptr;               // [kv_heads] span arrivals (zero between uses)
     unsigned* abort_flag = nullptr;             // set when a wait times out (device copy, polled by blocks)

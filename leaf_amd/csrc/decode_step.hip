@@ -1298,7 +1298,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         for (int i = t; i < words; i += kT) dst[i] = ldg(src + i);
     }
     __syncthreads();
-    if (P.x_part_local && t == 0 && xcc_id() != (b & 7)) raise_abort(P, kAbortXcdMapping);
+    if (P.x_part_local && t == 0 && (xcc_id() ^ P.xcd_check_flip) != (b & 7)) raise_abort(P, kAbortXcdMapping);
     const bool ok = wave < kA ? exchange_role(P, s) : weight_role(P, s);
     if (__syncthreads_or(!ok)) return;          // every wave leaves when one gave up (abort flags raised)
 

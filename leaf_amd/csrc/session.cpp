@@ -365,6 +365,9 @@ void Session::step_prepare() {
         step_part_local_.allocate(part * 8);
         hip_check(hipMemset(step_part_local_.ptr, 0, step_part_local_.bytes), "hipMemset");
         p.x_part_local = step_part_local_.as<unsigned long long>();
+        // LEAF_DECODE_STEP_FORCE_XCD_MISMATCH=1 (tests): the first step's XCD
+        // check fails, so the fallback to the memory-based merge runs.
+        if (const char* flip = std::getenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH")) p.xcd_check_flip = std::atoi(flip) ? 8 : 0;
     }
     p.counters = reinterpret_cast<unsigned*>(w);
     p.abort_flag = p.counters + c.kv_heads;

@@ -159,6 +159,29 @@ def test_step_and_graph_paths_agree(rt, small, monkeypatch):
     assert rel_rmse(runs[0], runs[1]) <= W8A8_RMSE_TOLERANCE
 
 
+def test_xcd_local_merge_matches_the_memory_merge(rt, wide, monkeypatch):
+    # At TinyLlama widths the span partials of each head pair go through one
+    # XCD's L2; with LEAF_DECODE_STEP_LOCAL_MERGE=0 they go through memory,
+    # and with a (host-forced) failed XCD check the first step aborts and
+    # runs again on the memory path.  Same arithmetic: identical logits.
+    feed = (np.arange(12, dtype=np.uint32) * 131 + 7) % 32000
+    prompt = np.arange(1, 90, dtype=np.uint32) * 11
+    runs = []
+    for local, force in (("1", "0"), ("0", "0"), ("1", "1")):
+        monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_MERGE", local)
+        monkeypatch.setenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH", force)
+        dec = rt.Decoder(wide, 8)
+        dec.set_profiling(True)
+        dec.forward(prompt)
+        rows = [dec.forward([int(tok)]) for tok in feed]
+        steps = dec.profile().get("decode_step", {}).get("launches", 0)
+        dec.close()
+        runs.append(np.stack(rows))
+        assert steps >= len(feed)
+    assert np.array_equal(runs[0], runs[1])
+    assert np.array_equal(runs[0], runs[2])
+
+
 def test_step_is_deterministic_across_reset(rt, small):
     dec = rt.Decoder(small, 8)
     prompt = np.arange(3, 53, dtype=np.uint32)
