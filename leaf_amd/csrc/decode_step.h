@@ -56,6 +56,9 @@ struct StepParams {
     // with plain stores that stay in that XCD's L2 and the merge waves read them from there.
     unsigned long long* x_part_local = nullptr;
     int xcd_check_flip = 0;                     // tests: nonzero makes the XCD check fail (forces the fallback)
+    // The q rows of each head slice, in plain device memory, for XCD-local q (null: off): the
+    // rows of a slice are computed on its XCD and its items read them from that XCD's L2.
+    unsigned long long* x_q_local = nullptr;
     unsigned long long* x_best = nullptr;       // per-block argmax candidates [blocks][2]
     unsigned* counters = nullptr;               // [kv_heads] span arrivals (zero between uses)
     unsigned* abort_flag = nullptr;             // set when a wait times out (device copy, polled by blocks)

@@ -736,7 +736,8 @@ struct Ownership {
 // weight 0.
 template <int HPW>
 __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, int lane, int aw, int h0, int h_end,
-                                               int keys, u64* parts, unsigned epoch, bool local) {
+                                               int keys, u64* parts, unsigned epoch, bool local,
+                                               float* keep = nullptr) {
     // plain stores (they stay in this XCD's L2) for the XCD-local merge
     auto put = [&](u64* p, float v) {
         if (local) __hip_atomic_store((LEAF_GLOBAL u64*)p, tagged(epoch, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
@@ -795,6 +796,13 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[h] = fmaf(e4[h][j], v[j], o[h]);
     }
+    if (keep) {
+        // the caller folds the new key in and publishes (one head per wave)
+        keep[0] = m[0];
+        keep[1] = l[0];
+        keep[2] = o[0];
+        return;
+    }
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
         const int gh = h0 + aw + kA * h;
@@ -807,6 +815,57 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
             }
         }
     }
+}
+
+// How a step lays out its attention (both roles compute the same plan).
+// Items are (KV head, span of keys, slice of the group's query heads);
+// slices are as narrow as the grid allows (hpw heads per exchange wave).
+// Local mode deals the head slices to the XCDs round robin (slice sigma to
+// XCD sigma % 8): its span items and its merge block run there and the span
+// partials go through that XCD's L2.  Local q also computes a slice's q rows
+// on its XCD (each block of XCD x owns `qkv_per_block` consecutive entries of
+// the list: q pairs of slices x, x + 8, ..., then 1/8 of the k|v pairs), so
+// the items read q from L2 as well; the new key's k and v still travel
+// through memory, and an item folds that key in after its cached keys.
+struct AttnPlan {
+    int begin, end, spans, hpw, slices, S, per;
+    bool local, local_q;
+    int qkv_per_xcd, qkv_per_block;
+};
+__device__ __forceinline__ AttnPlan attn_plan(const StepParams& P, int G) {
+    AttnPlan a;
+    const int group = P.heads / P.kv_heads;
+    a.end = P.position + 1;
+    a.begin = (P.window > 0 && a.end > P.window) ? a.end - P.window : 0;
+    a.spans = (a.end - a.begin + kStepSpanKeys - 1) / kStepSpanKeys;
+    a.hpw = 1;
+    while (a.hpw < kHeadsA && a.hpw < P.item_heads) a.hpw *= 2;
+    while (a.hpw < kHeadsA && P.kv_heads * a.spans * ((group + kA * a.hpw - 1) / (kA * a.hpw)) > G) a.hpw *= 2;
+    a.slices = (group + kA * a.hpw - 1) / (kA * a.hpw);
+    a.S = P.kv_heads * a.slices;
+    a.per = a.S / 8;
+    a.local = P.x_part_local && a.hpw == 1 && G % 8 == 0 && a.S % 8 == 0 && a.per * a.spans <= G / 8;
+    constexpr int pairs_per_head = kStepDim / 2;
+    a.qkv_per_xcd = a.per * kA * pairs_per_head + 2 * P.kv_heads * pairs_per_head / 8;
+    a.qkv_per_block = G >= 8 ? (a.qkv_per_xcd + G / 8 - 1) / (G / 8) : 0;
+    a.local_q = a.local && P.x_q_local && group % kA == 0 && a.qkv_per_block <= kQP * kB;
+    return a;
+}
+
+// Rotate-half pair `i` (of the plan's qkv_per_block) of block b in local-q
+// mode, or -1 past the block's share.
+__device__ __forceinline__ int local_qkv_pair(const AttnPlan& a, const StepParams& P, int b, int i) {
+    constexpr int pairs_per_head = kStepDim / 2;
+    const int group = P.heads / P.kv_heads;
+    const int x = b & 7, e = (b >> 3) * a.qkv_per_block + i;
+    if (i >= a.qkv_per_block || e >= a.qkv_per_xcd) return -1;
+    const int qpairs = a.per * kA * pairs_per_head;
+    if (e < qpairs) {
+        const int sigma = x + 8 * (e / (kA * pairs_per_head)), w = e % (kA * pairs_per_head);
+        const int head = sigma / a.slices * group + sigma % a.slices * kA + w / pairs_per_head;
+        return head * pairs_per_head + w % pairs_per_head;
+    }
+    return P.heads * pairs_per_head + x * (2 * P.kv_heads * pairs_per_head / 8) + (e - qpairs);
 }
 
 // ======================================================= exchange role ===
@@ -824,21 +883,10 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     // this block's attention item: (KV head, span of keys, slice of the
     // group's query heads).  Slices are as narrow as the grid allows (hpw
     // heads per exchange wave): an item's time grows with its heads.
-    const int end = pos + 1;
-    const int begin = (P.window > 0 && end > P.window) ? end - P.window : 0;
-    const int spans = (end - begin + kStepSpanKeys - 1) / kStepSpanKeys;
-    int hpw = 1;
-    while (hpw < kHeadsA && hpw < P.item_heads) hpw *= 2;
-    while (hpw < kHeadsA && P.kv_heads * spans * ((group + kA * hpw - 1) / (kA * hpw)) > G) hpw *= 2;
-    const int slices = (group + kA * hpw - 1) / (kA * hpw);
-    // XCD-local merge: head slices (kA heads, one merge block each) are dealt
-    // to the XCDs round robin, slice sigma to XCD sigma % 8; its span items
-    // and its merge block run on blocks of that XCD (block b on XCD b % 8,
-    // checked at kernel start), so the partials travel through that XCD's
-    // L2 instead of memory.  It needs one head per exchange wave, slices
-    // spread evenly over the XCDs, and room for their items on each XCD.
-    const int S = P.kv_heads * slices, per = S / 8;
-    const bool local = P.x_part_local && hpw == 1 && G % 8 == 0 && S % 8 == 0 && per * spans <= G / 8;
+    const AttnPlan plan = attn_plan(P, G);
+    const int end = plan.end, begin = plan.begin, spans = plan.spans, hpw = plan.hpw, slices = plan.slices;
+    const int per = plan.per;
+    const bool local = plan.local;
     int sigma = -1, merge_sigma = -1;      // this block's item slice and merge slice (local mode)
     bool has_item;
     int item_g, item_s, item_h0;
@@ -927,7 +975,56 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         // head's span of keys for all heads of its group and publish (max,
         // sum, unnormalized output) per head; merge waves (one per query head,
         // in the last blocks) combine the spans as soon as they land.
-        if (has_item) {
+        if (has_item && plan.local_q) {
+            // q of this item's kA heads from this XCD's L2; the span's
+            // cached keys first, then (last span) the new key folded in
+            const int kv_word = a < dim ? qw + item_g * dim + a : qw + kvw + item_g * dim + (a - dim);
+            float got2[2];
+            const bool ok_q = wait_published(s, 4 * L + 1) &&
+                              await_runs<2, 0, false>(P.x_q_local + (item_g * group + item_h0) * dim, kA * dim,
+                                                      epoch(L, 1), got2, a, P);
+            if (!a_check(ok_q, s, P)) return false;
+            stamp(P.trace, b, 64 * L + 3);
+            if (a < kA * dim / 2) *reinterpret_cast<v2f*>(s.q + item_h0 * dim + 2 * a) = v2f{got2[0], got2[1]};
+            if (!a_sync(s, round)) return false;
+            stamp(P.trace, b, 64 * L + 56);
+            float keep[3];
+            attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys - (new_key ? 1 : 0), nullptr, epoch(L, 2),
+                              true, keep);
+            float m = keep[0], l = keep[1], o = keep[2];
+            if (new_key) {
+                float kv_got;
+                if (!a_check(await_one(P.x_qkv + kv_word, a < 2 * dim, epoch(L, 1), kv_got, P), s, P)) return false;
+                if (!a_sync(s, round)) return false;   // both waves are done with the cached rows
+                const int nl = pos - k0;
+                if (a < dim) s.k[nl * kKStride + a] = kv_got;
+                else s.v[nl * dim + (a - dim)] = kv_got;
+                if (!a_sync(s, round)) return false;
+                // fold key nl in: rescale the cached keys' partials to the new max
+                const int gh = min(item_h0 + aw, item_h1 - 1);
+                const float qd = s.q[gh * dim + lane], kd = s.k[nl * kKStride + lane], vd = s.v[nl * dim + lane];
+                const float sn = dpp_sum_f32(qd * kd) * P.attention_scale * P.attention_scale;
+                const float mn = fmaxf(m, sn);
+                const float alpha = expf(m - mn), beta = expf(sn - mn);
+                l = l * alpha + beta;
+                o = fmaf(o, alpha, beta * vd);
+                m = mn;
+            }
+            const int gh = item_h0 + aw;
+            if (gh < item_h1) {
+                u64* part = part_base + ((size_t)(item_g * spans + item_s) * group + gh) * (dim + 2);
+                const unsigned e2 = epoch(L, 2);
+                __hip_atomic_store((LEAF_GLOBAL u64*)(part + 2 + lane), tagged(e2, o), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WAVEFRONT);
+                if (lane == 0) {
+                    __hip_atomic_store((LEAF_GLOBAL u64*)part, tagged(e2, m), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+                    __hip_atomic_store((LEAF_GLOBAL u64*)(part + 1), tagged(e2, l), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+                }
+            }
+            stamp(P.trace, b, 64 * L + 57);
+        } else if (has_item) {
             // q of the group's heads, and the new key's k (lanes < dim) or v
             // (the q|k|v buffer is padded so a lane's runs stay inside it)
             float got[kNQ - 1], kv_got;
@@ -1073,13 +1170,14 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     auto epoch = [&](int layer, int phase) { return P.epoch + (unsigned)(layer * 8 + phase); };
     const Ownership own(P, b, G);
 
+    const AttnPlan plan = attn_plan(P, G);
     int qr[kQP][2];
     bool has_q[kQP], has_r[kOR], has_g[kGP];
     float rope_c[kQP], rope_s[kQP];
 #pragma unroll
     for (int k = 0; k < kQP; ++k) {
-        const int p = own.q_first + bw + kB * k;
-        has_q[k] = p < own.q_end;
+        const int p = plan.local_q ? local_qkv_pair(plan, P, b, bw + kB * k) : own.q_first + bw + kB * k;
+        has_q[k] = plan.local_q ? p >= 0 : p < own.q_end;
         qr[k][0] = qr[k][1] = 0;
         rope_c[k] = 1.0f;
         rope_s[k] = 0.0f;
@@ -1178,8 +1276,16 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                             v0 = x0;
                             v1 = x1;
                         }
-                        publish(P.x_qkv + r0, epoch(L, 1), v0);
-                        publish(P.x_qkv + r1, epoch(L, 1), v1);
+                        if (plan.local_q && hb < P.heads) {
+                            // a q row of this XCD's head slices: plain stores, read from L2
+                            __hip_atomic_store((LEAF_GLOBAL u64*)(P.x_q_local + r0), tagged(epoch(L, 1), v0),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                            __hip_atomic_store((LEAF_GLOBAL u64*)(P.x_q_local + r1), tagged(epoch(L, 1), v1),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                        } else {
+                            publish(P.x_qkv + r0, epoch(L, 1), v0);
+                            publish(P.x_qkv + r1, epoch(L, 1), v1);
+                        }
                         if (hb >= P.heads) {
                             float* dst = hb < P.heads + P.kv_heads
                                              ? Kc + ((size_t)(hb - P.heads) * P.capacity + pos) * dim

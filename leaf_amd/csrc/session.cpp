@@ -365,6 +365,14 @@ void Session::step_prepare() {
         step_part_local_.allocate(part * 8);
         hip_check(hipMemset(step_part_local_.ptr, 0, step_part_local_.bytes), "hipMemset");
         p.x_part_local = step_part_local_.as<unsigned long long>();
+        // and the q rows of each head slice, read by that slice's items
+        // (LEAF_DECODE_STEP_LOCAL_Q=0 turns this part off)
+        const char* local_q = std::getenv("LEAF_DECODE_STEP_LOCAL_Q");
+        if (!(local_q && std::string(local_q) == "0")) {
+            step_q_local_.allocate(qkv_words * 8);
+            hip_check(hipMemset(step_q_local_.ptr, 0, step_q_local_.bytes), "hipMemset");
+            p.x_q_local = step_q_local_.as<unsigned long long>();
+        }
         // LEAF_DECODE_STEP_FORCE_XCD_MISMATCH=1 (tests): the first step's XCD
         // check fails, so the fallback to the memory-based merge runs.
         if (const char* flip = std::getenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH")) p.xcd_check_flip = std::atoi(flip) ? 8 : 0;
@@ -437,6 +445,7 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
         hip_check(hipMemsetAsync(step_exchange_.ptr, 0, step_exchange_.bytes, s), "hipMemsetAsync");
         if (step_part_local_.ptr)
             hip_check(hipMemsetAsync(step_part_local_.ptr, 0, step_part_local_.bytes, s), "hipMemsetAsync");
+        if (step_q_local_.ptr) hip_check(hipMemsetAsync(step_q_local_.ptr, 0, step_q_local_.bytes, s), "hipMemsetAsync");
         step_launch_ = 1;
     }
     StepParams p = step_;
@@ -463,12 +472,14 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
         *step_host_abort_ = 0;
         hip_check(hipMemset(step_exchange_.ptr, 0, step_exchange_.bytes), "hipMemset");
         if (step_part_local_.ptr) hip_check(hipMemset(step_part_local_.ptr, 0, step_part_local_.bytes), "hipMemset");
+        if (step_q_local_.ptr) hip_check(hipMemset(step_q_local_.ptr, 0, step_q_local_.bytes), "hipMemset");
         step_token_valid_ = false;
         if (why == 2 && step_.x_part_local) {
             // A block ran off XCD blockIdx % 8: the XCD-local merge is off
             // from now on, and the step (which wrote nothing but its own
             // layers' KV rows for this position) runs again.
             step_.x_part_local = nullptr;
+            step_.x_q_local = nullptr;
             return decode_step(id, host_logits, argmax);
         }
         check(false, "decode step timed out waiting for another block", LH_ERROR_DEVICE);

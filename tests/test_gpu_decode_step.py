@@ -159,16 +159,21 @@ def test_step_and_graph_paths_agree(rt, small, monkeypatch):
     assert rel_rmse(runs[0], runs[1]) <= W8A8_RMSE_TOLERANCE
 
 
-def test_xcd_local_merge_matches_the_memory_merge(rt, wide, monkeypatch):
+def test_xcd_local_attention_matches_the_memory_path(rt, wide, oracle, monkeypatch):
     # At TinyLlama widths the span partials of each head pair go through one
-    # XCD's L2; with LEAF_DECODE_STEP_LOCAL_MERGE=0 they go through memory,
-    # and with a (host-forced) failed XCD check the first step aborts and
-    # runs again on the memory path.  Same arithmetic: identical logits.
+    # XCD's L2 (LEAF_DECODE_STEP_LOCAL_MERGE), and so do the q rows of the
+    # pair, with the new key folded into its span after the cached keys
+    # (LEAF_DECODE_STEP_LOCAL_Q).  The local merge moves the same words: with
+    # it alone the logits equal those of the memory path, and so do those of
+    # a run whose (host-forced) failed XCD check makes the first step abort
+    # and every step fall back.  The late fold sums in another order: those
+    # logits stay within the decode step's bounds of the oracle.
     feed = (np.arange(12, dtype=np.uint32) * 131 + 7) % 32000
     prompt = np.arange(1, 90, dtype=np.uint32) * 11
     runs = []
-    for local, force in (("1", "0"), ("0", "0"), ("1", "1")):
-        monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_MERGE", local)
+    for merge, q, force in (("1", "0", "0"), ("0", "0", "0"), ("1", "1", "1"), ("1", "1", "0")):
+        monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_MERGE", merge)
+        monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_Q", q)
         monkeypatch.setenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH", force)
         dec = rt.Decoder(wide, 8)
         dec.set_profiling(True)
@@ -179,7 +184,13 @@ def test_xcd_local_merge_matches_the_memory_merge(rt, wide, monkeypatch):
         runs.append(np.stack(rows))
         assert steps >= len(feed)
     assert np.array_equal(runs[0], runs[1])
-    assert np.array_equal(runs[0], runs[2])
+    assert np.array_equal(runs[2], runs[1])
+    od = oracle.decoder(wide, 8, False)
+    od.forward(prompt)
+    ref = np.stack([od.forward([int(tok)]) for tok in feed])
+    for got in runs[3], runs[1]:
+        assert max(rel_error(x, y) for x, y in zip(got, ref)) <= W8A8_LOGIT_TOLERANCE
+        assert max(rel_rmse(x, y) for x, y in zip(got, ref)) <= W8A8_RMSE_TOLERANCE
 
 
 def test_step_is_deterministic_across_reset(rt, small):
