@@ -1298,10 +1298,6 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 9 + 8 * bw, kAT + kWave * bw);
-        // this layer's first down row: the attention that follows reads
-        // little from memory, and the norm and q|k|v phases are over (the
-        // second goes out with the o prefetch, after the x_mid hop)
-        load_down(layer_at(s, L), true, 0, 1);
         if (!wait_received(s, 4 * L + 1)) return false;
         load_qkv(next, more);
         // ---- o_proj + residual
@@ -1326,7 +1322,11 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 11 + 8 * bw, kAT + kWave * bw);
         if (!wait_received(s, 4 * L + 2)) return false;
         load_o(next, more);
-        load_down(layer_at(s, L), true, 1, kOR);
+        // this layer's down rows (free since the last layer's down phase):
+        // with the attention's reads and stores now in XCD-local L2, a load
+        // burst in the attention window slowed the items down (640 against
+        // 635 us per token with them here)
+        load_down(layer_at(s, L), true);
         // ---- gate|up + SiLU gate
         if (!wait_ready(s, 4 * L + 2)) return false;
         stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
