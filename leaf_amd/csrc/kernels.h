@@ -39,6 +39,12 @@ void launch_embedding(const WeightView& table, const WeightView* positions, cons
                       const int* position_ptr = nullptr);
 void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream);
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream);
+// norm_kernel + quantize_kernel in one launch (same q and scales, no f32 row in between)
+void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
+                          hipStream_t stream);
+// activation_kernel + quantize_kernel in one launch
+void launch_activation_quantize(const float* gate_up, int tokens, int width, int gated, int activation, int8_t* q,
+                                float* scales, hipStream_t stream);
 void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y,
                           hipStream_t stream);
 

@@ -112,6 +112,27 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, int wi
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = (int8_t)quantize_one(in[c], multiplier);
 }
 
+// A row's norm and its per-token int8 quantization in one pass over the
+// block: the statistics of norm_kernel, then the absmax of the normalized
+// values and their quantization as quantize_kernel does them (recomputing
+// each normalized value with the same expression), so q and the scale are
+// bit-identical to the two kernels in sequence without the f32 round trip.
+__global__ __launch_bounds__(kBlock) void norm_quantize_kernel(const float* x, int width, NormView norm, int8_t* q,
+                                                              float* scales) {
+    __shared__ float scratch[16];
+    const float* in = x + (size_t)blockIdx.x * width;
+    const NormStats st = block_norm_stats(in, width, norm, scratch);
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) m = fmaxf(m, fabsf(apply_norm(in[c], c, st, norm)));
+    m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    const float s = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / s;
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x)
+        out[c] = (int8_t)quantize_one(apply_norm(in[c], c, st, norm), multiplier);
+}
+
 __global__ void scale_columns_kernel(const float* x, int width, size_t count, const float* factors, float* y) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
         y[i] = x[i] * factors[i % width];
@@ -1336,6 +1357,23 @@ __global__ void activation_kernel(const float* gate_up, int tokens, int width, i
     }
 }
 
+// The MLP activation of a token row (as activation_kernel computes it) and
+// its per-token int8 quantization (as quantize_kernel does it) in one pass.
+__global__ __launch_bounds__(kBlock) void activation_quantize_kernel(const float* gate_up, int width, int gated,
+                                                                    int activation, int8_t* q, float* scales) {
+    __shared__ float scratch[16];
+    const float* in = gate_up + (size_t)blockIdx.x * width * (gated ? 2 : 1);
+    auto value = [&](int j) { return gated ? in[width + j] * activate(activation, in[j]) : activate(activation, in[j]); };
+    float m = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) m = fmaxf(m, fabsf(value(j)));
+    m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    const float s = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / s;
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) out[j] = (int8_t)quantize_one(value(j), multiplier);
+}
+
 __global__ void residual_kernel(float* hidden, const float* a, const float* b, int count) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
         hidden[i] = hidden[i] + (a[i] + (b ? b[i] : 0.0f));
@@ -1461,6 +1499,16 @@ void launch_norm(const float* x, int rows, int width, const NormView& norm, floa
 
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {
     quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, q, scales);
+}
+
+void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
+                          hipStream_t stream) {
+    norm_quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales);
+}
+
+void launch_activation_quantize(const float* gate_up, int tokens, int width, int gated, int activation, int8_t* q,
+                                float* scales, hipStream_t stream) {
+    activation_quantize_kernel<<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q, scales);
 }
 
 void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y, hipStream_t stream) {

@@ -202,7 +202,11 @@ private:
     LinearCall make_call(const Linear& l, const float* x, int tokens, float* y, int epilogue,
                          const NormView* fuse_norm);
     void run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue, const NormView* fuse_norm,
-                    const PairEpilogue* pair = nullptr);
+                    const PairEpilogue* pair = nullptr, bool prequantized = false);
+    // Whether a multi-token integer linear can take its input quantized by a
+    // fused norm or activation kernel (into xq_ / xs_).
+    bool prequantizes(const Linear& l, int tokens) const;
+    bool fuse_quantize_ = true;   // LEAF_PREFILL_FUSE=0 turns the fused norm / activation quantization off
     template <typename F> void timed(int kind, double bytes, double ops, F&& launch) {
         if (profiler.enabled) profiler.begin(stream());
         launch();

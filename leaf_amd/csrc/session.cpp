@@ -99,6 +99,8 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m
     const char* graphs = std::getenv("LEAF_DECODE_GRAPH");
     graphs_enabled_ = !(graphs && std::string(graphs) == "0");
     plan(max_prefill ? max_prefill : 512, false);
+    const char* fuse = std::getenv("LEAF_PREFILL_FUSE");
+    fuse_quantize_ = !(fuse && std::string(fuse) == "0");
     const char* step = std::getenv("LEAF_DECODE_STEP");
     step_enabled_ = !(step && std::string(step) == "0");
     if (step_enabled_) step_prepare();
@@ -161,8 +163,12 @@ LinearCall Session::make_call(const Linear& l, const float* x, int tokens, float
     return call;
 }
 
+bool Session::prequantizes(const Linear& l, int tokens) const {
+    return fuse_quantize_ && tokens > 1 && model.integer_linear(l) && !l.input_scale;
+}
+
 void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue,
-                         const NormView* fuse_norm, const PairEpilogue* pair) {
+                         const NormView* fuse_norm, const PairEpilogue* pair, bool prequantized) {
     LinearCall call;
     call.w = l.view;
     call.tokens = tokens;
@@ -180,6 +186,12 @@ void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, 
         x = scaled_.as<float>();
     }
     call.x = x;
+    if (prequantized) {
+        // xq_ / xs_ already hold this input quantized per token
+        call.x = nullptr;
+        call.xq = xq_.as<int8_t>();
+        call.xs = xs_.as<float>();
+    }
     if (fuse_norm) call.norm = *fuse_norm;
     if (pair) call.pair = *pair;
     // Algorithmic traffic: weights, scales, activations (int8 when quantized),
@@ -549,6 +561,12 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm, &rope);
         } else if (fuse_in) {
             run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
+        } else if (L.stacked_qkv && prequantizes(L.qkv, M)) {
+            // norm + per-token quantization in one launch, then the GEMM
+            timed(Profiler::Other, 0, 0, [&] {
+                launch_norm_quantize(hidden, M, h, L.input_norm, xq_.as<int8_t>(), xs_.as<float>(), s);
+            });
+            run_linear(L.qkv, nullptr, M, qkv, kStore, nullptr, nullptr, true);
         } else {
             launch_norm(hidden, M, h, L.input_norm, normed, s);
             if (L.stacked_qkv) {
@@ -640,6 +658,11 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                 run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm, &gated);
             } else if (fuse_post) {
                 run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm);
+            } else if (L.stacked_gate_up && prequantizes(L.gate_up, rows)) {
+                timed(Profiler::Other, 0, 0, [&] {
+                    launch_norm_quantize(hid, rows, h, L.post_norm, xq_.as<int8_t>(), xs_.as<float>(), s);
+                });
+                run_linear(L.gate_up, nullptr, rows, gate_up, kStore, nullptr, nullptr, true);
             } else {
                 launch_norm(hid, rows, h, L.post_norm, normed, s);
                 if (L.stacked_gate_up) {
@@ -656,17 +679,26 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                     }
                 }
             }
-            if (!fuse_act) timed(Profiler::Other, 0, 0, [&] { launch_activation(gate_up, rows, f, 1, int(c.activation), act, s); });
+            if (!fuse_act && !prequantizes(L.down, rows))
+                timed(Profiler::Other, 0, 0, [&] { launch_activation(gate_up, rows, f, 1, int(c.activation), act, s); });
         } else {
             launch_norm(hid, rows, h, L.post_norm, normed, s);
             run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
             launch_activation(gate_up, rows, f, 0, int(c.activation), act, s);
         }
+        const bool down_q = c.gated && prequantizes(L.down, rows) &&
+                            !(rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up);
+        if (down_q) {
+            // the gated activation and its quantization in one launch
+            timed(Profiler::Other, 0, 0, [&] {
+                launch_activation_quantize(gate_up, rows, f, 1, int(c.activation), xq_.as<int8_t>(), xs_.as<float>(), s);
+            });
+        }
         if (!c.parallel) {
-            run_linear(L.down, act, rows, hid, kAccumulate, nullptr);         // hidden += down(act) + b
+            run_linear(L.down, act, rows, hid, kAccumulate, nullptr, nullptr, down_q);   // hidden += down(act) + b
         } else {
             float* proj = proj_.as<float>();
-            run_linear(L.down, act, rows, proj, kStore, nullptr);
+            run_linear(L.down, act, rows, proj, kStore, nullptr, nullptr, down_q);
             launch_residual(hid, proj, attn_proj, rows * h, s);              // hidden += proj + attn_proj
         }
         if (trim) hidden = hid;   // the final norm and head see only the last row
