@@ -133,6 +133,75 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_kernel(const float* x, i
         out[c] = (int8_t)quantize_one(apply_norm(in[c], c, st, norm), multiplier);
 }
 
+// The same row norm + quantization with the row held in registers: thread t
+// owns columns t + k * kBlock (k < K), so every load of the row is issued up
+// front instead of once per pass.  Each thread sums its columns in the same
+// order as block_norm_stats and the reductions are the same, so q and the
+// scale are bit-identical to norm_quantize_kernel.
+template <int K>
+__global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float* x, int width, NormView norm,
+                                                                   int8_t* q, float* scales) {
+    __shared__ float scratch[16];
+    const float* in = x + (size_t)blockIdx.x * width;
+    float v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = threadIdx.x + k * kBlock;
+        v[k] = c < width ? in[c] : 0.0f;
+    }
+    float mean = 0.0f;
+    if (norm.kind == 1) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) if (threadIdx.x + k * kBlock < width) s += v[k];
+        s = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
+        mean = s / (float)width;
+    }
+    float square;
+    if (norm.kind == 0 && norm.accurate) {
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (threadIdx.x + k * kBlock < width) { const float w = v[k] * v[k]; s += (double)w; }
+        __shared__ double dscratch[16];
+        s = block_reduce<double>(s, dscratch, [](double a, double b) { return a + b; }, wave_sum_f64);
+        square = (float)s;
+    } else {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (threadIdx.x + k * kBlock < width) { const float w = v[k] - mean; s += w * w; }
+        square = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
+    }
+    NormStats st;
+    st.mean = mean;
+    st.scale = 1.0f / sqrtf(square / (float)width + norm.epsilon);
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = threadIdx.x + k * kBlock;
+        if (c < width) { v[k] = apply_norm(v[k], c, st, norm); m = fmaxf(m, fabsf(v[k])); }
+    }
+    m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    const float sc = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sc;
+    if (threadIdx.x == 0) scales[blockIdx.x] = sc;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = threadIdx.x + k * kBlock;
+        if (c < width) out[c] = (int8_t)quantize_one(v[k], multiplier);
+    }
+}
+
+// Columns per thread for the register-row kernels (0: the row does not fit).
+int row_registers(int width) {
+    const int k = (width + kBlock - 1) / kBlock;
+    for (int c : {1, 2, 4, 8, 12, 16, 24, 32})
+        if (k <= c) return c;
+    return 0;
+}
+
 __global__ void scale_columns_kernel(const float* x, int width, size_t count, const float* factors, float* y) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
         y[i] = x[i] * factors[i % width];
@@ -1374,6 +1443,50 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_kernel(const float
     for (int j = threadIdx.x; j < width; j += blockDim.x) out[j] = (int8_t)quantize_one(value(j), multiplier);
 }
 
+// activation_quantize_kernel with the row held in registers (thread t owns
+// columns t + k * kBlock); each activation is computed once.  Same values,
+// reductions and roundings: q and the scale are bit-identical.
+template <int K>
+__global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const float* gate_up, int width, int gated,
+                                                                         int activation, int8_t* q, float* scales) {
+    __shared__ float scratch[16];
+    const float* in = gate_up + (size_t)blockIdx.x * width * (gated ? 2 : 1);
+    float a[K];
+    if (gated) {
+        float u[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int j = threadIdx.x + k * kBlock;
+            a[k] = j < width ? in[j] : 0.0f;
+            u[k] = j < width ? in[width + j] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) a[k] = u[k] * activate(activation, a[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int j = threadIdx.x + k * kBlock;
+            a[k] = j < width ? in[j] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) a[k] = activate(activation, a[k]);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if (threadIdx.x + k * kBlock < width) m = fmaxf(m, fabsf(a[k]));
+    m = block_reduce<float>(m, scratch, [](float x, float y) { return fmaxf(x, y); }, wave_max_f32);
+    const float s = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / s;
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = threadIdx.x + k * kBlock;
+        if (j < width) out[j] = (int8_t)quantize_one(a[k], multiplier);
+    }
+}
+
 __global__ void residual_kernel(float* hidden, const float* a, const float* b, int count) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
         hidden[i] = hidden[i] + (a[i] + (b ? b[i] : 0.0f));
@@ -1503,12 +1616,26 @@ void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scal
 
 void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
                           hipStream_t stream) {
-    norm_quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales);
+    switch (row_registers(width)) {
+#define LEAF_ROWS(K) case K: norm_quantize_rows_kernel<K><<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales); break;
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+#undef LEAF_ROWS
+        default: norm_quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales);
+    }
 }
 
 void launch_activation_quantize(const float* gate_up, int tokens, int width, int gated, int activation, int8_t* q,
                                 float* scales, hipStream_t stream) {
-    activation_quantize_kernel<<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    switch (row_registers(width)) {
+#define LEAF_ROWS(K)                                                                                               \
+    case K:                                                                                                        \
+        activation_quantize_rows_kernel<K><<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q,    \
+                                                                         scales);                                  \
+        break;
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+#undef LEAF_ROWS
+        default: activation_quantize_kernel<<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    }
 }
 
 void launch_scale_columns(const float* x, int rows, int width, const float* factors, float* y, hipStream_t stream) {
