@@ -1091,7 +1091,10 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int 
 
 // ----------------------------------------- prefill attention: f32 MFMA ---
 // Flash attention for head dim 64 (every supported decoder family).  A block
-// owns one query head and 64 tokens; wave w owns tokens t0 + 16w .. +15.  Key
+// owns one query head and 64 tokens; waves w and w + 4 own tokens
+// t0 + 16w .. +15, wave w the even 16-key slices of each key tile and wave
+// w + 4 the odd ones, each with its own online softmax; the two states merge
+// at the end (two waves per SIMD, so one's MFMAs overlap the other's softmax).  Key
 // tiles of 64 keys are staged in LDS (K and V, rows padded to 68 floats: the
 // MFMA operand reads then hit every bank twice, the minimum for 64 lanes),
 // the next tile waiting in registers while this one is used.
@@ -1107,15 +1110,16 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int 
 constexpr int kPrefillQ = 64;        // tokens per block
 constexpr int kPrefillKeys = 64;     // keys per LDS tile
 constexpr int kPrefillStride = 68;   // padded row of a K or V tile
+constexpr int kPrefillThreads = 512; // 8 waves
 
-// One thread's share of a 64 x 64 K (and V) tile: float4 i, i + 256, ... .
+// One thread's share of a 64 x 64 K (and V) tile: float4 i and i + 512.
 // Rows at or past `end` were never written (they may hold NaN, and a masked
 // key still multiplies its V row by 0): they are zeros.
-__device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end, v4f (&kr)[4],
-                                                  v4f (&vr)[4]) {
+__device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end, v4f (&kr)[2],
+                                                  v4f (&vr)[2]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int f = threadIdx.x + kBlock * j, row = f / 16, col = 4 * (f % 16);
+    for (int j = 0; j < 2; ++j) {
+        const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
         const int key = k0 + row;
         const bool ok = key < end;
         const size_t at = (size_t)(ok ? key : 0) * 64 + col;
@@ -1125,24 +1129,26 @@ __device__ __forceinline__ void prefill_tile_load(const float* K, const float* V
         vr[j] = ok ? vv : zero;
     }
 }
-__device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[4], const v4f (&vr)[4]) {
+__device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[2], const v4f (&vr)[2]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int f = threadIdx.x + kBlock * j, row = f / 16, col = 4 * (f % 16);
+    for (int j = 0; j < 2; ++j) {
+        const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
         *(v4f*)(ks + row * kPrefillStride + col) = kr[j];
         *(v4f*)(vs + row * kPrefillStride + col) = vr[j];
     }
 }
 
-__global__ __launch_bounds__(kBlock) void attention_prefill_kernel(AttentionCall p) {
-    __shared__ float ks[kPrefillKeys * kPrefillStride];
-    __shared__ float vs[kPrefillKeys * kPrefillStride];
+__global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(AttentionCall p) {
+    __shared__ float lds[2 * kPrefillKeys * kPrefillStride];
+    float* ks = lds;
+    float* vs = lds + kPrefillKeys * kPrefillStride;
     constexpr int dim = 64;
     const int h = blockIdx.x, t0 = blockIdx.y * kPrefillQ;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int group = wave & 3, half = wave >> 2;     // token group, key slice parity
     const int li = lane & 15, lj = lane >> 4;
     const int kvh = h / (p.heads / p.kv_heads);
-    const int tw = t0 + 16 * wave;                    // this wave's first token
+    const int tw = t0 + 16 * group;                   // this wave's first token
     const int q_tok = tw + li;                        // this lane's query (score columns)
     const int q_pos = p.position + q_tok;
     const bool q_live = q_tok < p.tokens;
@@ -1159,7 +1165,7 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(AttentionCall
     first &= ~(kPrefillKeys - 1);
     const float* K = p.keys + (size_t)kvh * p.capacity * dim;
     const float* V = p.values + (size_t)kvh * p.capacity * dim;
-    v4f kr[4], vr[4];
+    v4f kr[2], vr[2];
     prefill_tile_load(K, V, first, end, kr, vr);
     v4f o[4];   // O^T: dims 16 dc + 4 lj + i, query li
 #pragma unroll
@@ -1173,7 +1179,7 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(AttentionCall
         if (k0 + kPrefillKeys < end) prefill_tile_load(K, V, k0 + kPrefillKeys, end, kr, vr);
         // the keys this wave can see in this tile
         const int wave_end = min(end, p.position + min(tw + 16, p.tokens));
-        for (int sub = 0; sub < kPrefillKeys && k0 + sub < wave_end; sub += 16) {
+        for (int sub = 16 * half; sub < kPrefillKeys && k0 + sub < wave_end; sub += 32) {
             v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             const float* krow = ks + (sub + li) * kPrefillStride + lj;
 #pragma unroll
@@ -1213,6 +1219,32 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(AttentionCall
                     o[dc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * dc], e[r], o[dc], 0, 0, 0);
             }
         }
+    }
+    // merge the odd-slice state into the even-slice wave of the same tokens
+    constexpr int kMerge = 18;   // per lane: O^T (16), max, sum
+    __syncthreads();             // the last tile is no longer read
+    if (half == 1) {
+        float* dst = lds + (group * kWave + lane) * kMerge;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[4 * dc + i] = o[dc][i];
+        dst[16] = m;
+        dst[17] = l;
+    }
+    __syncthreads();
+    if (half == 1) return;
+    {
+        const float* src = lds + (group * kWave + lane) * kMerge;
+        const float m1 = src[16], l1 = src[17];
+        const float mt = fmaxf(m, m1);
+        const float a0 = m == -INFINITY ? 0.0f : expf(m - mt);
+        const float a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mt);
+        l = l * a0 + l1 * a1;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dc][i] = o[dc][i] * a0 + src[4 * dc + i] * a1;
     }
     if (q_live) {
         float* out = p.out + ((size_t)q_tok * p.heads + h) * dim;
@@ -1702,11 +1734,11 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         if (path == 3 && w.group == K && K % kGemmStage == 0) {
             const int tiles = ceil_div(w.rows, kGemmTile) * ceil_div(c.tokens, kGemmTile);
             const int steps = K / 64;
-            // Split K until the grid covers the CUs twice (two blocks per CU),
+            // Split K until the grid covers the CUs once (measured ahead of twice),
             // each split a whole number of stages, when a workspace is given.
             int splits = 1;
             const int stages = steps / (kGemmStage / 64);
-            while (c.split_scratch && tiles * splits < 512 && stages % (2 * splits) == 0 &&
+            while (c.split_scratch && tiles * splits < 256 && stages % (2 * splits) == 0 &&
                    stages / (2 * splits) >= 2 && (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
                 splits *= 2;
             dim3 grid(ceil_div(w.rows, kGemmTile), ceil_div(c.tokens, kGemmTile), splits);
@@ -1793,7 +1825,8 @@ bool launch_attention(const AttentionCall& call, hipStream_t stream) {
         if (splits == 1) per_split = total;
     }
     if (splits == 1 && call.tokens > 1 && call.dim == 64) {
-        attention_prefill_kernel<<<dim3(call.heads, (call.tokens + kPrefillQ - 1) / kPrefillQ), kBlock, 0, stream>>>(
+        attention_prefill_kernel<<<dim3(call.heads, (call.tokens + kPrefillQ - 1) / kPrefillQ), kPrefillThreads, 0,
+                                   stream>>>(
             call);
         return true;
     }

@@ -193,3 +193,24 @@ def test_configured_span_decode_matches_prefill(rt, full_artifacts, family, math
     assert e_step <= LOGIT_TOLERANCE
     assert e_chunk <= LOGIT_TOLERANCE
     assert int(np.argmax(stepped)) == int(np.argmax(whole)) == int(np.argmax(chunked))
+
+
+
+def test_tinyllama_fused_prefill_quantization_is_bit_identical(rt, full_artifacts, monkeypatch):
+    """At TinyLlama's shapes the 512-token prefill splits K in the q|k|v, o and
+    down GEMMs.  The norm / activation fused into the per-token quantization
+    (default) or run as separate kernels (LEAF_PREFILL_FUSE=0) must give the
+    same logits for every token, and again on a second, shorter prefill."""
+    path = full_artifacts("tinyllama")
+    prompt = np.random.default_rng(6).integers(0, 32000, 512).astype(np.uint32)
+    runs = []
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("LEAF_PREFILL_FUSE", fuse)
+        dec = rt.Decoder(path, 8, "fast", max_context=600, max_prefill=512)
+        first = dec.forward(prompt, all_logits=True)
+        dec.reset()
+        second = dec.forward(prompt[:40], all_logits=True)
+        dec.close()
+        runs.append((first, second))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
