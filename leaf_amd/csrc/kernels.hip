@@ -1090,11 +1090,14 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int 
 }
 
 // ----------------------------------------- prefill attention: f32 MFMA ---
-// Flash attention for head dim 64 (every supported decoder family).  A block
-// owns one query head and 64 tokens; waves w and w + 4 own tokens
-// t0 + 16w .. +15, wave w the even 16-key slices of each key tile and wave
-// w + 4 the odd ones, each with its own online softmax; the two states merge
-// at the end (two waves per SIMD, so one's MFMAs overlap the other's softmax).  Key
+// Flash attention for head dim 64 (every supported decoder family).  A work
+// item is one query head and 32 tokens; waves w + 2 s (w < 2, s <
+// kPrefillSlices) own tokens t0 + 16w .. +15, wave w + 2 s the 16-key slices
+// s, s + kPrefillSlices, ... of each key tile, each with its own online
+// softmax; the states merge at the end (several waves per SIMD, so one's
+// MFMAs overlap another's softmax).  Items are numbered token-tile-major, and
+// block b runs item b, then item n - 1 - b: a causal prefill's short and long
+// key ranges pair up, so every block does about the same work.  Key
 // tiles of 64 keys are staged in LDS (K and V, rows padded to 68 floats: the
 // MFMA operand reads then hit every bank twice, the minimum for 64 lanes),
 // the next tile waiting in registers while this one is used.
@@ -1107,18 +1110,25 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttentionCall p, int 
 // online per query (max and sum exchanged between the four lanes of a query),
 // scores are (q.k * scale) * scale and masked keys are -inf, as in
 // transformer.cpp:112-143; the output is divided by the sum at the end.
-constexpr int kPrefillQ = 64;        // tokens per block
+constexpr int kPrefillQ = 32;        // tokens per work item
+constexpr int kPrefillGroups = kPrefillQ / 16;
 constexpr int kPrefillKeys = 64;     // keys per LDS tile
 constexpr int kPrefillStride = 68;   // padded row of a K or V tile
-constexpr int kPrefillThreads = 512; // 8 waves
+constexpr int kPrefillSlices = 4;    // waves per 16-token group
+constexpr int kPrefillThreads = kPrefillGroups * kWave * kPrefillSlices;
+constexpr int kPrefillLoads = 1024 / kPrefillThreads;   // float4 of a 64 x 64 tile per thread
+constexpr int kPrefillMerge = 18;    // merge record per lane: O^T (16), max, sum
+constexpr int kPrefillLds = 2 * kPrefillKeys * kPrefillStride > (kPrefillSlices - 1) * kPrefillGroups * kWave * kPrefillMerge
+                                ? 2 * kPrefillKeys * kPrefillStride
+                                : (kPrefillSlices - 1) * kPrefillGroups * kWave * kPrefillMerge;
 
-// One thread's share of a 64 x 64 K (and V) tile: float4 i and i + 512.
+// One thread's share of a 64 x 64 K (and V) tile: float4 i, i + kPrefillThreads, ...
 // Rows at or past `end` were never written (they may hold NaN, and a masked
 // key still multiplies its V row by 0): they are zeros.
-__device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end, v4f (&kr)[2],
-                                                  v4f (&vr)[2]) {
+__device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end,
+                                                  v4f (&kr)[kPrefillLoads], v4f (&vr)[kPrefillLoads]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kPrefillLoads; ++j) {
         const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
         const int key = k0 + row;
         const bool ok = key < end;
@@ -1129,23 +1139,25 @@ __device__ __forceinline__ void prefill_tile_load(const float* K, const float* V
         vr[j] = ok ? vv : zero;
     }
 }
-__device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[2], const v4f (&vr)[2]) {
+__device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[kPrefillLoads],
+                                                   const v4f (&vr)[kPrefillLoads]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kPrefillLoads; ++j) {
         const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
         *(v4f*)(ks + row * kPrefillStride + col) = kr[j];
         *(v4f*)(vs + row * kPrefillStride + col) = vr[j];
     }
 }
 
-__global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(AttentionCall p) {
-    __shared__ float lds[2 * kPrefillKeys * kPrefillStride];
+// One work item: query head h, tokens t0 .. t0 + kPrefillQ - 1.  Starts and
+// ends with a barrier, so items can follow each other on the same LDS.
+__device__ __forceinline__ void attention_prefill_item(const AttentionCall& p, int h, int t0, float* lds) {
     float* ks = lds;
     float* vs = lds + kPrefillKeys * kPrefillStride;
     constexpr int dim = 64;
-    const int h = blockIdx.x, t0 = blockIdx.y * kPrefillQ;
+    constexpr int kMerge = kPrefillMerge;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int group = wave & 3, half = wave >> 2;     // token group, key slice parity
+    const int group = wave % kPrefillGroups, slice = wave / kPrefillGroups;   // token group, key slice
     const int li = lane & 15, lj = lane >> 4;
     const int kvh = h / (p.heads / p.kv_heads);
     const int tw = t0 + 16 * group;                   // this wave's first token
@@ -1165,7 +1177,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Atte
     first &= ~(kPrefillKeys - 1);
     const float* K = p.keys + (size_t)kvh * p.capacity * dim;
     const float* V = p.values + (size_t)kvh * p.capacity * dim;
-    v4f kr[2], vr[2];
+    v4f kr[kPrefillLoads], vr[kPrefillLoads];
     prefill_tile_load(K, V, first, end, kr, vr);
     v4f o[4];   // O^T: dims 16 dc + 4 lj + i, query li
 #pragma unroll
@@ -1179,7 +1191,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Atte
         if (k0 + kPrefillKeys < end) prefill_tile_load(K, V, k0 + kPrefillKeys, end, kr, vr);
         // the keys this wave can see in this tile
         const int wave_end = min(end, p.position + min(tw + 16, p.tokens));
-        for (int sub = 16 * half; sub < kPrefillKeys && k0 + sub < wave_end; sub += 32) {
+        for (int sub = 16 * slice; sub < kPrefillKeys && k0 + sub < wave_end; sub += 16 * kPrefillSlices) {
             v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             const float* krow = ks + (sub + li) * kPrefillStride + lj;
 #pragma unroll
@@ -1220,11 +1232,10 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Atte
             }
         }
     }
-    // merge the odd-slice state into the even-slice wave of the same tokens
-    constexpr int kMerge = 18;   // per lane: O^T (16), max, sum
+    // merge the other slices' states into slice 0's wave of the same tokens
     __syncthreads();             // the last tile is no longer read
-    if (half == 1) {
-        float* dst = lds + (group * kWave + lane) * kMerge;
+    if (slice > 0) {
+        float* dst = lds + (((slice - 1) * kPrefillGroups + group) * kWave + lane) * kMerge;
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -1233,20 +1244,27 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Atte
         dst[17] = l;
     }
     __syncthreads();
-    if (half == 1) return;
-    {
-        const float* src = lds + (group * kWave + lane) * kMerge;
-        const float m1 = src[16], l1 = src[17];
-        const float mt = fmaxf(m, m1);
+    if (slice == 0) {
+        float mt = m;
+#pragma unroll
+        for (int z = 1; z < kPrefillSlices; ++z)
+            mt = fmaxf(mt, lds[(((z - 1) * kPrefillGroups + group) * kWave + lane) * kMerge + 16]);
         const float a0 = m == -INFINITY ? 0.0f : expf(m - mt);
-        const float a1 = m1 == -INFINITY ? 0.0f : expf(m1 - mt);
-        l = l * a0 + l1 * a1;
+        l = l * a0;
 #pragma unroll
-        for (int dc = 0; dc < 4; ++dc)
+        for (int dc = 0; dc < 4; ++dc) o[dc] = o[dc] * a0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[dc][i] = o[dc][i] * a0 + src[4 * dc + i] * a1;
+        for (int z = 1; z < kPrefillSlices; ++z) {
+            const float* src = lds + (((z - 1) * kPrefillGroups + group) * kWave + lane) * kMerge;
+            const float a = src[16] == -INFINITY ? 0.0f : expf(src[16] - mt);
+            l = l + src[17] * a;
+#pragma unroll
+            for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[dc][i] = o[dc][i] + src[4 * dc + i] * a;
+        }
     }
-    if (q_live) {
+    if (slice == 0 && q_live) {
         float* out = p.out + ((size_t)q_tok * p.heads + h) * dim;
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc) {
@@ -1255,6 +1273,14 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Atte
             *(v4f*)(out + 16 * dc + 4 * lj) = v;
         }
     }
+    __syncthreads();   // the merge records are read before the next item's tile lands
+}
+
+__global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(AttentionCall p, int items) {
+    __shared__ float lds[kPrefillLds];
+    const int first = blockIdx.x, second = items - 1 - (int)blockIdx.x;
+    attention_prefill_item(p, first % p.heads, (first / p.heads) * kPrefillQ, lds);
+    if (second > first) attention_prefill_item(p, second % p.heads, (second / p.heads) * kPrefillQ, lds);
 }
 
 __global__ void attention_merge_kernel(AttentionCall p, int splits) {
@@ -1825,9 +1851,8 @@ bool launch_attention(const AttentionCall& call, hipStream_t stream) {
         if (splits == 1) per_split = total;
     }
     if (splits == 1 && call.tokens > 1 && call.dim == 64) {
-        attention_prefill_kernel<<<dim3(call.heads, (call.tokens + kPrefillQ - 1) / kPrefillQ), kPrefillThreads, 0,
-                                   stream>>>(
-            call);
+        const int items = call.heads * ((call.tokens + kPrefillQ - 1) / kPrefillQ);
+        attention_prefill_kernel<<<(items + 1) / 2, kPrefillThreads, 0, stream>>>(call, items);
         return true;
     }
     dim3 grid(call.heads, call.tokens, splits);
