@@ -185,6 +185,7 @@ private:
     bool step_token_valid_ = false;   // ids_[0] holds the previous step's argmax
     uint32_t step_token_ = 0;
     unsigned step_launch_ = 0;
+    int step_xcd_misses_ = 0;        // consecutive steps re-run after an XCD mapping mismatch
     double step_bytes_ = 0;          // algorithmic bytes of one step, without KV
     double step_kv_bytes_ = 0;       // KV bytes per visible key
     StepParams step_;

@@ -487,12 +487,21 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
         if (step_q_local_.ptr) hip_check(hipMemset(step_q_local_.ptr, 0, step_q_local_.bytes), "hipMemset");
         step_token_valid_ = false;
         if (why == 2 && step_.x_part_local) {
-            // A block ran off XCD blockIdx % 8: the XCD-local merge is off
-            // from now on, and the step (which wrote nothing but its own
-            // layers' KV rows for this position) runs again.
+            // A block ran off XCD blockIdx % 8: the step (which wrote nothing
+            // but its own layers' KV rows for this position) runs again with
+            // the XCD-local merge off.  After four such steps in a row it
+            // stays off for the session.
+            void* part_local = step_.x_part_local;
+            void* q_local = step_.x_q_local;
             step_.x_part_local = nullptr;
             step_.x_q_local = nullptr;
-            return decode_step(id, host_logits, argmax);
+            const bool retry_local = ++step_xcd_misses_ < 4;
+            decode_step(id, host_logits, argmax);
+            if (retry_local) {
+                step_.x_part_local = static_cast<decltype(step_.x_part_local)>(part_local);
+                step_.x_q_local = static_cast<decltype(step_.x_q_local)>(q_local);
+            }
+            return;
         }
         check(false, "decode step timed out waiting for another block", LH_ERROR_DEVICE);
     }
@@ -504,6 +513,7 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
             std::fclose(f);
         }
     }
+    if (p.x_part_local) step_xcd_misses_ = 0;
     const uint32_t next = *host_argmax_;
     if (argmax) *argmax = next;
     step_token_ = next;

@@ -108,12 +108,20 @@ def run_steps(rt, oracle, path, prompt_tokens, steps, seed, **decoder_args):
     return worst, tokens, profile
 
 
+def ran_every_step(profile, steps):
+    # Every step ran on the persistent decode step; a step whose blocks ran
+    # off their XCD (checked inside the kernel) runs again on the memory path,
+    # and after four such steps in a row the XCD-local path stays off.
+    launches = profile.get("decode_step", {}).get("launches", 0)
+    return steps <= launches <= steps + 4
+
+
 def test_step_matches_oracle_across_span_boundaries(rt, oracle, small):
     # a 70-token prompt, then 80 steps: 2 -> 3 spans of 64 keys
     worst, _, profile = run_steps(rt, oracle, small, 70, 80, seed=3)
     print(f"decode step: worst relative logit error {worst:.2e}")
     assert worst <= W8A8_LOGIT_TOLERANCE
-    assert profile.get("decode_step", {}).get("launches") == 80, profile
+    assert ran_every_step(profile, 80)
 
 
 @pytest.mark.parametrize("item_heads", [2, 4, 8])
@@ -123,14 +131,14 @@ def test_step_with_wider_attention_items(rt, oracle, small, monkeypatch, item_he
     monkeypatch.setenv("LEAF_DECODE_STEP_ITEM_HEADS", str(item_heads))
     worst, _, profile = run_steps(rt, oracle, small, 70, 30, seed=6)
     assert worst <= W8A8_LOGIT_TOLERANCE
-    assert profile.get("decode_step", {}).get("launches") == 30, profile
+    assert ran_every_step(profile, 30)
 
 
 def test_step_at_full_tinyllama_width(rt, oracle, wide):
     worst, _, profile = run_steps(rt, oracle, wide, 300, 12, seed=4)
     print(f"decode step (2048/5632/32:4): worst relative logit error {worst:.2e}")
     assert worst <= W8A8_LOGIT_TOLERANCE
-    assert profile.get("decode_step", {}).get("launches") == 12, profile
+    assert ran_every_step(profile, 12)
 
 
 def test_step_with_sliding_window(rt, oracle, tmp_path):
@@ -138,7 +146,7 @@ def test_step_with_sliding_window(rt, oracle, tmp_path):
     write_artifact(path, step_spec(sliding_window=100, layers=2), seed=13)
     worst, _, profile = run_steps(rt, oracle, path, 90, 40, seed=5)
     assert worst <= W8A8_LOGIT_TOLERANCE
-    assert profile.get("decode_step", {}).get("launches") == 40, profile
+    assert ran_every_step(profile, 40)
 
 
 def test_step_and_graph_paths_agree(rt, small, monkeypatch):

@@ -155,7 +155,8 @@ def test_tinyllama_w8a8_full_prefill_and_decode_steps(rt, oracle, full_artifacts
     print(f"tinyllama full: oracle band {band:.2e} (RMSE {band_rmse:.2e}); GPU worst {worst:.2e} (RMSE {rmse:.2e}); "
           f"greedy choice compared at {checked} of {steps + 1} rows; same argmax as the oracle in {same_gpu} rows "
           f"(the oracle's pairwise-norm run: {same_alt}); {launches} persistent-step launches")
-    assert launches == steps
+    # a step whose blocks ran off their XCD runs again on the memory path
+    assert steps <= launches <= steps + 4
     assert worst <= 1.5 * band
     assert rmse <= 1.5 * band_rmse
     assert same_gpu >= same_alt - 2, "the greedy choice departs from the oracle more often than a reorder does"
