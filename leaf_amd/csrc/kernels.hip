@@ -202,6 +202,34 @@ int row_registers(int width) {
     return 0;
 }
 
+// quantize_kernel with the row in registers (thread t holds columns
+// t + k * kBlock): one load pass.  The absmax is exact in any order, so q and
+// the scale are bit-identical.
+template <int K>
+__global__ __launch_bounds__(kBlock) void quantize_rows_kernel(const float* x, int width, int8_t* q, float* scales) {
+    __shared__ float scratch[16];
+    const float* in = x + (size_t)blockIdx.x * width;
+    float v[K];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = threadIdx.x + k * kBlock;
+        v[k] = c < width ? in[c] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(v[k]));
+    m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    const float s = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / s;
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int c = threadIdx.x + k * kBlock;
+        if (c < width) out[c] = (int8_t)quantize_one(v[k], multiplier);
+    }
+}
+
 __global__ void scale_columns_kernel(const float* x, int width, size_t count, const float* factors, float* y) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
         y[i] = x[i] * factors[i % width];
@@ -1669,7 +1697,12 @@ void launch_norm(const float* x, int rows, int width, const NormView& norm, floa
 }
 
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {
-    quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, q, scales);
+    switch (row_registers(width)) {
+#define LEAF_ROWS(K) case K: quantize_rows_kernel<K><<<rows, kBlock, 0, stream>>>(x, width, q, scales); break;
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+#undef LEAF_ROWS
+        default: quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, q, scales);
+    }
 }
 
 void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
