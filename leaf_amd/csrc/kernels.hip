@@ -194,6 +194,16 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float*
     }
 }
 
+// Columns per thread for the 1024-thread register-row kernels (0: the row
+// does not fit).
+constexpr int kWideRow = 1024;
+int wide_row_registers(int width) {
+    const int k = (width + kWideRow - 1) / kWideRow;
+    for (int c : {1, 2, 3, 4, 6, 8})
+        if (k <= c) return c;
+    return 0;
+}
+
 // Columns per thread for the register-row kernels (0: the row does not fit).
 int row_registers(int width) {
     const int k = (width + kBlock - 1) / kBlock;
@@ -202,18 +212,18 @@ int row_registers(int width) {
     return 0;
 }
 
-// quantize_kernel with the row in registers (thread t holds columns
-// t + k * kBlock): one load pass.  The absmax is exact in any order, so q and
-// the scale are bit-identical.
-template <int K>
-__global__ __launch_bounds__(kBlock) void quantize_rows_kernel(const float* x, int width, int8_t* q, float* scales) {
+// quantize_kernel with the row in registers (thread t of T holds columns
+// t + k * T): one load pass.  The absmax is exact in any order, so q and the
+// scale are bit-identical whatever T is.
+template <int K, int T>
+__global__ __launch_bounds__(T) void quantize_rows_kernel(const float* x, int width, int8_t* q, float* scales) {
     __shared__ float scratch[16];
     const float* in = x + (size_t)blockIdx.x * width;
     float v[K];
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int c = threadIdx.x + k * kBlock;
+        const int c = threadIdx.x + k * T;
         v[k] = c < width ? in[c] : 0.0f;
     }
 #pragma unroll
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(kBlock) void quantize_rows_kernel(const float* x, i
     int8_t* out = q + (size_t)blockIdx.x * width;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int c = threadIdx.x + k * kBlock;
+        const int c = threadIdx.x + k * T;
         if (c < width) out[c] = (int8_t)quantize_one(v[k], multiplier);
     }
 }
@@ -1529,11 +1539,11 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_kernel(const float
     for (int j = threadIdx.x; j < width; j += blockDim.x) out[j] = (int8_t)quantize_one(value(j), multiplier);
 }
 
-// activation_quantize_kernel with the row held in registers (thread t owns
-// columns t + k * kBlock); each activation is computed once.  Same values,
-// reductions and roundings: q and the scale are bit-identical.
-template <int K>
-__global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const float* gate_up, int width, int gated,
+// activation_quantize_kernel with the row held in registers (thread t of T
+// owns columns t + k * T); each activation is computed once.  Elementwise
+// values and an exact absmax: q and the scale are bit-identical whatever T is.
+template <int K, int T>
+__global__ __launch_bounds__(T) void activation_quantize_rows_kernel(const float* gate_up, int width, int gated,
                                                                          int activation, int8_t* q, float* scales) {
     __shared__ float scratch[16];
     const float* in = gate_up + (size_t)blockIdx.x * width * (gated ? 2 : 1);
@@ -1542,7 +1552,7 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const 
         float u[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const int j = threadIdx.x + k * kBlock;
+            const int j = threadIdx.x + k * T;
             a[k] = j < width ? in[j] : 0.0f;
             u[k] = j < width ? in[width + j] : 0.0f;
         }
@@ -1551,7 +1561,7 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const 
     } else {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const int j = threadIdx.x + k * kBlock;
+            const int j = threadIdx.x + k * T;
             a[k] = j < width ? in[j] : 0.0f;
         }
 #pragma unroll
@@ -1560,7 +1570,7 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const 
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; ++k)
-        if (threadIdx.x + k * kBlock < width) m = fmaxf(m, fabsf(a[k]));
+        if (threadIdx.x + k * T < width) m = fmaxf(m, fabsf(a[k]));
     m = block_reduce<float>(m, scratch, [](float x, float y) { return fmaxf(x, y); }, wave_max_f32);
     const float s = fmaxf(m / 127.0f, 1e-12f);
     const float multiplier = 1.0f / s;
@@ -1568,7 +1578,7 @@ __global__ __launch_bounds__(kBlock) void activation_quantize_rows_kernel(const 
     int8_t* out = q + (size_t)blockIdx.x * width;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int j = threadIdx.x + k * kBlock;
+        const int j = threadIdx.x + k * T;
         if (j < width) out[j] = (int8_t)quantize_one(a[k], multiplier);
     }
 }
@@ -1697,9 +1707,9 @@ void launch_norm(const float* x, int rows, int width, const NormView& norm, floa
 }
 
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {
-    switch (row_registers(width)) {
-#define LEAF_ROWS(K) case K: quantize_rows_kernel<K><<<rows, kBlock, 0, stream>>>(x, width, q, scales); break;
-        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+    switch (wide_row_registers(width)) {
+#define LEAF_ROWS(K) case K: quantize_rows_kernel<K, kWideRow><<<rows, kWideRow, 0, stream>>>(x, width, q, scales); break;
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(3) LEAF_ROWS(4) LEAF_ROWS(6) LEAF_ROWS(8)
 #undef LEAF_ROWS
         default: quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, q, scales);
     }
@@ -1717,13 +1727,13 @@ void launch_norm_quantize(const float* x, int rows, int width, const NormView& n
 
 void launch_activation_quantize(const float* gate_up, int tokens, int width, int gated, int activation, int8_t* q,
                                 float* scales, hipStream_t stream) {
-    switch (row_registers(width)) {
+    switch (wide_row_registers(width)) {
 #define LEAF_ROWS(K)                                                                                               \
     case K:                                                                                                        \
-        activation_quantize_rows_kernel<K><<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q,    \
-                                                                         scales);                                  \
+        activation_quantize_rows_kernel<K, kWideRow><<<tokens, kWideRow, 0, stream>>>(gate_up, width, gated,       \
+                                                                                     activation, q, scales);       \
         break;
-        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(3) LEAF_ROWS(4) LEAF_ROWS(6) LEAF_ROWS(8)
 #undef LEAF_ROWS
         default: activation_quantize_kernel<<<tokens, kBlock, 0, stream>>>(gate_up, width, gated, activation, q, scales);
     }
