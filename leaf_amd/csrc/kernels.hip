@@ -19,6 +19,7 @@ namespace leafhip {
 namespace {
 
 constexpr int kBlock = 256;
+constexpr int kWideRow = 1024;   // threads of the per-token row kernels (norm, quantize)
 
 __device__ __forceinline__ float weight_value(const WeightView& w, int row, int col) {
     const size_t index = (size_t)row * w.cols + col;
@@ -89,7 +90,7 @@ __device__ __forceinline__ float apply_norm(float x, int c, const NormStats& st,
     return (x - st.mean) * st.scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
 }
 
-__global__ __launch_bounds__(kBlock) void norm_kernel(const float* x, int width, NormView norm, float* y) {
+__global__ __launch_bounds__(kWideRow) void norm_kernel(const float* x, int width, NormView norm, float* y) {
     __shared__ float scratch[16];
     const float* in = x + (size_t)blockIdx.x * width;
     float* out = y + (size_t)blockIdx.x * width;
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, int wi
 // values and their quantization as quantize_kernel does them (recomputing
 // each normalized value with the same expression), so q and the scale are
 // bit-identical to the two kernels in sequence without the f32 round trip.
-__global__ __launch_bounds__(kBlock) void norm_quantize_kernel(const float* x, int width, NormView norm, int8_t* q,
+__global__ __launch_bounds__(kWideRow) void norm_quantize_kernel(const float* x, int width, NormView norm, int8_t* q,
                                                               float* scales) {
     __shared__ float scratch[16];
     const float* in = x + (size_t)blockIdx.x * width;
@@ -134,26 +135,26 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_kernel(const float* x, i
 }
 
 // The same row norm + quantization with the row held in registers: thread t
-// owns columns t + k * kBlock (k < K), so every load of the row is issued up
-// front instead of once per pass.  Each thread sums its columns in the same
-// order as block_norm_stats and the reductions are the same, so q and the
-// scale are bit-identical to norm_quantize_kernel.
+// owns columns t + k * kWideRow (k < K), so every load of the row is issued
+// up front instead of once per pass.  Each thread sums its columns in the
+// same order as block_norm_stats over kWideRow threads and the reductions are
+// the same, so q and the scale are bit-identical to norm_quantize_kernel.
 template <int K>
-__global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float* x, int width, NormView norm,
+__global__ __launch_bounds__(kWideRow) void norm_quantize_rows_kernel(const float* x, int width, NormView norm,
                                                                    int8_t* q, float* scales) {
     __shared__ float scratch[16];
     const float* in = x + (size_t)blockIdx.x * width;
     float v[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int c = threadIdx.x + k * kBlock;
+        const int c = threadIdx.x + k * kWideRow;
         v[k] = c < width ? in[c] : 0.0f;
     }
     float mean = 0.0f;
     if (norm.kind == 1) {
         float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < K; ++k) if (threadIdx.x + k * kBlock < width) s += v[k];
+        for (int k = 0; k < K; ++k) if (threadIdx.x + k * kWideRow < width) s += v[k];
         s = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
         mean = s / (float)width;
     }
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float*
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < K; ++k)
-            if (threadIdx.x + k * kBlock < width) { const float w = v[k] * v[k]; s += (double)w; }
+            if (threadIdx.x + k * kWideRow < width) { const float w = v[k] * v[k]; s += (double)w; }
         __shared__ double dscratch[16];
         s = block_reduce<double>(s, dscratch, [](double a, double b) { return a + b; }, wave_sum_f64);
         square = (float)s;
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float*
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < K; ++k)
-            if (threadIdx.x + k * kBlock < width) { const float w = v[k] - mean; s += w * w; }
+            if (threadIdx.x + k * kWideRow < width) { const float w = v[k] - mean; s += w * w; }
         square = block_reduce<float>(s, scratch, [](float a, float b) { return a + b; }, wave_sum_f32);
     }
     NormStats st;
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float*
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int c = threadIdx.x + k * kBlock;
+        const int c = threadIdx.x + k * kWideRow;
         if (c < width) { v[k] = apply_norm(v[k], c, st, norm); m = fmaxf(m, fabsf(v[k])); }
     }
     m = block_reduce<float>(m, scratch, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
@@ -189,25 +190,16 @@ __global__ __launch_bounds__(kBlock) void norm_quantize_rows_kernel(const float*
     int8_t* out = q + (size_t)blockIdx.x * width;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int c = threadIdx.x + k * kBlock;
+        const int c = threadIdx.x + k * kWideRow;
         if (c < width) out[c] = (int8_t)quantize_one(v[k], multiplier);
     }
 }
 
 // Columns per thread for the 1024-thread register-row kernels (0: the row
 // does not fit).
-constexpr int kWideRow = 1024;
 int wide_row_registers(int width) {
     const int k = (width + kWideRow - 1) / kWideRow;
     for (int c : {1, 2, 3, 4, 6, 8})
-        if (k <= c) return c;
-    return 0;
-}
-
-// Columns per thread for the register-row kernels (0: the row does not fit).
-int row_registers(int width) {
-    const int k = (width + kBlock - 1) / kBlock;
-    for (int c : {1, 2, 4, 8, 12, 16, 24, 32})
         if (k <= c) return c;
     return 0;
 }
@@ -1703,7 +1695,7 @@ void launch_embedding(const WeightView& table, const WeightView* positions, cons
 }
 
 void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream) {
-    norm_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, y);
+    norm_kernel<<<rows, kWideRow, 0, stream>>>(x, width, norm, y);
 }
 
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {
@@ -1717,11 +1709,11 @@ void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scal
 
 void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
                           hipStream_t stream) {
-    switch (row_registers(width)) {
-#define LEAF_ROWS(K) case K: norm_quantize_rows_kernel<K><<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales); break;
-        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(4) LEAF_ROWS(8) LEAF_ROWS(12) LEAF_ROWS(16) LEAF_ROWS(24) LEAF_ROWS(32)
+    switch (wide_row_registers(width)) {
+#define LEAF_ROWS(K) case K: norm_quantize_rows_kernel<K><<<rows, kWideRow, 0, stream>>>(x, width, norm, q, scales); break;
+        LEAF_ROWS(1) LEAF_ROWS(2) LEAF_ROWS(3) LEAF_ROWS(4) LEAF_ROWS(6) LEAF_ROWS(8)
 #undef LEAF_ROWS
-        default: norm_quantize_kernel<<<rows, kBlock, 0, stream>>>(x, width, norm, q, scales);
+        default: norm_quantize_kernel<<<rows, kWideRow, 0, stream>>>(x, width, norm, q, scales);
     }
 }
 
