@@ -910,6 +910,33 @@ __global__ __launch_bounds__(kBlock) void gemm_w8a8_split_epilogue(WeightView w,
     }
 }
 
+// gemm_w8a8_split_epilogue four outputs per thread (N % 4 == 0): 128-bit
+// loads of each split's sums and of y.  Exact integer sums, the same
+// epilogue per output: identical results.
+__global__ __launch_bounds__(kBlock) void gemm_w8a8_split_epilogue4(WeightView w, const float* __restrict__ xs,
+                                                                   int tokens, const int32_t* __restrict__ partial,
+                                                                   int splits, float* __restrict__ y, int epilogue,
+                                                                   int32_t* __restrict__ acc_out) {
+    const int N = w.rows;
+    const size_t count = (size_t)tokens * N;
+    for (size_t i = 4 * (blockIdx.x * (size_t)kBlock + threadIdx.x); i < count; i += 4 * (size_t)gridDim.x * kBlock) {
+        v4i acc = *(const v4i*)(partial + i);
+        for (int s = 1; s < splits; ++s) acc += *(const v4i*)(partial + s * count + i);
+        const int t = (int)(i / N), n = (int)(i % N);
+        if (acc_out) *(v4i*)(acc_out + i) = acc;
+        const float sx = xs[t];
+        v4f prev = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (epilogue == kAccumulate) prev = *(const v4f*)(y + i);
+        v4f out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float v = fmaf((float)acc[j] * sx, w.scales[n + j], 0.0f) + bias_at(w, n + j);
+            out[j] = epilogue == kAccumulate ? prev[j] + v : v;
+        }
+        *(v4f*)(y + i) = out;
+    }
+}
+
 // ------------------------------------------------ FP prefill: f32 MFMA ---
 // Y[t, n] = sum_k X[t, k] W[n, k] with v_mfma_f32_16x16x4_f32; weights of any
 // storage are widened (BF16) or dequantized (INT8 / INT4) as they are loaded.
@@ -1808,8 +1835,16 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
                                                               stages / splits, partial);
             if (partial) {
                 const int blocks = std::min(ceil_div((size_t)c.tokens * w.rows, kBlock), 4096);
-                gemm_w8a8_split_epilogue<<<blocks, kBlock, 0, stream>>>(w, xs, c.tokens, partial, splits, c.y,
-                                                                        c.epilogue, c.acc_out);
+                const bool vec = w.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(c.y) & 15) == 0 &&
+                                 (reinterpret_cast<uintptr_t>(partial) & 15) == 0 &&
+                                 (reinterpret_cast<uintptr_t>(c.acc_out) & 15) == 0;
+                if (vec)
+                    gemm_w8a8_split_epilogue4<<<std::min(ceil_div((size_t)c.tokens * w.rows / 4, kBlock), 4096), kBlock,
+                                                0, stream>>>(w, xs, c.tokens, partial, splits, c.y, c.epilogue,
+                                                             c.acc_out);
+                else
+                    gemm_w8a8_split_epilogue<<<blocks, kBlock, 0, stream>>>(w, xs, c.tokens, partial, splits, c.y,
+                                                                            c.epilogue, c.acc_out);
             }
             return 3;
         }
