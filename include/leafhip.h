@@ -4,7 +4,7 @@
  * Drop-in boundary for Leaf's native decoder runtime.  The reference exposes
  * the C++ class leaf::runtime::Decoder (engine/include/leaf/runtime/decoder.h:15-50)
  * and the leaf_decoder process protocol (engine/src/main_decoder.cpp:116-363);
- * this header is what a C++ Decoder wrapper (leaf_amd/csrc/leaf_decoder.hpp),
+ * this header is what a C++ Decoder wrapper (include/leafhip_decoder.hpp),
  * the leaf_decoder-compatible executable and any FFI binding call instead.
  *
  * Conventions:
@@ -86,9 +86,25 @@ lh_status lh_model_eos_tokens(const lh_model* model, uint32_t* out, size_t capac
 lh_status lh_model_destroy(lh_model* model);
 
 /* ---------------------------------------------------------------- session */
+/* Floating-point order of a session's kernels.
+ *  FAST: parallel reductions (per-lane partials, wave trees, key spans merged
+ *    by log-sum-exp) and the device's libm.  Integer stages stay bit-exact;
+ *    FP32 logits stay within 1e-3 of the CPU path, W8A8 ones within a few
+ *    percent (a one-ulp change upstream of a quantization can move an int8 bin).
+ *  REFERENCE: the CPU path's summation orders (sequential norm and softmax
+ *    sums, dot_avx's lane chains) and glibc's expf, so logits equal the CPU
+ *    reference's bit for bit, hence identical greedy tokens, for decoders with
+ *    SiLU or ReLU activations and fast FP32 math (GELU uses the device's
+ *    erff / tanhf; accurate FP32 math is rejected).  Slower.
+ *  DEFAULT: FAST, unless the environment variable LEAF_GPU_NUMERICS=reference. */
+#define LH_NUMERICS_DEFAULT 0
+#define LH_NUMERICS_FAST 1
+#define LH_NUMERICS_REFERENCE 2
+
 typedef struct lh_session_options {
     uint32_t max_context;  /* KV capacity in tokens; 0 = the artifact's max_positions */
     uint32_t max_prefill;  /* tokens per forward the workspaces are planned for; 0 = 512 (grown on demand) */
+    uint32_t numerics;     /* LH_NUMERICS_*; no reference counterpart (the CPU has one order) */
 } lh_session_options;
 
 /* A decoding session: preallocated device KV cache for max_context tokens,
@@ -155,7 +171,18 @@ lh_status lh_timer_start(lh_stream stream, lh_timer** out);
 lh_status lh_timer_stop(lh_timer* timer, lh_stream stream, double* milliseconds); /* destroys the timer */
 
 /* ------------------------------------------------- kernel-level entry points
- * One weight matrix as stored in a LEAFDC artifact (Weight, decoder.cpp:236-251):
+ * Numerics of this thread's later kernel-level calls (LH_NUMERICS_FAST or
+ * LH_NUMERICS_REFERENCE, as for sessions): lh_rmsnorm, lh_layernorm,
+ * lh_attention, lh_silu_gate, lh_activation and the FP paths of lh_linear,
+ * lh_gemv_{f32,bf16,w8a32,w4a32} and lh_gemm_f32 follow it; the integer
+ * paths are exact either way.  No reference counterpart. */
+lh_status lh_set_kernel_numerics(uint32_t numerics);
+/* y[i] = expf(x[i]) with the result glibc 2.35's expf returns on x86-64 with
+ * FMA (the exp of the CPU path's softmax and SiLU, transformer.cpp:134,
+ * decoder.cpp:983), for every float input. */
+lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream);
+
+/* One weight matrix as stored in a LEAFDC artifact (Weight, decoder.cpp:236-251):
  * bits 32 = f32, 16 = BF16 bits, 8 = int8, 4 = signed nibbles (low = even column);
  * scales[row * (cols / group) + col / group] for bits 8 and 4; bias may be NULL.
  * All pointers are device pointers. */

@@ -1,12 +1,16 @@
 // extern "C" surface of libleafhip (include/leafhip.h).  Every entry point
 // converts exceptions into a status code plus a thread-local message; nothing
 // throws across the ABI.
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -49,42 +53,67 @@ void require_arg(bool ok, const char* what) {
 
 hipStream_t as_stream(lh_stream s) { return static_cast<hipStream_t>(s); }
 
-// Scratch for kernel-level calls that quantize or normalize internally;
-// grown on demand and kept for the process (one per device).
-struct Scratch {
-    std::mutex lock;
-    leafhip::DeviceBuffer buffers[8];
-    int device[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
+// Device scratch of the kernel-level entry points (quantized inputs, split-K
+// sums, attention partials), one set per (device, stream): calls on different
+// streams never share memory.  A buffer that must grow is replaced and the old
+// one is kept until the process ends, so work already queued on it, or a
+// graph captured with it, stays valid without any synchronization.  Growth
+// while the stream is capturing is refused: run the call once before
+// capturing it.  The sets are never freed -- in particular not by static
+// destructors, which run after the HIP runtime and a profiler may have shut
+// down.
+struct StreamScratch {
+    leafhip::DeviceBuffer* work = nullptr;       // grown on demand
+    leafhip::DeviceBuffer* counters = nullptr;   // zeroed once; the attention kernel resets what it uses
 };
-Scratch g_scratch;
+std::mutex g_scratch_lock;
+auto* g_scratch = new std::map<std::pair<int, hipStream_t>, StreamScratch>();
+auto* g_retired = new std::vector<leafhip::DeviceBuffer*>();
 
-void* scratch_bytes(size_t bytes) {
+StreamScratch& scratch_of(hipStream_t stream) {
     int dev = 0;
     leafhip::hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> guard(g_scratch.lock);
-    const int slot = dev & 7;
-    if (g_scratch.buffers[slot].bytes < bytes) {
-        leafhip::hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        g_scratch.buffers[slot].allocate(bytes);
+    return (*g_scratch)[{dev, stream}];
+}
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    leafhip::hip_check(hipStreamIsCapturing(stream, &status), "hipStreamIsCapturing");
+    return status != hipStreamCaptureStatusNone;
+}
+
+void* scratch_bytes(size_t bytes, hipStream_t stream) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    StreamScratch& sc = scratch_of(stream);
+    if (!sc.work || sc.work->bytes < bytes) {
+        if (capturing(stream))
+            throw leafhip::Error(LH_ERROR_STATE, "Leaf decoder: kernel scratch must grow outside stream capture "
+                                                 "(run the call once before capturing it)");
+        auto* grown = new leafhip::DeviceBuffer(std::max(bytes, sc.work ? 2 * sc.work->bytes : size_t(1) << 20));
+        if (sc.work) g_retired->push_back(sc.work);
+        sc.work = grown;
     }
-    return g_scratch.buffers[slot].ptr;
+    return sc.work->ptr;
 }
 
 // Zero-initialized span counters of the decode attention kernel (it resets
-// them itself), one set per device.
-unsigned* attention_counters() {
-    static leafhip::DeviceBuffer counters[8];
-    static std::mutex lock;
-    int dev = 0;
-    leafhip::hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> guard(lock);
-    auto& b = counters[dev & 7];
-    if (!b.ptr) {
-        b.allocate(1024 * sizeof(unsigned));
-        leafhip::hip_check(hipMemset(b.ptr, 0, b.bytes), "hipMemset");
+// them itself), one set per (device, stream).
+unsigned* attention_counters(hipStream_t stream) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    StreamScratch& sc = scratch_of(stream);
+    if (!sc.counters) {
+        if (capturing(stream))
+            throw leafhip::Error(LH_ERROR_STATE, "Leaf decoder: attention counters must be set up outside stream "
+                                                 "capture (run the call once before capturing it)");
+        auto* b = new leafhip::DeviceBuffer(1024 * sizeof(unsigned));
+        leafhip::hip_check(hipMemsetAsync(b->ptr, 0, b->bytes, stream), "hipMemsetAsync");
+        sc.counters = b;
     }
-    return b.as<unsigned>();
+    return sc.counters->as<unsigned>();
 }
+
+// Numerics of this thread's kernel-level calls (lh_set_kernel_numerics).
+thread_local bool t_reference_order = false;
 
 leafhip::WeightView view_of(const lh_weight* w) {
     require_arg(w && w->data && w->rows && w->cols, "weight descriptor is empty");
@@ -132,13 +161,22 @@ lh_status linear_impl(const lh_weight* weight, const float* x, const int8_t* q, 
             const size_t q_bytes = q ? 0 : ((tokens * c.w.cols + 255) / 256) * 256;
             const size_t s_bytes = q ? 0 : ((tokens * 4 + 255) / 256) * 256;
             const size_t split = tokens > 4 ? 8 * tokens * c.w.rows : 0;
-            auto* base = static_cast<uint8_t*>(scratch_bytes(q_bytes + s_bytes + split * sizeof(int32_t) + 256));
+            auto* base = static_cast<uint8_t*>(
+                scratch_bytes(q_bytes + s_bytes + split * sizeof(int32_t) + 256, as_stream(stream)));
             if (!q) {
                 c.xq_scratch = reinterpret_cast<int8_t*>(base);
                 c.xs_scratch = reinterpret_cast<float*>(base + q_bytes);
             }
             c.split_scratch = split ? reinterpret_cast<int32_t*>(base + q_bytes + s_bytes) : nullptr;
             c.split_capacity = split;
+        }
+        if (t_reference_order && !c.integer_activations) {
+            // dot_avx order; the integer path is exact in every mode
+            require_arg(x != nullptr, "input is required");
+            if (!leafhip::launch_linear_fp_reference_order(c.w, x, int(tokens), y, leafhip::kStore, as_stream(stream)))
+                throw leafhip::Error(LH_ERROR_UNSUPPORTED, "Leaf decoder: unsupported linear configuration");
+            leafhip::hip_check(hipGetLastError(), "linear launch");
+            return;
         }
         const int path = leafhip::launch_linear(c, as_stream(stream));
         if (path < 0) throw leafhip::Error(LH_ERROR_UNSUPPORTED, "Leaf decoder: unsupported linear configuration");
@@ -257,7 +295,8 @@ lh_status lh_session_create(lh_model* model, const lh_session_options* options, 
         leafhip::hip_check(hipSetDevice(model->impl->context.device), "hipSetDevice");
         const uint32_t context = options ? options->max_context : 0;
         const uint32_t prefill = options ? options->max_prefill : 0;
-        *out = new lh_session{std::make_unique<leafhip::Session>(*model->impl, context, prefill)};
+        const uint32_t numerics = options ? options->numerics : LH_NUMERICS_DEFAULT;
+        *out = new lh_session{std::make_unique<leafhip::Session>(*model->impl, context, prefill, numerics)};
     });
 }
 
@@ -445,6 +484,22 @@ lh_status lh_timer_stop(lh_timer* timer, lh_stream stream, double* milliseconds)
     });
 }
 
+lh_status lh_set_kernel_numerics(uint32_t numerics) {
+    return guarded([&] {
+        require_arg(numerics == LH_NUMERICS_FAST || numerics == LH_NUMERICS_REFERENCE, "unknown numerics mode");
+        t_reference_order = numerics == LH_NUMERICS_REFERENCE;
+    });
+}
+
+lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream) {
+    return guarded([&] {
+        require_arg(x && y, "input and output are required");
+        if (!count) return;
+        leafhip::launch_libm_expf(x, count, y, as_stream(stream));
+        leafhip::hip_check(hipGetLastError(), "expf launch");
+    });
+}
+
 lh_status lh_quantize_rows_i8(const float* x, size_t rows, size_t cols, int8_t* q, float* scales, lh_stream stream) {
     return guarded([&] {
         require_arg(x && q && scales && rows && cols && rows <= 0x7fffffff && cols <= 0x7fffffff, "invalid quantization call");
@@ -492,7 +547,12 @@ lh_status lh_rmsnorm(const float* x, size_t rows, size_t width, const float* gam
     return guarded([&] {
         require_arg(x && gamma && y && rows && width && rows <= 0x7fffffff && width <= 0x7fffffff, "invalid norm call");
         leafhip::NormView n{gamma, nullptr, epsilon, 0, accurate ? 1 : 0};
-        leafhip::launch_norm(x, int(rows), int(width), n, y, as_stream(stream));
+        if (t_reference_order) {
+            require_arg(leafhip::launch_norm_reference_order(x, int(rows), int(width), n, y, as_stream(stream)),
+                        "reference-order norm rows are at most 16384 wide");
+        } else {
+            leafhip::launch_norm(x, int(rows), int(width), n, y, as_stream(stream));
+        }
         leafhip::hip_check(hipGetLastError(), "norm launch");
     });
 }
@@ -501,7 +561,12 @@ lh_status lh_layernorm(const float* x, size_t rows, size_t width, const float* g
     return guarded([&] {
         require_arg(x && gamma && y && rows && width && rows <= 0x7fffffff && width <= 0x7fffffff, "invalid norm call");
         leafhip::NormView n{gamma, beta, epsilon, 1, 0};
-        leafhip::launch_norm(x, int(rows), int(width), n, y, as_stream(stream));
+        if (t_reference_order) {
+            require_arg(leafhip::launch_norm_reference_order(x, int(rows), int(width), n, y, as_stream(stream)),
+                        "reference-order norm rows are at most 16384 wide");
+        } else {
+            leafhip::launch_norm(x, int(rows), int(width), n, y, as_stream(stream));
+        }
         leafhip::hip_check(hipGetLastError(), "norm launch");
     });
 }
@@ -536,11 +601,21 @@ lh_status lh_attention(const float* q_heads, const float* keys, const float* val
         a.kv_heads = int(kv_heads); a.tokens = int(tokens); a.position = int(position); a.dim = int(dim);
         a.capacity = int(capacity); a.window = int(window);
         a.scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(dim)));
+        if (t_reference_order) {
+            size_t keys = position + tokens;
+            if (window) keys = std::min<size_t>(keys, window);
+            require_arg(keys <= size_t(leafhip::reference_order_attention_keys()),
+                        "too many keys for one query in reference order");
+            leafhip::check(leafhip::launch_attention_reference_order(a, int(keys), as_stream(stream)),
+                           "attention launch rejected", LH_ERROR_UNSUPPORTED);
+            leafhip::hip_check(hipGetLastError(), "attention launch");
+            return;
+        }
         if (tokens == 1 && kv_heads <= 1024) {
             const size_t floats = ((position + tokens + 15) / 16) * heads * (dim + 2);
-            a.partial = static_cast<float*>(scratch_bytes(floats * sizeof(float)));
+            a.partial = static_cast<float*>(scratch_bytes(floats * sizeof(float), as_stream(stream)));
             a.partial_capacity = int(floats);
-            a.counters = attention_counters();
+            a.counters = attention_counters(as_stream(stream));
         }
         leafhip::check(leafhip::launch_attention(a, as_stream(stream)), "attention launch rejected", LH_ERROR_UNSUPPORTED);
         leafhip::hip_check(hipGetLastError(), "attention launch");
@@ -549,14 +624,20 @@ lh_status lh_attention(const float* q_heads, const float* keys, const float* val
 lh_status lh_silu_gate(const float* gate_up, size_t tokens, size_t width, float* out, lh_stream stream) {
     return guarded([&] {
         require_arg(gate_up && out && tokens && width && tokens * width <= 0x7fffffff, "invalid SiLU call");
-        leafhip::launch_activation(gate_up, int(tokens), int(width), 1, 0, out, as_stream(stream));
+        if (t_reference_order)
+            leafhip::launch_activation_reference_order(gate_up, int(tokens), int(width), 1, 0, out, as_stream(stream));
+        else
+            leafhip::launch_activation(gate_up, int(tokens), int(width), 1, 0, out, as_stream(stream));
         leafhip::hip_check(hipGetLastError(), "activation launch");
     });
 }
 lh_status lh_activation(const float* x, size_t count, uint32_t activation, float* out, lh_stream stream) {
     return guarded([&] {
         require_arg(x && out && count && count <= 0x7fffffff && activation <= 3, "invalid activation call");
-        leafhip::launch_activation(x, 1, int(count), 0, int(activation), out, as_stream(stream));
+        if (t_reference_order)
+            leafhip::launch_activation_reference_order(x, 1, int(count), 0, int(activation), out, as_stream(stream));
+        else
+            leafhip::launch_activation(x, 1, int(count), 0, int(activation), out, as_stream(stream));
         leafhip::hip_check(hipGetLastError(), "activation launch");
     });
 }

@@ -154,4 +154,26 @@ int attention_decode_spans(int keys, int dim);
 // Whether single-token attention runs the span kernels (graph-capturable).
 bool attention_decode_supported(int heads, int kv_heads, int dim);
 
+// ---- reference-order kernels (reference_order.hip): the CPU path's
+// summation orders and libm results, so logits match it bit for bit.
+constexpr int kReferenceOrderMaxWidth = 16384;   // norm rows staged in LDS
+// norm() with sequential sums; false when width exceeds kReferenceOrderMaxWidth.
+bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
+                                 hipStream_t stream);
+// Most visible keys one query of the reference-order attention can score (LDS).
+int reference_order_attention_keys();
+// attention_impl order; `max_keys` bounds the visible keys of every query
+// (the LDS it sizes).  False when max_keys or the head dim is too large.
+bool launch_attention_reference_order(const AttentionCall& call, int max_keys, hipStream_t stream);
+// activate() with glibc's expf for SiLU (GELU codes use the device's erff / tanhf).
+void launch_activation_reference_order(const float* gate_up, int tokens, int width, int gated, int activation,
+                                       float* act, hipStream_t stream);
+// y[i] = expf(x[i]) as glibc computes it.
+void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream);
+// dot_avx / dot_source_bf16_avx order for FP32, BF16, INT8 and INT4 weights with
+// FP32 activations, tokens in groups of four; y = result + bias (kStore) or
+// y += result + bias (kAccumulate).  False for other storage.
+bool launch_linear_fp_reference_order(const WeightView& w, const float* x, int tokens, float* y, int epilogue,
+                                      hipStream_t stream);
+
 }  // namespace leafhip

@@ -1,0 +1,340 @@
+// Reference-order kernels (gfx950): floating-point work in the order and
+// rounding of Leaf's CPU path, so that a decoder's logits equal the CPU's bit
+// for bit.
+//
+// The fast kernels reduce in parallel orders (per-lane partials, DPP trees,
+// span partials merged by log-sum-exp).  That moves W8A8 logits by a few
+// percent, because a one-ulp change upstream of a quantization can move an
+// int8 bin.  These kernels instead follow the reference's sequential sums:
+//   * norm() (engine/src/decoder.cpp:706-727): one lane sums the row's
+//     squares (or values, for LayerNorm's mean) in column order;
+//     accurate_rms_square_sum (accurate_fp32.h:6-13) sums the float squares
+//     in double, in column order.
+//   * attention_impl (engine/src/kernels/transformer.cpp:94-146): per query,
+//     scores (q.k * scale) * scale with the scalar dot of the Linux build
+//     (:69-73), the maximum, exp(s - max) with glibc's expf (libm_expf.h), a
+//     sequential denominator, p = e / denominator, then output[d] += p * v[d]
+//     in key order, one lane per d.
+//   * activate (decoder.cpp:982-987): SiLU g / (1 + expf(-g)) with glibc's
+//     expf and ReLU as std::max(x, 0.0f).  GELU uses the device's erff /
+//     tanhf, which are not glibc's: GELU decoders are not bit-exact here.
+//   * dot_avx / dot_source_bf16_avx (decoder.cpp:355-420): FP32, BF16-source
+//     and weight-only INT8 / INT4 rows.  One token: four 8-lane FMA chains over
+//     32-column blocks, (a + b) + (c + d), 8-column blocks, the 8-lane
+//     horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), a scalar fused
+//     tail of (value / scale) * x, then result += partial * scale per group
+//     (fused).  Two to four tokens: one 8-lane chain per token.  The linear
+//     runs tokens in groups of four (decoder.cpp:1217-1228).
+// The W8A8 integer path needs none of this: its quantization, int32 sums and
+// epilogue already match the CPU exactly in the fast kernels.
+//
+// All files are compiled with -ffp-contract=off, so every product and sum
+// below rounds separately unless it is spelled fmaf().
+#include "device_common.h"
+#include "kernels.h"
+#include "libm_expf.h"
+
+#include <math.h>
+
+#include <algorithm>
+
+namespace leafhip {
+namespace {
+
+constexpr int kRoBlock = 256;
+
+// ------------------------------------------------------------------ norm ---
+// One block per row.  The row is staged in LDS, every thread forms its
+// columns' squares (the same rounded products the CPU forms), and thread 0
+// adds them in column order.
+__global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int width, NormView norm, float* y) {
+    extern __shared__ float row[];        // [width] values, then [width] squares
+    float* sq = row + width;
+    __shared__ float stat[2];
+    const float* in = x + (size_t)blockIdx.x * width;
+    float* out = y + (size_t)blockIdx.x * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) row[c] = in[c];
+    __syncthreads();
+    float mean = 0.0f;
+    if (norm.kind == 1) {
+        if (threadIdx.x == 0) {
+            float s = 0.0f;
+            for (int c = 0; c < width; ++c) s += row[c];
+            stat[0] = s / (float)width;
+        }
+        __syncthreads();
+        mean = stat[0];
+    }
+    const bool accurate = norm.kind == 0 && norm.accurate;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        const float v = accurate ? row[c] : row[c] - mean;
+        sq[c] = v * v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float square;
+        if (accurate) {
+            double total = 0.0;
+            for (int c = 0; c < width; ++c) total += (double)sq[c];
+            square = (float)total;
+        } else {
+            square = 0.0f;
+            int c = 0;
+            for (; c + 4 <= width; c += 4) {
+                const v4f s4 = *reinterpret_cast<const v4f*>(sq + c);
+                square += s4[0];
+                square += s4[1];
+                square += s4[2];
+                square += s4[3];
+            }
+            for (; c < width; ++c) square += sq[c];
+        }
+        stat[1] = 1.0f / sqrtf(square / (float)width + norm.epsilon);
+    }
+    __syncthreads();
+    const float scale = stat[1];
+    for (int c = threadIdx.x; c < width; c += blockDim.x)
+        out[c] = (row[c] - mean) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+}
+
+// ------------------------------------------------------------- attention ---
+// One block per (query head, query token).  LDS holds q and the scores of the
+// visible keys; thread 0 sums the denominator; thread d < dim accumulates
+// output element d over the keys in order.
+__global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p) {
+    extern __shared__ float lds[];
+    float* qs = lds;                       // [dim]
+    float* sc = lds + p.dim;               // [visible keys]
+    __shared__ float red[kRoBlock / kWave];
+    __shared__ float den_shared;
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int position = p.position_ptr ? *p.position_ptr : p.position;
+    const int end = position + t + 1;
+    const int begin = (p.window && end > p.window) ? end - p.window : 0;
+    const int n = end - begin;
+    const int dim = p.dim;
+    const int kvh = h / (p.heads / p.kv_heads);
+    const float* q = p.q_heads + ((size_t)h * p.tokens + t) * dim;
+    const float* K = p.keys + (size_t)kvh * p.capacity * dim;
+    const float* V = p.values + (size_t)kvh * p.capacity * dim;
+    float* o = p.out + ((size_t)t * p.heads + h) * dim;
+    for (int d = threadIdx.x; d < dim; d += blockDim.x) qs[d] = q[d];
+    __syncthreads();
+    // scores and their maximum (NaN scores never become the maximum, as with
+    // std::max(maximum, score))
+    float m = -INFINITY;
+    for (int k = threadIdx.x; k < n; k += blockDim.x) {
+        const float* kr = K + (size_t)(begin + k) * dim;
+        float s = 0.0f;
+        for (int d = 0; d < dim; ++d) s += qs[d] * kr[d];
+        s = s * p.scale * p.scale;
+        sc[k] = s;
+        m = m < s ? s : m;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float other = __shfl_xor(m, off, kWave);
+        m = m < other ? other : m;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float maximum = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) maximum = maximum < red[w] ? red[w] : maximum;
+    if (!isfinite(maximum)) {
+        // fully masked (or infinite) row: the CPU leaves the zero-filled output
+        for (int d = threadIdx.x; d < dim; d += blockDim.x) o[d] = 0.0f;
+        return;
+    }
+    for (int k = threadIdx.x; k < n; k += blockDim.x) sc[k] = libm_expf(sc[k] - maximum);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // masked keys add exp(-inf) = 0, which leaves the sum unchanged
+        float den = 0.0f;
+        for (int k = 0; k < n; ++k) den += sc[k];
+        den_shared = den;
+    }
+    __syncthreads();
+    const float den = den_shared;
+    for (int k = threadIdx.x; k < n; k += blockDim.x) sc[k] = sc[k] / den;
+    __syncthreads();
+    // output[d] += p * v[d] in key order; masked keys add p * v = +-0, which
+    // leaves a sum that started at +0 unchanged
+    for (int d = threadIdx.x; d < dim; d += blockDim.x) {
+        float acc = 0.0f;
+        const float* vr = V + (size_t)begin * dim + d;
+        int k = 0;
+        for (; k + 4 <= n; k += 4) {
+            const float v0 = vr[(size_t)(k + 0) * dim], v1 = vr[(size_t)(k + 1) * dim];
+            const float v2 = vr[(size_t)(k + 2) * dim], v3 = vr[(size_t)(k + 3) * dim];
+            acc += sc[k + 0] * v0;
+            acc += sc[k + 1] * v1;
+            acc += sc[k + 2] * v2;
+            acc += sc[k + 3] * v3;
+        }
+        for (; k < n; ++k) acc += sc[k] * vr[(size_t)k * dim];
+        o[d] = acc;
+    }
+}
+
+// ------------------------------------------------------------ activation ---
+__device__ __forceinline__ float ro_activate(int activation, float x) {
+    if (activation == 0) return x / (1.0f + libm_expf(-x));
+    if (activation == 1) return 0.5f * x * (1.0f + erff(x * 0.7071067811865475f));
+    if (activation == 2) return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+    return x < 0.0f ? 0.0f : x;   // std::max(x, 0.0f)
+}
+
+__global__ void ro_activation_kernel(const float* gate_up, int tokens, int width, int gated, int activation,
+                                     float* act) {
+    const size_t count = (size_t)tokens * width;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / width, j = i % width;
+        if (gated) {
+            const float g = gate_up[t * 2 * width + j], u = gate_up[t * 2 * width + width + j];
+            act[i] = u * ro_activate(activation, g);
+        } else {
+            act[i] = ro_activate(activation, gate_up[i]);
+        }
+    }
+}
+
+__global__ void ro_expf_kernel(const float* x, size_t count, float* y) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = libm_expf(x[i]);
+}
+
+// ------------------------------------------------------------------ dot ----
+// The unscaled value a vector lane of dot_avx loads (f32 as stored, INT8 and
+// INT4 as integers; decoder.cpp:299-320), and Weight::value (:236-251).
+template <int BITS>
+__device__ __forceinline__ float lane_value(const WeightView& w, size_t index) {
+    if constexpr (BITS == 32) return ((const float*)w.data)[index];
+    else if constexpr (BITS == 16) return bf16_to_f32(((const uint16_t*)w.data)[index]);
+    else if constexpr (BITS == 8) return (float)((const int8_t*)w.data)[index];
+    else return (float)nibble(((const uint8_t*)w.data)[index / 2], (int)(index & 1));
+}
+
+// Horizontal sum of the eight lanes of an aligned 8-lane group in the CPU's
+// order: (l0+l4, l1+l5, l2+l6, l3+l7) -> (h0+h2, h1+h3) -> p0 + p1.  Every
+// lane of the group ends with the total (IEEE addition is commutative, so
+// which operand comes first does not matter).
+__device__ __forceinline__ float reduce8(float v) {
+    const int wl = threadIdx.x & 63, base = wl & ~7, l = wl & 7;
+    const float h = v + __shfl(v, base + ((l + 4) & 7), kWave);      // lanes 0-3: h_l = v_l + v_{l+4}
+    const float pp = h + __shfl(h, base + ((l + 2) & 3), kWave);     // lanes 0, 1: p_l = h_l + h_{l+2}
+    return __shfl(pp, base, kWave) + __shfl(pp, base + 1, kWave);
+}
+
+// y[t, row] for one (row, group of up to four tokens) per 32-lane worker.
+template <int BITS>
+__global__ __launch_bounds__(kRoBlock) void ro_gemv_kernel(WeightView w, const float* __restrict__ x, int tokens,
+                                                           float* y, int epilogue) {
+    const int lane = threadIdx.x & 31;
+    const int worker = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 5);
+    const int token_groups = (tokens + 3) / 4;
+    const bool live = worker < w.rows * token_groups;
+    const int row = live ? worker / token_groups : 0;
+    const int t0 = live ? (worker % token_groups) * 4 : 0;
+    const int count = min(4, tokens - t0);
+    const int K = w.cols;
+    const int group = (BITS == 32 || BITS == 16) ? K : w.group;
+    const int groups = K / group;
+    const size_t base = (size_t)row * K;
+    // token of this lane in the multi-token chains (lanes 8 tt .. 8 tt + 7)
+    const int tt = lane >> 3, l = lane & 7;
+    const bool chain = tt < count;
+    const float* xt = x + (size_t)(t0 + (count == 1 ? 0 : min(tt, count - 1))) * K;
+    float result = 0.0f;   // lanes 8 tt: the result of token tt
+    for (int g = 0; g < groups; ++g) {
+        int col = g * group;
+        const int end = col + group;
+        float acc = 0.0f;
+        if (count == 1) {
+            // lane c * 8 + l runs lane l of chain c (a, b, c, d)
+            for (; col + 32 <= end; col += 32) acc = fmaf(lane_value<BITS>(w, base + col + lane), xt[col + lane], acc);
+            const int half = threadIdx.x & 32;
+            const float b = __shfl(acc, half + l + 8, kWave);
+            const float c = __shfl(acc, half + l + 16, kWave);
+            const float d = __shfl(acc, half + l + 24, kWave);
+            acc = (acc + b) + (c + d);                  // lanes 0-7 of the worker: the combined chains
+        }
+        for (; col + 8 <= end; col += 8)
+            acc = fmaf(lane_value<BITS>(w, base + col + l), xt[col + l], acc);
+        float partial = reduce8(acc);
+        float scale = 1.0f;
+        if constexpr (BITS == 8 || BITS == 4) scale = w.scales[(size_t)row * groups + g];
+        for (; col < end; ++col) {
+            float value = lane_value<BITS>(w, base + col);
+            if constexpr (BITS == 8 || BITS == 4) value = (value * scale) / scale;   // Weight::value / scale
+            else if constexpr (BITS == 32) value = value / scale;
+            partial = fmaf(value, xt[col], partial);
+        }
+        if constexpr (BITS == 16) result = 0.0f + partial;                 // one group
+        else result = fmaf(partial, scale, result);
+    }
+    if (live && chain && l == 0) {
+        const size_t index = (size_t)(t0 + tt) * w.rows + row;
+        const float v = result + (w.bias ? w.bias[row] : 0.0f);
+        y[index] = epilogue == kAccumulate ? y[index] + v : v;
+    }
+}
+
+// Dynamic LDS beyond the default 64 KiB must be allowed per kernel first.
+template <typename K>
+void allow_lds(K kernel, size_t bytes, int& allowed) {
+    if (bytes <= 65536 || (int)bytes <= allowed) return;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    allowed = 160 * 1024;
+}
+int g_norm_lds = 0, g_attention_lds = 0;
+
+}  // namespace
+
+// --------------------------------------------------------------- launchers ---
+bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
+                                 hipStream_t stream) {
+    if (width > kReferenceOrderMaxWidth) return false;
+    const size_t lds = 2 * (size_t)width * sizeof(float);
+    allow_lds(ro_norm_kernel, lds, g_norm_lds);
+    ro_norm_kernel<<<rows, kRoBlock, lds, stream>>>(x, width, norm, y);
+    return true;
+}
+
+int reference_order_attention_keys() { return (160 * 1024 - 4096) / 4 - 256; }
+
+bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipStream_t stream) {
+    if (max_keys > reference_order_attention_keys() || p.dim > 256) return false;
+    const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
+    allow_lds(ro_attention_kernel, lds, g_attention_lds);
+    dim3 grid(p.heads, p.tokens);
+    ro_attention_kernel<<<grid, kRoBlock, lds, stream>>>(p);
+    return true;
+}
+
+void launch_activation_reference_order(const float* gate_up, int tokens, int width, int gated, int activation,
+                                       float* act, hipStream_t stream) {
+    const size_t count = (size_t)tokens * width;
+    const int grid = (int)std::min<size_t>((count + kRoBlock - 1) / kRoBlock, 4096);
+    ro_activation_kernel<<<grid, kRoBlock, 0, stream>>>(gate_up, tokens, width, gated, activation, act);
+}
+
+void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream) {
+    const int grid = (int)std::min<size_t>((count + kRoBlock - 1) / kRoBlock, 8192);
+    ro_expf_kernel<<<grid ? grid : 1, kRoBlock, 0, stream>>>(x, count, y);
+}
+
+bool launch_linear_fp_reference_order(const WeightView& w, const float* x, int tokens, float* y, int epilogue,
+                                      hipStream_t stream) {
+    const size_t workers = (size_t)w.rows * ((tokens + 3) / 4);
+    const int grid = (int)((workers * 32 + kRoBlock - 1) / kRoBlock);
+    switch (w.bits) {
+    case 32: ro_gemv_kernel<32><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
+    case 16: ro_gemv_kernel<16><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
+    case 8: ro_gemv_kernel<8><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
+    case 4: ro_gemv_kernel<4><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
+    default: return false;
+    }
+}
+
+}  // namespace leafhip

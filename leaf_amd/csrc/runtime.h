@@ -153,7 +153,10 @@ private:
 class Session {
 public:
     Profiler profiler;
-    Session(Model& model, uint32_t max_context, uint32_t max_prefill);
+    // numerics: LH_NUMERICS_* (DEFAULT reads LEAF_GPU_NUMERICS).
+    Session(Model& model, uint32_t max_context, uint32_t max_prefill, uint32_t numerics = LH_NUMERICS_DEFAULT);
+    // Whether the kernels follow the CPU reference's floating-point order.
+    bool reference_order() const { return reference_; }
     void reset() {
         length = 0;
         device_position_valid_ = false;
@@ -208,6 +211,10 @@ private:
     // fused norm or activation kernel (into xq_ / xs_).
     bool prequantizes(const Linear& l, int tokens) const;
     bool fuse_quantize_ = true;   // LEAF_PREFILL_FUSE=0 turns the fused norm / activation quantization off
+    bool reference_ = false;      // reference-order numerics (LH_NUMERICS_REFERENCE)
+    int reference_keys_ = 0;      // most keys one query may see in reference order
+    void norm(const float* x, int rows, int width, const NormView& n, float* y);
+    void activation(const float* gate_up, int rows, int width, int gated, float* act);
     template <typename F> void timed(int kind, double bytes, double ops, F&& launch) {
         if (profiler.enabled) profiler.begin(stream());
         launch();

@@ -62,10 +62,25 @@ Profiler::~Profiler() {
     for (auto e : events_) (void)hipEventDestroy(e);
 }
 
-Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m) {
+Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t numerics) : model(m) {
     const Config& c = m.config;
     capacity = max_context ? std::min(max_context, c.max_positions) : c.max_positions;
     check(capacity > 0, "session capacity must be positive", LH_ERROR_INVALID_ARGUMENT);
+    check(numerics <= LH_NUMERICS_REFERENCE, "unknown numerics mode", LH_ERROR_INVALID_ARGUMENT);
+    if (numerics == LH_NUMERICS_DEFAULT) {
+        const char* env = std::getenv("LEAF_GPU_NUMERICS");
+        reference_ = env && std::string(env) == "reference";
+    } else {
+        reference_ = numerics == LH_NUMERICS_REFERENCE;
+    }
+    if (reference_) {
+        // The accurate FP32 policy sums its GEMMs in 256-column blocks
+        // (accurate_fp32.h); the reference-order kernels follow dot_avx only.
+        check(!m.accurate, "reference-order numerics do not support accurate FP32 math", LH_ERROR_UNSUPPORTED);
+        check(c.hidden <= uint32_t(kReferenceOrderMaxWidth) && c.head_dim <= 256,
+              "reference-order numerics: hidden or head width too large", LH_ERROR_UNSUPPORTED);
+        reference_keys_ = reference_order_attention_keys();
+    }
     // KV cache for the whole context, [layers][k|v][kv_heads][capacity][dim].
     kv_.allocate(size_t(c.layers) * 2 * c.kv_heads * capacity * c.head_dim * sizeof(float));
     // RoPE tables for every position the cache can hold, from the same float
@@ -102,7 +117,10 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill) : model(m
     const char* fuse = std::getenv("LEAF_PREFILL_FUSE");
     fuse_quantize_ = !(fuse && std::string(fuse) == "0");
     const char* step = std::getenv("LEAF_DECODE_STEP");
-    step_enabled_ = !(step && std::string(step) == "0");
+    step_enabled_ = !(step && std::string(step) == "0") && !reference_;
+    // Graph-replayed decode sizes the reference-order attention for the whole cache.
+    if (reference_ && int(std::min<uint32_t>(capacity, c.sliding_window ? c.sliding_window : capacity)) > reference_keys_)
+        graphs_enabled_ = false;
     if (step_enabled_) step_prepare();
 }
 
@@ -164,7 +182,22 @@ LinearCall Session::make_call(const Linear& l, const float* x, int tokens, float
 }
 
 bool Session::prequantizes(const Linear& l, int tokens) const {
-    return fuse_quantize_ && tokens > 1 && model.integer_linear(l) && !l.input_scale;
+    return fuse_quantize_ && !reference_ && tokens > 1 && model.integer_linear(l) && !l.input_scale;
+}
+
+void Session::norm(const float* x, int rows, int width, const NormView& n, float* y) {
+    if (reference_) {
+        check(launch_norm_reference_order(x, rows, width, n, y, stream()), "reference-order norm rejected",
+              LH_ERROR_UNSUPPORTED);
+    } else {
+        launch_norm(x, rows, width, n, y, stream());
+    }
+}
+
+void Session::activation(const float* gate_up, int rows, int width, int gated, float* act) {
+    const int code = int(model.config.activation);
+    if (reference_) launch_activation_reference_order(gate_up, rows, width, gated, code, act, stream());
+    else launch_activation(gate_up, rows, width, gated, code, act, stream());
 }
 
 void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, int epilogue,
@@ -204,7 +237,15 @@ void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, 
     const int kind = tokens <= 4 ? (call.integer_activations ? Profiler::GemvW8A8 : Profiler::GemvFp)
                                  : (call.integer_activations ? Profiler::GemmW8A8 : Profiler::GemmFp);
     int path = 0;
-    timed(kind, bytes, ops, [&] { path = launch_linear(call, stream()); });
+    if (reference_ && !call.integer_activations) {
+        // dot_avx order (the integer path is exact in every mode)
+        check(!pair && !fuse_norm && !prequantized, "reference-order linear cannot fuse", LH_ERROR_UNSUPPORTED);
+        timed(kind, bytes, ops, [&] {
+            path = launch_linear_fp_reference_order(w, x, tokens, y, epilogue, stream()) ? 1 : -1;
+        });
+    } else {
+        timed(kind, bytes, ops, [&] { path = launch_linear(call, stream()); });
+    }
     check(path > 0, "linear launch rejected", LH_ERROR_UNSUPPORTED);
 }
 
@@ -554,7 +595,8 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* qkv = qkv_.as<float>();
         float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
         float* values = keys + plane;
-        const bool fuse_in = M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv && !L.qkv.input_scale;
+        const bool fuse_in = !reference_ && M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv &&
+                             !L.qkv.input_scale;
         // Single-token W8A8: one launch normalizes, quantizes, projects q|k|v,
         // rotates and appends k, v to the cache.
         PairEpilogue rope;
@@ -578,7 +620,7 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             });
             run_linear(L.qkv, nullptr, M, qkv, kStore, nullptr, nullptr, true);
         } else {
-            launch_norm(hidden, M, h, L.input_norm, normed, s);
+            norm(hidden, M, h, L.input_norm, normed);
             if (L.stacked_qkv) {
                 run_linear(L.qkv, normed, M, qkv, kStore, nullptr);
             } else {
@@ -605,8 +647,8 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             NormView kn{L.k_norm, nullptr, c.epsilon, 0, model.accurate ? 1 : 0};
             for (int t = 0; t < M; ++t) {
                 float* row = qkv + size_t(t) * qkv_width;
-                launch_norm(row, int(c.heads), dim, qn, row, s);
-                launch_norm(row + qw, int(c.kv_heads), dim, kn, row + qw, s);
+                norm(row, int(c.heads), dim, qn, row);
+                norm(row + qw, int(c.kv_heads), dim, kn, row + qw);
             }
         }
         RopeKvCall rk;
@@ -623,9 +665,11 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         // head (decoder.cpp:1375-1387 trims the MLP the same way; here the
         // attention output, projections and MLP of earlier rows are skipped too:
         // rows are independent, so the last row's values do not change).
+        // In reference order the kept rows are the last group of four, so an
+        // FP linear sees the token groups the CPU's linear forms (decoder.cpp:1217-1228).
         const bool trim = last && !all_logits && M > 1;
-        const int rows = trim ? 1 : M;
-        const int first_row = trim ? M - 1 : 0;
+        const int first_row = trim ? (reference_ ? 4 * ((M - 1) / 4) : M - 1) : 0;
+        const int rows = M - first_row;
         AttentionCall at;
         at.q_heads = q_heads_.as<float>(); at.keys = keys; at.values = values; at.out = attn_.as<float>();
         at.heads = int(c.heads); at.kv_heads = int(c.kv_heads); at.tokens = M; at.position = int(position);
@@ -637,8 +681,19 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         {
             // KV bytes read: keys and values of every visible position, per query row.
             const double kv_bytes = 2.0 * 4.0 * c.kv_heads * dim * double(position + M) * (M == 1 ? 1 : 0.5 * M);
-            timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M,
-                  [&] { check(launch_attention(at, s), "attention launch rejected", LH_ERROR_UNSUPPORTED); });
+            if (reference_) {
+                int keys = position_ptr ? int(capacity) : int(position) + M;
+                if (c.sliding_window) keys = std::min(keys, int(c.sliding_window));
+                check(keys <= reference_keys_, "reference-order attention: too many keys for one query",
+                      LH_ERROR_UNSUPPORTED);
+                timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M, [&] {
+                    check(launch_attention_reference_order(at, keys, s), "attention launch rejected",
+                          LH_ERROR_UNSUPPORTED);
+                });
+            } else {
+                timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M,
+                      [&] { check(launch_attention(at, s), "attention launch rejected", LH_ERROR_UNSUPPORTED); });
+            }
         }
         const float* attn_rows = attn_.as<float>() + size_t(first_row) * qw;
         float* hid = hidden + size_t(first_row) * h;
@@ -653,8 +708,8 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* act = act_.as<float>();
         const int f = int(c.intermediate);
         if (c.gated) {
-            const bool fuse_post = rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up &&
-                                   !L.gate_up.input_scale;
+            const bool fuse_post = !reference_ && rows == 1 && model.integer_linear(L.gate_up) &&
+                                   L.stacked_gate_up && !L.gate_up.input_scale;
             PairEpilogue gated;
             gated.mode = kPairGated;
             gated.width = f;
@@ -674,7 +729,7 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                 });
                 run_linear(L.gate_up, nullptr, rows, gate_up, kStore, nullptr, nullptr, true);
             } else {
-                launch_norm(hid, rows, h, L.post_norm, normed, s);
+                norm(hid, rows, h, L.post_norm, normed);
                 if (L.stacked_gate_up) {
                     run_linear(L.gate_up, normed, rows, gate_up, kStore, nullptr);
                 } else {
@@ -690,11 +745,11 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                 }
             }
             if (!fuse_act && !prequantizes(L.down, rows))
-                timed(Profiler::Other, 0, 0, [&] { launch_activation(gate_up, rows, f, 1, int(c.activation), act, s); });
+                timed(Profiler::Other, 0, 0, [&] { activation(gate_up, rows, f, 1, act); });
         } else {
-            launch_norm(hid, rows, h, L.post_norm, normed, s);
+            norm(hid, rows, h, L.post_norm, normed);
             run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
-            launch_activation(gate_up, rows, f, 0, int(c.activation), act, s);
+            activation(gate_up, rows, f, 0, act);
         }
         const bool down_q = c.gated && prequantizes(L.down, rows) &&
                             !(rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up);
@@ -711,13 +766,13 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             run_linear(L.down, act, rows, proj, kStore, nullptr, nullptr, down_q);
             launch_residual(hid, proj, attn_proj, rows * h, s);              // hidden += proj + attn_proj
         }
-        if (trim) hidden = hid;   // the final norm and head see only the last row
+        if (trim) hidden = hid + size_t(rows - 1) * h;   // the final norm and head see only the last row
     }
     const int head_rows = all_logits ? M : 1;
     // `hidden` now points at the rows the head reads: all rows, or the last one.
     const float* x = hidden;
     if (c.final_norm) {
-        launch_norm(hidden, head_rows, h, model.final_norm, normed, s);
+        norm(hidden, head_rows, h, model.final_norm, normed);
         x = normed;
     }
     run_linear(model.head, x, head_rows, logits_.as<float>(), kStore, nullptr);

@@ -9,6 +9,7 @@ library owns device memory and streams.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 from pathlib import Path
@@ -45,7 +46,11 @@ class ProfileEntry(C.Structure):
 
 
 class SessionOptions(C.Structure):
-    _fields_ = [("max_context", C.c_uint32), ("max_prefill", C.c_uint32)]
+    _fields_ = [("max_context", C.c_uint32), ("max_prefill", C.c_uint32), ("numerics", C.c_uint32)]
+
+
+# Floating-point order of a session or of kernel-level calls (include/leafhip.h).
+NUMERICS = {"default": 0, "fast": 1, "reference": 2}
 
 
 class Weight(C.Structure):
@@ -54,6 +59,19 @@ class Weight(C.Structure):
 
 
 _lib = None
+_exiting = False
+
+
+def _mark_exiting() -> None:
+    # Objects still alive at interpreter exit are not released through the
+    # library: finalizers then run in no fixed order, possibly after the HIP
+    # runtime (or a profiler attached to it) has begun shutting down.  Close
+    # them explicitly to release device memory earlier.
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_mark_exiting)
 
 
 def library(path: Path | None = None) -> C.CDLL:
@@ -108,6 +126,8 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_silu_gate": ([vp, sz, sz, vp, vp], i32),
         "lh_activation": ([vp, sz, u32, vp, vp], i32),
         "lh_argmax": ([vp, sz, sz, vp, vp], i32),
+        "lh_set_kernel_numerics": ([u32], i32),
+        "lh_expf": ([vp, sz, vp, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -159,7 +179,9 @@ class DeviceArray:
             library().lh_device_free(self.ptr)
             self.ptr = None
 
-    __del__ = free
+    def __del__(self):
+        if not _exiting:
+            self.free()
 
 
 class DeviceWeight:
@@ -186,7 +208,7 @@ class Decoder:
     """leaf::runtime::Decoder on one MI355X (engine/include/leaf/runtime/decoder.h:15-50)."""
 
     def __init__(self, artifact: str | os.PathLike, activation_bits: int = 32, fp32_math: str = "fast",
-                 device: int = 0, max_context: int = 0, max_prefill: int = 0):
+                 device: int = 0, max_context: int = 0, max_prefill: int = 0, numerics: str = "default"):
         lib = library()
         if fp32_math not in ("fast", "accurate"):
             raise RuntimeError("Leaf decoder: invalid FP32 math policy")
@@ -197,7 +219,7 @@ class Decoder:
         try:
             check(lib.lh_model_load_file(self._ctx, str(artifact).encode(), activation_bits,
                                          1 if fp32_math == "accurate" else 0, C.byref(self._model)))
-            options = SessionOptions(max_context, max_prefill)
+            options = SessionOptions(max_context, max_prefill, NUMERICS[numerics])
             check(lib.lh_session_create(self._model, C.byref(options), C.byref(self._session)))
         except Exception:
             self.close()
@@ -224,7 +246,9 @@ class Decoder:
             lib.lh_context_destroy(self._ctx)
             self._ctx = C.c_void_p()
 
-    __del__ = close
+    def __del__(self):
+        if not _exiting:
+            self.close()
 
     def __enter__(self):
         return self
@@ -315,6 +339,15 @@ def linear_q(weight: DeviceWeight, q: DeviceArray, scales: DeviceArray, tokens: 
                                 acc.ptr if acc is not None else None, stream))
 
 
+def set_kernel_numerics(numerics: str) -> None:
+    """Numerics of this thread's kernel-level calls: "fast" or "reference"."""
+    check(library().lh_set_kernel_numerics(NUMERICS[numerics]))
+
+
+def expf(x: DeviceArray, y: DeviceArray, stream=None) -> None:
+    check(library().lh_expf(x.ptr, int(np.prod(x.shape)), y.ptr, stream))
+
+
 def quantize_rows(x: DeviceArray, rows: int, cols: int, q: DeviceArray, scales: DeviceArray, stream=None) -> None:
     check(library().lh_quantize_rows_i8(x.ptr, rows, cols, q.ptr, scales.ptr, stream))
 
@@ -334,7 +367,9 @@ class Stream:
             library().lh_stream_destroy(self.handle)
             self.handle = C.c_void_p()
 
-    __del__ = close
+    def __del__(self):
+        if not _exiting:
+            self.close()
 
 
 class Graph:
@@ -358,7 +393,9 @@ class Graph:
             library().lh_graph_destroy(self.handle)
             self.handle = C.c_void_p()
 
-    __del__ = close
+    def __del__(self):
+        if not _exiting:
+            self.close()
 
 
 class Timer:

@@ -62,6 +62,8 @@ class Oracle:
                                          C.c_float]
         lib.oracle_activate.argtypes = [C.c_uint, C.c_float]
         lib.oracle_activate.restype = C.c_float
+        lib.oracle_activation.argtypes = [_f32p, _sz, _sz, C.c_int, C.c_uint, _f32p]
+        lib.oracle_expf.argtypes = [_f32p, _sz, _f32p]
         lib.oracle_quantize_weights.argtypes = [_f32p, _sz, _sz, C.c_uint, _sz, _u8p, _f32p]
         lib.oracle_decoder_open.argtypes = [C.c_char_p, C.c_uint, C.c_int, C.c_char_p, _sz]
         lib.oracle_decoder_open.restype = C.c_void_p
@@ -151,6 +153,18 @@ class Oracle:
         return np.array([self.lib.oracle_activate(code, float(v)) for v in np.asarray(x, np.float32).ravel()],
                         np.float32).reshape(np.shape(x))
 
+    def activation(self, gate_up, tokens, width, gated, code):
+        gate_up = np.ascontiguousarray(gate_up, np.float32)
+        act = np.empty((tokens, width), np.float32)
+        self.lib.oracle_activation(gate_up, tokens, width, int(gated), code, act)
+        return act
+
+    def expf(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.oracle_expf(x, x.size, y)
+        return y
+
     def quantize_weights(self, w, bits, group):
         w = np.ascontiguousarray(w, np.float32)
         rows, cols = w.shape
@@ -216,7 +230,23 @@ class Reference:
         lib.ref_linear_fp.argtypes = [C.c_uint, _sz, _sz, _sz, C.c_void_p, C.c_void_p, C.c_void_p, _f32p, _sz, _f32p]
         lib.ref_linear_accurate.argtypes = [C.c_uint, _sz, _sz, C.c_void_p, C.c_void_p, _f32p, _sz, _f32p]
         lib.ref_norm.argtypes = [_f32p, _sz, _sz, _f32p, C.c_void_p, C.c_float, C.c_uint, C.c_int, _f32p]
+        lib.ref_decoder_greedy.argtypes = [C.c_char_p, C.c_uint, C.c_uint, C.c_int, _u32p, _sz, C.c_uint, _u32p,
+                                           C.POINTER(C.c_uint), _sz, _f32p, C.c_char_p, _sz]
+        lib.ref_decoder_greedy.restype = C.c_int
         self.features = lib.ref_cpu_features()
+
+    def greedy(self, path, prompt, limit, activation_bits=32, accurate=False, keep=(0,), threads=8, vocab=None):
+        """The real Decoder's greedy run: (tokens, logits of the forwards in `keep`)."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        keep_arr = (C.c_uint * len(keep))(*keep)
+        tokens = np.empty(max(limit, 1), np.uint32)
+        logits = np.empty((len(keep), vocab), np.float32)
+        err = C.create_string_buffer(512)
+        n = self.lib.ref_decoder_greedy(str(path).encode(), threads, activation_bits, int(accurate), prompt,
+                                        len(prompt), limit, tokens, keep_arr, len(keep), logits, err, 512)
+        if n < 0:
+            raise RuntimeError(err.value.decode())
+        return tokens[:n], logits
 
     def quantize_rows(self, x):
         x = np.ascontiguousarray(x, np.float32)

@@ -701,6 +701,25 @@ void oracle_attention(const float* q_heads, const float* keys, const float* valu
 
 float oracle_activate(unsigned activation_code, float x) { return activate(activation_code, x); }
 
+void oracle_activation(const float* gate_up, size_t tokens, size_t width, int gated, unsigned activation_code,
+                       float* act) {
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t j = 0; j < width; ++j) {
+            if (gated) {
+                float up = gate_up[t * 2 * width + width + j];
+                up *= activate(activation_code, gate_up[t * 2 * width + j]);
+                act[t * width + j] = up;
+            } else {
+                act[t * width + j] = activate(activation_code, gate_up[t * width + j]);
+            }
+        }
+}
+
+void oracle_expf(const float* x, size_t count, float* y) {
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < long(count); ++i) y[i] = std::exp(x[i]);
+}
+
 // export_decoder.quantize (tools/export_decoder.py:91-105) in float32.
 void oracle_quantize_weights(const float* w, size_t rows, size_t cols, unsigned bits, size_t group,
                              uint8_t* packed, float* scales) {

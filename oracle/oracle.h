@@ -54,6 +54,13 @@ void oracle_attention(const float* q_heads, const float* keys, const float* valu
                       size_t tokens, size_t total, size_t stride, size_t dim, float scale);
 // R12: activation function by header code.
 float oracle_activate(unsigned activation, float x);
+// R12 over rows: gated, act[t,j] = up[t,j] * activate(gate[t,j]) with
+// gate_up = [tokens, 2 width] = [gate | up] (decoder.cpp:1414); otherwise
+// act = activate(x) over [tokens, width].
+void oracle_activation(const float* gate_up, size_t tokens, size_t width, int gated, unsigned activation,
+                       float* act);
+// The libm expf the reference's softmax and SiLU call (std::exp on float).
+void oracle_expf(const float* x, size_t count, float* y);
 // R16: weight quantization (export side); packed is int8 [rows,cols] or nibble-packed.
 void oracle_quantize_weights(const float* w, size_t rows, size_t cols, unsigned bits, size_t group,
                              uint8_t* packed, float* scales);

@@ -14,6 +14,7 @@
 #include LEAF_REFERENCE_DECODER_CPP
 
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 
 using leaf::runtime::Weight;
@@ -172,6 +173,46 @@ void ref_norm(const float* x, std::size_t M, std::size_t width, const float* gam
     Weight b = make_weight(32, 1, width, 0, beta, nullptr);
     leaf::runtime::norm(input, g, beta ? &b : nullptr, epsilon, kind, output, width, accurate != 0);
     std::memcpy(out, output.data(), M * width * sizeof(float));
+}
+
+// The real Decoder's greedy continuation, as generate_continuation runs it
+// (engine/src/main_decoder.cpp:95-113): forward_into(prompt) without
+// all-token logits, the first maximal index, then one forward per token, up
+// to `limit` tokens or an EOS token.  Writes the tokens and, for each forward
+// index listed in `keep` (0 = the prompt, i = the i-th single-token step), its
+// logits into logits[k * vocab].  Returns the number of tokens, or -1 with the
+// error text.
+int ref_decoder_greedy(const char* artifact, unsigned threads, unsigned activation_bits, int accurate,
+                       const std::uint32_t* prompt, std::size_t count, unsigned limit, std::uint32_t* tokens,
+                       const unsigned* keep, std::size_t keep_count, float* logits, char* error,
+                       std::size_t error_size) {
+    try {
+        leaf::runtime::Decoder decoder(artifact, threads, false, activation_bits, {},
+                                       accurate ? leaf::runtime::FP32Math::Accurate : leaf::runtime::FP32Math::Fast);
+        const std::size_t vocab = decoder.vocabulary_size();
+        std::vector<float> out;
+        std::vector<std::uint32_t> ids(prompt, prompt + count);
+        auto record = [&](unsigned forward) {
+            for (std::size_t k = 0; k < keep_count; ++k)
+                if (keep[k] == forward) std::memcpy(logits + k * vocab, out.data(), vocab * sizeof(float));
+        };
+        decoder.forward_into(ids, out);
+        record(0);
+        int produced = 0;
+        for (unsigned token = 0; token < limit; ++token) {
+            const auto id = static_cast<std::uint32_t>(std::max_element(out.begin(), out.end()) - out.begin());
+            tokens[produced++] = id;
+            if (decoder.is_eos_token(id)) break;
+            if (token + 1 < limit) {
+                decoder.forward_into({id}, out);
+                record(token + 1);
+            }
+        }
+        return produced;
+    } catch (const std::exception& e) {
+        std::snprintf(error, error_size, "%s", e.what());
+        return -1;
+    }
 }
 
 }  // extern "C"

@@ -5,7 +5,8 @@ oracle/Makefile into oracle/_ref/: the real leaf_decoder binary and a harness
 exposing its kernels).  The fixtures are data: inputs and the reference's
 outputs.  Regenerate with
 
-    make -C oracle && python tests/golden/make_golden.py
+    make -C oracle && python tests/golden/make_golden.py          # kernels, reduced decoders
+    make -C oracle && python tests/golden/make_golden.py --full   # configured sizes (minutes)
 """
 from __future__ import annotations
 
@@ -150,9 +151,60 @@ def decoder_vectors(tmp: Path) -> tuple[dict, dict]:
     return arrays, meta
 
 
+# The benchmark configurations at their configured sizes: (prompt tokens,
+# greedy tokens, prompt seed).  Artifacts: models.PRESETS[family]() written
+# with FULL_ARTIFACT_SEED.  The real reference Decoder runs the greedy loop;
+# the fixture keeps the tokens, and the logits of the prefill (forward 0) and
+# of the last single-token forward.
+FULL_ARTIFACT_SEED = 20261202
+FULL_CASES = {
+    "gpt2": (16, 32, 1),
+    "tinyllama": (512, 128, 3),
+    "qwen": (4096, 256, 4),
+    "smollm2": (2048, 256, 5),
+}
+
+
+def full_prompt(family: str) -> np.ndarray:
+    length, _, seed = FULL_CASES[family]
+    vocab = models.PRESETS[family]().vocab
+    return np.random.default_rng(seed).integers(0, vocab, length).astype(np.uint32)
+
+
+def full_config_vectors(tmp: Path, ref: Reference, families) -> tuple[dict, dict]:
+    arrays, meta = {}, {}
+    for family in families:
+        spec = models.PRESETS[family]()
+        art = tmp / f"{family}_full.leaf"
+        write_artifact(art, spec, seed=FULL_ARTIFACT_SEED)
+        bits, math = models.RUN_POLICY[family]
+        length, limit, seed = FULL_CASES[family]
+        prompt = full_prompt(family)
+        tokens, logits = ref.greedy(art, prompt, limit, activation_bits=bits, accurate=math == "accurate",
+                                    keep=(0, limit - 1), vocab=spec.vocab)
+        arrays[f"{family}_tokens"] = tokens
+        arrays[f"{family}_prefill_logits"] = logits[0]
+        arrays[f"{family}_last_logits"] = logits[1]
+        meta[family] = {"artifact_sha256": artifact_digest(art), "artifact_seed": FULL_ARTIFACT_SEED,
+                        "activation_bits": bits, "fp32_math": math, "prompt_tokens": length,
+                        "prompt_seed": seed, "generate": limit, "last_forward": limit - 1}
+        print(f"{family}: {len(tokens)} tokens from the reference", flush=True)
+        art.unlink()
+    return arrays, meta
+
+
 def main() -> None:
     subprocess.run(["make", "-C", str(ROOT / "oracle"), "-s"], check=True)
     ref = Reference()
+    if "--full" in sys.argv:
+        # the configured sizes only (minutes: the reference's attention is scalar)
+        with tempfile.TemporaryDirectory() as tmp:
+            arrays, meta = full_config_vectors(Path(tmp), ref, FULL_CASES)
+        np.savez_compressed(OUT / "full_configs.npz", **arrays)
+        meta["reference_cpu_features"] = ref.features
+        (OUT / "full_configs.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
+        print("full_configs.npz", (OUT / "full_configs.npz").stat().st_size, "bytes")
+        return
     kernels = kernel_vectors(ref)
     np.savez_compressed(OUT / "kernels.npz", **kernels)
     with tempfile.TemporaryDirectory() as tmp:
