@@ -32,6 +32,19 @@ struct StepLayer {
     const float* post_gamma = nullptr;
 };
 
+// Diagnostics: the integer stages of one step, recorded by a separately
+// compiled variant of the kernel (null pointers: off).  Per layer, phase p of
+// 0 q|k|v, 1 o_proj, 2 gate|up, 3 down_proj: the f32 vector the phase
+// quantizes (block 0's copy: the normalized layer input, the attention
+// output, the normalized mid vector, the gated activation), its int8 values
+// and per-token scale, and the exact int32 dot of every output row.
+struct StepCapture {
+    float* x = nullptr;        // [layers][4][kStepMaxFfn]
+    int8_t* q = nullptr;       // [layers][4][kStepMaxFfn]
+    float* sx = nullptr;       // [layers][4]
+    int32_t* acc = nullptr;    // [layers][4][2 * kStepMaxFfn] (q|k|v rows, o rows, gate then up rows, down rows)
+};
+
 struct StepParams {
     int layers = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, rotary = 0, vocab = 0;
     int window = 0, capacity = 0, activation = 0;
@@ -55,7 +68,7 @@ struct StepParams {
     // merge waves of a head pair then sit on one XCD (block b runs on XCD b % 8), the items write
     // with plain stores that stay in that XCD's L2 and the merge waves read them from there.
     unsigned long long* x_part_local = nullptr;
-    int xcd_check_flip = 0;                     // tests: nonzero makes the XCD check fail (forces the fallback)
+    int xcd_check_flip = 0;                     // tests: nonzero fails the last block's XCD check (forces the fallback)
     // The q rows of each head slice, in plain device memory, for XCD-local q (null: off): the
     // rows of a slice are computed on its XCD and its items read them from that XCD's L2.
     unsigned long long* x_q_local = nullptr;
@@ -69,6 +82,7 @@ struct StepParams {
     unsigned long long* trace = nullptr;        // [blocks][kStepTracePoints] clock stamps, or null
     int position = 0;                           // index of this token in the cache
     unsigned epoch = 0;                         // launch tag (launch number << 12)
+    StepCapture capture;                        // diagnostics, off unless set
 };
 
 // Whether a decoder of this geometry runs on the persistent step kernel.

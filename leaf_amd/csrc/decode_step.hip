@@ -180,9 +180,16 @@ __device__ __forceinline__ u64 fetch(const u64* p) {
 __device__ __forceinline__ bool aborted(const unsigned* flag) {
     return __hip_atomic_load((const LEAF_GLOBAL unsigned*)flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
+// The first code raised stands: a wave that gives up only because another
+// block aborted must not overwrite the reason the host acts on (a mismatched
+// XCD, which makes the host run the step again, against a timeout).  Only the
+// block that raised first writes the host copy.
 __device__ __forceinline__ void raise_abort(const StepParams& P, unsigned why = 1u) {
-    __hip_atomic_store((LEAF_GLOBAL unsigned*)P.abort_flag, why, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (P.host_abort) *P.host_abort = why;
+    unsigned expected = 0u;
+    if (__hip_atomic_compare_exchange_strong((LEAF_GLOBAL unsigned*)P.abort_flag, &expected, why, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &&
+        P.host_abort)
+        *P.host_abort = why;
 }
 // Abort code: a block did not run on XCD blockIdx.x % 8, so the XCD-local
 // merge cannot work (the host turns it off and runs the step again).
@@ -869,7 +876,37 @@ __device__ __forceinline__ int local_qkv_pair(const AttnPlan& a, const StepParam
 }
 
 // ======================================================= exchange role ===
+// Diagnostics (CAP): block 0 records phase `phase` of layer L -- this lane's
+// runs of the f32 vector it quantized, their int8 values (read back from the
+// LDS runs this lane wrote) and the scale.
+template <bool CAP, int N>
+__device__ __forceinline__ void capture_input(const StepParams& P, const Shared& s, const float (&x)[N], int n,
+                                              int buf, int L, int phase, int a) {
+    if constexpr (CAP) {
+        if (blockIdx.x != 0) return;
+        const size_t at = ((size_t)L * 4 + phase) * kStepMaxFfn;
+#pragma unroll
+        for (int g = 0; g < N / kRun; ++g)
+#pragma unroll
+            for (int j = 0; j < kRun; ++j) {
+                const int e = kRun * run_of(g, a) + j;
+                if (e < n) {
+                    P.capture.x[at + e] = x[kRun * g + j];
+                    P.capture.q[at + e] = s.xq[buf][e];
+                }
+            }
+        if (a == 0) P.capture.sx[L * 4 + phase] = s.sx[buf];
+    }
+}
+
+// The exact int32 dot of output row `row` of phase `phase` (CAP only).
+template <bool CAP>
+__device__ __forceinline__ void capture_acc(const StepParams& P, int L, int phase, int row, int acc) {
+    if constexpr (CAP) P.capture.acc[((size_t)L * 4 + phase) * (2 * kStepMaxFfn) + row] = acc;
+}
+
 // Returns false when the kernel is abandoned (abort).
+template <bool CAP>
 __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     int a = threadIdx.x;                     // 0 .. kAT - 1
     const int G = gridDim.x, b = blockIdx.x;
@@ -959,6 +996,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         }
         store_runs(s.h_in, x, a);
         if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        capture_input<CAP>(P, s, x, H, 0, L, 0, a);
         post(s, 4 * L + 0);
         stamp(P.trace, b, 64 * L + 2);
         if (has_item) {
@@ -1095,6 +1133,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             stamp(P.trace, b, 64 * L + 5);
             stamp(P.trace, b, 64 * L + 58, kWave);
             if (!quantize_into(xa, qw, 1, a, s, round)) return false;
+            capture_input<CAP>(P, s, xa, qw, 1, L, 1, a);
             post(s, 4 * L + 1);
         }
         // ---- after o_proj -> RMSNorm -> int8 for gate|up
@@ -1112,6 +1151,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 59, kWave);
         store_runs(s.h_mid, x, a);
         if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        capture_input<CAP>(P, s, x, H, 0, L, 2, a);
         post(s, 4 * L + 2);
         // ---- SiLU-gated activation -> int8 for down_proj
         {
@@ -1123,6 +1163,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             note_received(s, 4 * L + 3);
             stamp(P.trace, b, 64 * L + 7);
             if (!quantize_into(xd, F, 1, a, s, round)) return false;
+            capture_input<CAP>(P, s, xd, F, 1, L, 3, a);
             post(s, 4 * L + 3);
         }
         // ---- the next layer's input (the last layer's feeds the head below)
@@ -1161,6 +1202,7 @@ struct LayerRows {
     RowScale gs;   // per lane: the gate|up row whose total this lane's 8-lane group holds
 };
 
+template <bool CAP>
 __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     const int t = threadIdx.x, lane = t & 63;
     const int bw = __builtin_amdgcn_readfirstlane((t >> 6) - kA);   // 0 .. kB - 1, wave-uniform
@@ -1266,6 +1308,8 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                     const int a1 = row_dot(w.q[k][1], s.xq[0], H / 16, lane);
                     if (lane == 0) {
                         const int r0 = qr[k][0], r1 = qr[k][1];
+                        capture_acc<CAP>(P, L, 0, r0, a0);
+                        capture_acc<CAP>(P, L, 0, r1, a1);
                         float v0 = dequant(a0, sx, w.qs[k][0].scale, w.qs[k][0].bias);
                         float v1 = dequant(a1, sx, w.qs[k][1].scale, w.qs[k][1].bias);
                         const int hb = r0 / dim, i0 = r0 % dim, i1 = r1 % dim, half = P.rotary / 2;
@@ -1315,6 +1359,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
             const int p0 = has_r[0] ? row_part(w.o[0], xc, chunks, lane) : 0;
             const int p1 = has_r[1] ? row_part(w.o[1], xc, chunks, lane) : 0;
             const int acc = sum2_transposed(p0, p1);
+            if ((lane & 31) == 0 && r_live) capture_acc<CAP>(P, L, 1, r_row, acc);
             if ((lane & 31) == 0 && r_live)
                 publish(P.x_mid + r_row, epoch(L, 4), s.h_in[r_row] + dequant(acc, sx, w.os.scale, w.os.bias));
         }
@@ -1347,7 +1392,9 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
                 part[k] = has_g[k] ? row_part(w.g[k][0], xc, chunks, lane) : 0;
                 part[kGP + k] = has_g[k] ? row_part(w.g[k][1], xc, chunks, lane) : 0;
             }
-            const float mine = dequant(sum8_transposed(part, lane), sx, w.gs.scale, w.gs.bias);
+            const int total = sum8_transposed(part, lane);
+            if ((lane & 7) == 0 && g_live) capture_acc<CAP>(P, L, 2, g_row, total);
+            const float mine = dequant(total, sx, w.gs.scale, w.gs.bias);
             const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
                                                                              __float_as_uint(mine), false, false)[1]);
             if (lane < 32 && (lane & 7) == 0 && g_live)
@@ -1374,6 +1421,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
             const int p0 = has_r[0] ? row_part(w.d[0], xc, chunks, lane) : 0;
             const int p1 = has_r[1] ? row_part(w.d[1], xc, chunks, lane) : 0;
             const int acc = sum2_transposed(p0, p1);
+            if ((lane & 31) == 0 && r_live) capture_acc<CAP>(P, L, 3, r_row, acc);
             if ((lane & 31) == 0 && r_live)
                 publish(P.x_hidden + r_row, epoch(L, 6), s.h_mid[r_row] + dequant(acc, sx, w.ds.scale, w.ds.bias));
         }
@@ -1384,6 +1432,7 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     return wait_ready(s, 4 * P.layers);
 }
 
+template <bool CAP>
 __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     __shared__ Shared s;
     const int t = threadIdx.x, lane = t & 63;
@@ -1404,8 +1453,13 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         for (int i = t; i < words; i += kT) dst[i] = ldg(src + i);
     }
     __syncthreads();
-    if (P.x_part_local && t == 0 && (xcc_id() ^ P.xcd_check_flip) != (b & 7)) raise_abort(P, kAbortXcdMapping);
-    const bool ok = wave < kA ? exchange_role(P, s) : weight_role(P, s);
+    // Tests force a failed check on the last block, which then leaves at once:
+    // the other blocks find its outputs missing and leave through their
+    // bounded waits, and the host must still see the mismatch code.
+    const bool forced = P.x_part_local && P.xcd_check_flip && b == G - 1;
+    if (P.x_part_local && t == 0 && (forced || xcc_id() != (b & 7))) raise_abort(P, kAbortXcdMapping);
+    if (forced) return;
+    const bool ok = wave < kA ? exchange_role<CAP>(P, s) : weight_role<CAP>(P, s);
     if (__syncthreads_or(!ok)) return;          // every wave leaves when one gave up (abort flags raised)
 
     // ---------------- FP32 LM head and greedy argmax (all waves)
@@ -1501,10 +1555,12 @@ int decode_step_spans(int keys) { return (keys + kStepSpanKeys - 1) / kStepSpanK
 int decode_step_blocks(int device) {
     int cus = 0, resident = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, reinterpret_cast<const void*>(decode_step_kernel), kT,
-                                                     0) != hipSuccess)
-        return 0;
-    return resident >= 1 ? cus : 0;
+    for (const void* kernel : {reinterpret_cast<const void*>(decode_step_kernel<false>),
+                               reinterpret_cast<const void*>(decode_step_kernel<true>)}) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kernel, kT, 0) != hipSuccess || resident < 1)
+            return 0;
+    }
+    return cus;
 }
 
 bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int vocab, int blocks) {
@@ -1520,8 +1576,9 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
 hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream) {
     StepParams p = params;
     void* args[] = {&p};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(blocks), dim3(kT), args,
-                                      0, stream);
+    const void* kernel = p.capture.x ? reinterpret_cast<const void*>(decode_step_kernel<true>)
+                                     : reinterpret_cast<const void*>(decode_step_kernel<false>);
+    return hipLaunchCooperativeKernel(kernel, dim3(blocks), dim3(kT), args, 0, stream);
 }
 
 }  // namespace leafhip

@@ -192,7 +192,8 @@ private:
     double step_bytes_ = 0;          // algorithmic bytes of one step, without KV
     double step_kv_bytes_ = 0;       // KV bytes per visible key
     StepParams step_;
-    DeviceBuffer step_layers_, step_trace_, step_part_local_, step_q_local_;
+    DeviceBuffer step_layers_, step_trace_, step_part_local_, step_q_local_, step_capture_;
+    std::string step_capture_path_;
     UncachedBuffer step_exchange_;
     std::string step_trace_path_;
     unsigned* step_host_abort_ = nullptr;

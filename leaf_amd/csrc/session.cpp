@@ -426,9 +426,10 @@ void Session::step_prepare() {
             hip_check(hipMemset(step_q_local_.ptr, 0, step_q_local_.bytes), "hipMemset");
             p.x_q_local = step_q_local_.as<unsigned long long>();
         }
-        // LEAF_DECODE_STEP_FORCE_XCD_MISMATCH=1 (tests): the first step's XCD
-        // check fails, so the fallback to the memory-based merge runs.
-        if (const char* flip = std::getenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH")) p.xcd_check_flip = std::atoi(flip) ? 8 : 0;
+        // LEAF_DECODE_STEP_FORCE_XCD_MISMATCH=1 (tests): the last block's XCD
+        // check fails and it leaves at once, so the step aborts and the
+        // fallback to the memory-based merge runs.
+        if (const char* flip = std::getenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH")) p.xcd_check_flip = std::atoi(flip) ? 1 : 0;
     }
     p.counters = reinterpret_cast<unsigned*>(w);
     p.abort_flag = p.counters + c.kv_heads;
@@ -468,6 +469,21 @@ void Session::step_prepare() {
     // LEAF_DECODE_STEP_ITEM_HEADS=<n>: at least n query heads per exchange
     // wave in each attention item (wider items, fewer blocks; for tests).
     if (const char* heads = std::getenv("LEAF_DECODE_STEP_ITEM_HEADS")) p.item_heads = std::max(1, std::atoi(heads));
+    // LEAF_DECODE_STEP_CAPTURE=<file>: run the kernel's capture variant and
+    // append every step's integer stages to the file: "LHSC", u32 layers,
+    // u32 max_ffn, then x f32 [layers][4][max_ffn], q i8 [layers][4][max_ffn],
+    // sx f32 [layers][4], acc i32 [layers][4][2 max_ffn] (StepCapture).
+    if (const char* capture = std::getenv("LEAF_DECODE_STEP_CAPTURE")) {
+        step_capture_path_ = capture;
+        const size_t vec = size_t(c.layers) * 4 * kStepMaxFfn;
+        step_capture_.allocate(vec * 4 + vec + size_t(c.layers) * 4 * 4 + 2 * vec * 4);
+        hip_check(hipMemset(step_capture_.ptr, 0, step_capture_.bytes), "hipMemset");
+        auto* base = static_cast<uint8_t*>(step_capture_.ptr);
+        p.capture.x = reinterpret_cast<float*>(base);
+        p.capture.q = reinterpret_cast<int8_t*>(base + vec * 4);
+        p.capture.sx = reinterpret_cast<float*>(base + vec * 5);
+        p.capture.acc = reinterpret_cast<int32_t*>(base + vec * 5 + size_t(c.layers) * 16);
+    }
     // LEAF_DECODE_STEP_TRACE=<file>: append every step's phase timeline
     // (blocks x kStepTracePoints u64 stamps of the 100 MHz device clock).
     if (const char* trace = std::getenv("LEAF_DECODE_STEP_TRACE")) {
@@ -545,6 +561,16 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
             return;
         }
         check(false, "decode step timed out waiting for another block", LH_ERROR_DEVICE);
+    }
+    if (!step_capture_path_.empty()) {
+        std::vector<uint8_t> bytes(step_capture_.bytes);
+        hip_check(hipMemcpy(bytes.data(), step_capture_.ptr, bytes.size(), hipMemcpyDeviceToHost), "capture copy");
+        if (FILE* f = std::fopen(step_capture_path_.c_str(), "ab")) {
+            const uint32_t head[3] = {0x4353484cu, uint32_t(c.layers), uint32_t(kStepMaxFfn)};   // "LHSC"
+            std::fwrite(head, 4, 3, f);
+            std::fwrite(bytes.data(), 1, bytes.size(), f);
+            std::fclose(f);
+        }
     }
     if (!step_trace_path_.empty()) {
         std::vector<unsigned long long> stamps(step_trace_.bytes / 8);

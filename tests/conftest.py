@@ -50,3 +50,21 @@ def artifacts(tmp_path_factory):
         write_artifact(path, decoder_spec(family), seed=101)
         out[family] = path
     return out
+
+
+@pytest.fixture(scope="session")
+def full_artifacts(tmp_path_factory):
+    """The benchmark configurations' full-size synthetic artifacts, written on first use."""
+    from leaf_amd import models
+    from leaf_amd.artifact import write_artifact
+    from tests.golden.make_golden import FULL_ARTIFACT_SEED
+    root = tmp_path_factory.mktemp("full")
+    cache = {}
+
+    def get(family):
+        if family not in cache:
+            path = root / f"{family}.leaf"
+            write_artifact(path, models.PRESETS[family](), seed=FULL_ARTIFACT_SEED)
+            cache[family] = path
+        return cache[family]
+    return get

@@ -49,20 +49,6 @@ def rt():
     return runtime
 
 
-@pytest.fixture(scope="module")
-def full_artifacts(tmp_path_factory):
-    root = tmp_path_factory.mktemp("full")
-    cache = {}
-
-    def get(family):
-        if family not in cache:
-            path = root / f"{family}.leaf"
-            write_artifact(path, models.PRESETS[family](), seed=20261202)
-            cache[family] = path
-        return cache[family]
-    return get
-
-
 def teacher_forced(dec, od, prompt, steps, tolerance):
     """Prefill, then `steps` decode steps fed the oracle's greedy token; returns
     the worst relative logit error and the tokens."""
