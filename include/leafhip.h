@@ -205,6 +205,20 @@ lh_status lh_quantize_rows_i8(const float* x, size_t rows, size_t cols, int8_t* 
  * larger ones the MFMA GEMMs. */
 lh_status lh_linear(const lh_weight* weight, const float* x, size_t tokens, uint32_t activation_bits, float* y,
                     int32_t* acc, lh_stream stream);
+/* lh_linear without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The integer path's
+ * scratch -- the quantized input, its per-token scales and split-K sums -- is
+ * a fixed device array of LH_NOALLOC_SCRATCH_BYTES per GPU, present from
+ * library load until the process ends; nothing in it has to start at zero.
+ * A call whose quantized input and scales need more than the array
+ * (about tokens * (cols + 4) bytes) fails with LH_ERROR_INVALID_ARGUMENT;
+ * the split-K sums use what is left.  Every call on one GPU shares the
+ * array: calls that overlap (other streams, other threads) race.  Results
+ * equal lh_linear's bit for bit. */
+#define LH_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+lh_status lh_linear_noalloc(const lh_weight* weight, const float* x, size_t tokens, uint32_t activation_bits,
+                            float* y, int32_t* acc, lh_stream stream);
 /* The integer path from already-quantized activations (q [tokens, cols], scales [tokens]). */
 lh_status lh_linear_q(const lh_weight* weight, const int8_t* q, const float* scales, size_t tokens, float* y,
                       int32_t* acc, lh_stream stream);

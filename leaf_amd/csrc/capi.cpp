@@ -115,6 +115,31 @@ unsigned* attention_counters(hipStream_t stream) {
 // Numerics of this thread's kernel-level calls (lh_set_kernel_numerics).
 thread_local bool t_reference_order = false;
 
+// Scratch of lh_linear_noalloc: a device array that exists from module load
+// to process end, one copy per GPU, so that entry point allocates nothing.
+// Host code never uses the array's name as an address: its per-device
+// address comes from hipGetSymbolAddress, resolved once per device with that
+// device current (at lh_context_create, or at the entry point's first call on
+// the device) and kept in g_noalloc_address.
+static __device__ __align__(256) uint8_t scratch[LH_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_lock;
+void* g_noalloc_address[kMaxDevices] = {};
+
+// The current device's copy of `scratch`.
+void* noalloc_scratch() {
+    int dev = 0;
+    leafhip::hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require_arg(dev >= 0 && dev < kMaxDevices, "device index out of range");
+    std::lock_guard<std::mutex> guard(g_noalloc_lock);
+    if (!g_noalloc_address[dev]) {
+        void* address = nullptr;
+        leafhip::hip_check(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)), "hipGetSymbolAddress");
+        g_noalloc_address[dev] = address;
+    }
+    return g_noalloc_address[dev];
+}
+
 leafhip::WeightView view_of(const lh_weight* w) {
     require_arg(w && w->data && w->rows && w->cols, "weight descriptor is empty");
     require_arg(w->bits == 32 || w->bits == 16 || w->bits == 8 || w->bits == 4, "weight bits must be 32, 16, 8 or 4");
@@ -136,7 +161,7 @@ leafhip::WeightView view_of(const lh_weight* w) {
 
 lh_status linear_impl(const lh_weight* weight, const float* x, const int8_t* q, const float* qs, size_t tokens,
                       uint32_t activation_bits, float* y, int32_t* acc, lh_stream stream, int force_path,
-                      unsigned required_bits) {
+                      unsigned required_bits, bool no_alloc = false) {
     return guarded([&] {
         leafhip::LinearCall c;
         c.w = view_of(weight);
@@ -160,9 +185,20 @@ lh_status linear_impl(const lh_weight* weight, const float* x, const int8_t* q, 
             // then room for 8 split-K partial sums of the output (prefill GEMM)
             const size_t q_bytes = q ? 0 : ((tokens * c.w.cols + 255) / 256) * 256;
             const size_t s_bytes = q ? 0 : ((tokens * 4 + 255) / 256) * 256;
-            const size_t split = tokens > 4 ? 8 * tokens * c.w.rows : 0;
-            auto* base = static_cast<uint8_t*>(
-                scratch_bytes(q_bytes + s_bytes + split * sizeof(int32_t) + 256, as_stream(stream)));
+            size_t split = tokens > 4 ? 8 * tokens * c.w.rows : 0;
+            uint8_t* base = nullptr;
+            if (no_alloc) {
+                // the fixed array: the quantized input must fit; split-K uses
+                // what is left (the GEMM splits less when it has less room,
+                // with identical integer sums)
+                require_arg(q_bytes + s_bytes <= LH_NOALLOC_SCRATCH_BYTES,
+                            "input too large for the allocation-free scratch (tokens * (cols + 4) bytes)");
+                base = static_cast<uint8_t*>(noalloc_scratch());
+                split = std::min(split, (LH_NOALLOC_SCRATCH_BYTES - q_bytes - s_bytes) / sizeof(int32_t));
+            } else {
+                base = static_cast<uint8_t*>(
+                    scratch_bytes(q_bytes + s_bytes + split * sizeof(int32_t) + 256, as_stream(stream)));
+            }
             if (!q) {
                 c.xq_scratch = reinterpret_cast<int8_t*>(base);
                 c.xs_scratch = reinterpret_cast<float*>(base + q_bytes);
@@ -198,6 +234,7 @@ lh_status lh_context_create(int device, lh_context** out) {
         leafhip::hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount");
         require_arg(device >= 0 && device < count, "no such GPU");
         leafhip::hip_check(hipSetDevice(device), "hipSetDevice");
+        (void)noalloc_scratch();   // lh_linear_noalloc's array on this device
         auto* c = new lh_context();
         c->impl.device = device;
         const hipError_t st = hipStreamCreateWithFlags(&c->impl.stream, hipStreamNonBlocking);
@@ -511,6 +548,10 @@ lh_status lh_quantize_rows_i8(const float* x, size_t rows, size_t cols, int8_t* 
 lh_status lh_linear(const lh_weight* weight, const float* x, size_t tokens, uint32_t activation_bits, float* y,
                     int32_t* acc, lh_stream stream) {
     return linear_impl(weight, x, nullptr, nullptr, tokens, activation_bits, y, acc, stream, 0, 0);
+}
+lh_status lh_linear_noalloc(const lh_weight* weight, const float* x, size_t tokens, uint32_t activation_bits, float* y,
+                            int32_t* acc, lh_stream stream) {
+    return linear_impl(weight, x, nullptr, nullptr, tokens, activation_bits, y, acc, stream, 0, 0, true);
 }
 lh_status lh_linear_q(const lh_weight* weight, const int8_t* q, const float* scales, size_t tokens, float* y,
                       int32_t* acc, lh_stream stream) {

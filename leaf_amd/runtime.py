@@ -111,6 +111,7 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_quantize_rows_i8": ([vp, sz, sz, vp, vp, vp], i32),
         "lh_linear": ([C.POINTER(Weight), vp, sz, u32, vp, vp, vp], i32),
         "lh_linear_q": ([C.POINTER(Weight), vp, vp, sz, vp, vp, vp], i32),
+        "lh_linear_noalloc": ([C.POINTER(Weight), vp, sz, u32, vp, vp, vp], i32),
         "lh_gemv_f32": ([C.POINTER(Weight), vp, sz, vp, vp], i32),
         "lh_gemv_bf16": ([C.POINTER(Weight), vp, sz, vp, vp], i32),
         "lh_gemv_w8a32": ([C.POINTER(Weight), vp, sz, vp, vp], i32),
