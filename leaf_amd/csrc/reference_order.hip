@@ -279,6 +279,71 @@ __global__ __launch_bounds__(kRoBlock) void ro_gemv_kernel(WeightView w, const f
     }
 }
 
+// Full groups of four tokens (every group but a ragged last one), TG groups
+// per 32-lane worker: lane 8 tt + l runs lane l of token tt's chain in each
+// group, so one load of a weight element serves all 4 TG tokens.  The order
+// per token is that of ro_gemv_kernel's multi-token case.
+template <int BITS, int TG>
+__global__ __launch_bounds__(kRoBlock) void ro_gemm_kernel(WeightView w, const float* __restrict__ x, int groups,
+                                                           float* y, int epilogue) {
+    const int lane = threadIdx.x & 31;
+    const int worker = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 5);
+    const int per_row = (groups + TG - 1) / TG;
+    const bool live = worker < w.rows * per_row;
+    const int row = live ? worker / per_row : 0;
+    const int g0 = live ? (worker % per_row) * TG : 0;
+    const int K = w.cols;
+    const int group = (BITS == 32 || BITS == 16) ? K : w.group;
+    const int sgroups = K / group;
+    const size_t base = (size_t)row * K;
+    const int tt = lane >> 3, l = lane & 7;
+    const float* xt[TG];
+#pragma unroll
+    for (int j = 0; j < TG; ++j) xt[j] = x + (size_t)(4 * min(g0 + j, groups - 1) + tt) * K;
+    float result[TG];
+#pragma unroll
+    for (int j = 0; j < TG; ++j) result[j] = 0.0f;
+    for (int g = 0; g < sgroups; ++g) {
+        int col = g * group;
+        const int end = col + group;
+        float acc[TG];
+#pragma unroll
+        for (int j = 0; j < TG; ++j) acc[j] = 0.0f;
+        for (; col + 8 <= end; col += 8) {
+            const float wv = lane_value<BITS>(w, base + col + l);
+#pragma unroll
+            for (int j = 0; j < TG; ++j) acc[j] = fmaf(wv, xt[j][col + l], acc[j]);
+        }
+        float scale = 1.0f;
+        if constexpr (BITS == 8 || BITS == 4) scale = w.scales[(size_t)row * sgroups + g];
+        float partial[TG];
+#pragma unroll
+        for (int j = 0; j < TG; ++j) partial[j] = reduce8(acc[j]);
+        for (; col < end; ++col) {
+            float value = lane_value<BITS>(w, base + col);
+            if constexpr (BITS == 8 || BITS == 4) value = (value * scale) / scale;
+            else if constexpr (BITS == 32) value = value / scale;
+#pragma unroll
+            for (int j = 0; j < TG; ++j) partial[j] = fmaf(value, xt[j][col], partial[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < TG; ++j) {
+            if constexpr (BITS == 16) result[j] = 0.0f + partial[j];
+            else result[j] = fmaf(partial[j], scale, result[j]);
+        }
+    }
+    if (live && l == 0) {
+        const float b = w.bias ? w.bias[row] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TG; ++j)
+            if (g0 + j < groups) {
+                const size_t index = (size_t)(4 * (g0 + j) + tt) * w.rows + row;
+                const float v = result[j] + b;
+                y[index] = epilogue == kAccumulate ? y[index] + v : v;
+            }
+    }
+}
+
 // Dynamic LDS beyond the default 64 KiB must be allowed per kernel first.
 template <typename K>
 void allow_lds(K kernel, size_t bytes, int& allowed) {
@@ -324,15 +389,35 @@ void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream
     ro_expf_kernel<<<grid ? grid : 1, kRoBlock, 0, stream>>>(x, count, y);
 }
 
+namespace {
+template <int BITS>
+void launch_ro_linear(const WeightView& w, const float* x, int tokens, float* y, int epilogue, hipStream_t stream) {
+    constexpr int TG = 16;
+    // Full groups of four while more than 4 TG tokens remain, then the rest
+    // (up to 4 TG tokens, the ragged group among them) one group per worker.
+    const int batched = tokens > 4 * TG ? tokens / 4 : 0;   // whole groups; a ragged one stays in the rest
+    if (batched) {
+        const size_t workers = (size_t)w.rows * ((batched + TG - 1) / TG);
+        const int grid = (int)((workers * 32 + kRoBlock - 1) / kRoBlock);
+        ro_gemm_kernel<BITS, TG><<<grid, kRoBlock, 0, stream>>>(w, x, batched, y, epilogue);
+    }
+    const int rest = tokens - 4 * batched;
+    if (rest > 0) {
+        const size_t workers = (size_t)w.rows * ((rest + 3) / 4);
+        const int grid = (int)((workers * 32 + kRoBlock - 1) / kRoBlock);
+        ro_gemv_kernel<BITS><<<grid, kRoBlock, 0, stream>>>(w, x + (size_t)4 * batched * w.cols, rest,
+                                                            y + (size_t)4 * batched * w.rows, epilogue);
+    }
+}
+}  // namespace
+
 bool launch_linear_fp_reference_order(const WeightView& w, const float* x, int tokens, float* y, int epilogue,
                                       hipStream_t stream) {
-    const size_t workers = (size_t)w.rows * ((tokens + 3) / 4);
-    const int grid = (int)((workers * 32 + kRoBlock - 1) / kRoBlock);
     switch (w.bits) {
-    case 32: ro_gemv_kernel<32><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
-    case 16: ro_gemv_kernel<16><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
-    case 8: ro_gemv_kernel<8><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
-    case 4: ro_gemv_kernel<4><<<grid, kRoBlock, 0, stream>>>(w, x, tokens, y, epilogue); return true;
+    case 32: launch_ro_linear<32>(w, x, tokens, y, epilogue, stream); return true;
+    case 16: launch_ro_linear<16>(w, x, tokens, y, epilogue, stream); return true;
+    case 8: launch_ro_linear<8>(w, x, tokens, y, epilogue, stream); return true;
+    case 4: launch_ro_linear<4>(w, x, tokens, y, epilogue, stream); return true;
     default: return false;
     }
 }

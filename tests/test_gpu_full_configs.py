@@ -4,9 +4,9 @@
   and 32 greedy tokens.  Every logit of the prefill and of each decode step
   within LOGIT_TOLERANCE, and the GPU's own greedy run identical to the
   oracle's.
-* TinyLlama-1.1B W8A8 (22 x 2048, 32/4 heads, SwiGLU 5632, FP32 head): a
-  512-token prompt, then 48 teacher-forced decode steps on the persistent
-  decode step, within a band the oracle measures on itself (see the test).
+* TinyLlama-1.1B W8A8 (22 x 2048, 32/4 heads, SwiGLU 5632, FP32 head): the
+  fused and unfused prefill quantization give identical logits.  Its parity
+  with the reference at 512 + 128 tokens is tests/test_gpu_configured_sizes.py.
 * Qwen2.5-0.5B INT4 group 32 (24 x 896, 14/2 heads, vocab 151936, tied) and
   SmolLM2-360M BF16 with accurate FP32 math (32 x 960, 15/5 heads): full
   geometry against the oracle with 128-token prompts (the oracle's scalar
@@ -22,7 +22,6 @@ import numpy as np
 import pytest
 
 from leaf_amd import models
-from leaf_amd.artifact import write_artifact
 
 pytestmark = pytest.mark.gpu
 
@@ -35,11 +34,6 @@ def rel_error(a, b):
 
 def rel_rmse(a, b):
     return float(np.sqrt(np.mean((a - b) ** 2)) / max(np.sqrt(np.mean(b ** 2)), 1e-12))
-
-
-def decisive(reference, band):
-    top = np.sort(reference)[-2:]
-    return top[1] - top[0] > 2 * band * np.max(np.abs(reference))
 
 
 @pytest.fixture(scope="module")
@@ -80,72 +74,6 @@ def test_gpt2_small_full_logits_and_greedy_run(rt, oracle, full_artifacts):
     assert tokens == expected
     assert tokens[:len(forced)] == forced[:len(tokens)]
     dec.close()
-
-
-def oracle_rows(oracle, path, prompt, tokens, norm_order):
-    """The oracle's last-row logits of the prefill and of one decode step per
-    token, with its RMSNorm square sum in the given order."""
-    oracle.set_norm_order(norm_order)
-    try:
-        od = oracle.decoder(path, 8, False)
-        rows = [od.forward(prompt)]
-        for tok in tokens:
-            rows.append(od.forward([tok]))
-        od.close()
-    finally:
-        oracle.set_norm_order(0)
-    return np.stack(rows)
-
-
-def test_tinyllama_w8a8_full_prefill_and_decode_steps(rt, oracle, full_artifacts):
-    """At 22 layers the int8 rounding flips of W8A8 compound: the oracle itself,
-    with nothing but its RMSNorm square sum taken pairwise instead of
-    sequentially, moves these logits by 6-9% of the largest |logit| (measured
-    at 512 keys).  That distance, measured here on the same inputs, is the
-    band: the GPU must stay within 1.5 times it, its greedy choice must match
-    wherever the oracle's top-2 margin is wider than twice it, and it must
-    agree with the oracle's greedy choice about as often as the pairwise-norm
-    oracle does (43 and 42 of 49 rows when this was written)."""
-    path = full_artifacts("tinyllama")
-    prompt = np.random.default_rng(2).integers(0, 32000, 512).astype(np.uint32)
-    steps = 48
-    od = oracle.decoder(path, 8, False)
-    ref = [od.forward(prompt)]
-    tokens = []
-    for _ in range(steps):
-        tokens.append(int(np.argmax(ref[-1])))
-        ref.append(od.forward([tokens[-1]]))
-    od.close()
-    ref = np.stack(ref)
-    alt = oracle_rows(oracle, path, prompt, tokens, 1)
-    band = max(rel_error(x, y) for x, y in zip(alt, ref))
-    band_rmse = max(rel_rmse(x, y) for x, y in zip(alt, ref))
-    dec = rt.Decoder(path, 8, "fast", max_context=700, max_prefill=512)
-    rows = [dec.forward(prompt)]
-    dec.set_profiling(True)
-    for tok in tokens:
-        rows.append(dec.forward([tok]))
-    launches = dec.profile().get("decode_step", {}).get("launches", 0)
-    dec.close()
-    worst = max(rel_error(x, y) for x, y in zip(rows, ref))
-    rmse = max(rel_rmse(x, y) for x, y in zip(rows, ref))
-    checked = 0
-    for i, (x, y) in enumerate(zip(rows, ref)):
-        if decisive(y, band):
-            assert int(np.argmax(x)) == int(np.argmax(y)), f"greedy token differs at row {i} with a decisive margin"
-            checked += 1
-    # how often the greedy choice survives inside the band: the oracle against
-    # itself, and the GPU against the oracle
-    same_alt = sum(int(np.argmax(x)) == int(np.argmax(y)) for x, y in zip(alt, ref))
-    same_gpu = sum(int(np.argmax(x)) == int(np.argmax(y)) for x, y in zip(rows, ref))
-    print(f"tinyllama full: oracle band {band:.2e} (RMSE {band_rmse:.2e}); GPU worst {worst:.2e} (RMSE {rmse:.2e}); "
-          f"greedy choice compared at {checked} of {steps + 1} rows; same argmax as the oracle in {same_gpu} rows "
-          f"(the oracle's pairwise-norm run: {same_alt}); {launches} persistent-step launches")
-    # a step whose blocks ran off their XCD runs again on the memory path
-    assert steps <= launches <= steps + 4
-    assert worst <= 1.5 * band
-    assert rmse <= 1.5 * band_rmse
-    assert same_gpu >= same_alt - 2, "the greedy choice departs from the oracle more often than a reorder does"
 
 
 @pytest.mark.parametrize("family,math", [("qwen", "fast"), ("smollm2", "accurate")])

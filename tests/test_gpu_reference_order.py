@@ -133,7 +133,7 @@ def test_fp_linears_bit_exact(rt, oracle, K, N):
         forms.append((8, *quantize(w, 8, 64), 64))
     for bits, data, scales, group in forms:
         dw = rt.DeviceWeight(data, bits, K, scales, group, bias)
-        for M in (1, 2, 3, 4, 5, 6, 9):
+        for M in (1, 2, 3, 4, 5, 6, 9, 65, 66, 67, 68, 133):
             x = rng.standard_normal((M, K), dtype=np.float32)
             dx, dy = rt.DeviceArray.of(x), rt.DeviceArray((M, N), np.float32)
             rt.linear(dw, dx, M, 32, dy)
