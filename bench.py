@@ -4,24 +4,37 @@ Workload (the configuration the metric is quoted on): 22 layers, d_model 2048,
 32 query / 4 KV heads of 64, SwiGLU 5632, RMSNorm eps 1e-5, RoPE theta 1e4,
 vocab 32000, untied FP32 LM head; random-init weights N(0, 0.02) quantized to
 INT8 per output row, RMSNorm weights 1; activations quantized per token
-(W8A8).  A 512-token random prompt is prefilled, then greedy decode runs;
-config.prefill_ms is that first (cold) prefill, config.prefill_warm_p50_ms the
-median of ten more on the warm session after the decode.
+(W8A8).  The artifact and the 512-token prompt are the seeded ones of the
+reference's greedy run in tests/golden/full_configs.json; the prompt is
+prefilled, then greedy decode runs.  config.prefill_ms is that first (cold)
+prefill, config.prefill_warm_p50_ms the median of ten more on the warm session.
 A "step" is one decode token (one forward of one token plus the device argmax
 that feeds the next step).  `value` is decode tokens per second with all
-weights and the KV cache resident in HBM.
+weights and the KV cache resident in HBM, on the fast kernels.
 
 Beside it:
+  parity        the fast kernels' greedy tokens and prefill logits against the
+                reference's (tests/golden/full_configs.npz): how many leading
+                tokens agree and the logit error; then the same run with
+                reference-order numerics (bit-exact): tokens, logits and tok/s;
   roofline      the dominant decode kernel (the persistent decode step; the W8A8
                 GEMVs when the multi-launch path runs), algorithmic bytes per
                 launch / its HIP-event time, from a second, instrumented pass
-                of the same decode steps;
+                of the same decode steps, against the datasheet and the
+                measured (hbm_copy) bandwidth;
+  peaks         measured streaming bandwidth (leaf_amd/bin/hbm_copy, 1 GiB) and
+                MFMA rates (leaf_amd/bin/mfma_peak) beside the datasheet;
   gemv          standalone W8A8 GEMV at the TinyLlama shapes (M = 1), rotating
                 >= 1 GiB of weight copies so the 256 MiB MALL cannot serve them;
   linear_w8a8   the same shapes at M = 4, 16, 128 and 512 tokens (the prefill
                 GEMM at 512): us per call, int8 TOPS against the 5.0 POPS peak;
+  configs       the other benchmark configurations at their configured sizes
+                (GPT-2 FP32 16 + 32, Qwen INT4 4096 + 256, SmolLM2 BF16-accurate
+                2048 + 256): prefill ms and TFLOP/s, decode tok/s, bytes per
+                token and GB/s against HBM peak, agreement with the reference;
   cpu_baseline  the reference CPU engine (oracle/_ref/leaf_decoder, built from the
-                reference sources) on this host, on a bounded sample.
+                reference sources) on this host, on bounded samples: all allowed
+                cores (at most 64) and one core, with the host's CPU model.
   traffic       HBM bytes per launch of the dominant kernel from two rocprofv3
                 counter passes (FETCH_SIZE, WRITE_SIZE), each scaled by what the
                 same counter reads for a copy of known size (leaf_amd/bin/hbm_copy);
@@ -48,45 +61,68 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, datasheet
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, datasheet
+F32_PEAK_TFLOPS = 157.3        # MI355X dense f32 MFMA, datasheet
 TRAFFIC_FILE = ROOT / "profiles" / "decode_step_tinyllama_w8a8_traffic.json"
 COPY_BYTES = 1 << 30           # hbm_copy 1024: reads and writes this many bytes per launch
+GOLDEN = ROOT / "tests" / "golden"
 PROMPT_TOKENS = 512
-SEED = 20261201
+SEED = 20261201                # microbenchmark inputs
 METRIC = "decode tok/s + GEMV HBM GB/s (% peak), TinyLlama-shape W8A8, batch 1"
+
+
+def golden() -> tuple[dict, dict]:
+    """The reference's greedy runs at the configured sizes (data only)."""
+    meta = json.loads((GOLDEN / "full_configs.json").read_text())
+    with np.load(GOLDEN / "full_configs.npz", allow_pickle=False) as data:
+        arrays = {k: data[k] for k in data.files}
+    return meta, arrays
+
+
+def config_prompt(meta: dict, vocab: int) -> np.ndarray:
+    return np.random.default_rng(meta["prompt_seed"]).integers(0, vocab, meta["prompt_tokens"]).astype(np.uint32)
 
 
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def artifact_path() -> Path:
-    base = Path(os.environ.get("LEAF_BENCH_DIR", Path(tempfile.gettempdir()) / "leaf_bench"))
-    base.mkdir(parents=True, exist_ok=True)
-    return base / f"tinyllama_w8a8_seed{SEED}.leaf"
-
-
-def ensure_artifact() -> Path:
+def ensure_artifact(family: str = "tinyllama") -> Path:
+    """The configuration's seeded artifact, as the reference's greedy run used it."""
     from leaf_amd import models
     from leaf_amd.artifact import write_artifact
-    path = artifact_path()
+    meta = golden()[0][family]
+    base = Path(os.environ.get("LEAF_BENCH_DIR", Path(tempfile.gettempdir()) / "leaf_bench"))
+    base.mkdir(parents=True, exist_ok=True)
+    path = base / f"{family}_seed{meta['artifact_seed']}.leaf"
     if not path.exists():
         t = time.perf_counter()
-        write_artifact(path, models.tinyllama_w8a8(), seed=SEED)
+        write_artifact(path, models.PRESETS[family](), seed=meta["artifact_seed"])
         log(f"wrote {path} ({path.stat().st_size / 1e9:.2f} GB) in {time.perf_counter() - t:.1f}s")
     return path
 
 
+def rel_error(a, b) -> float:
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def leading_agreement(tokens, reference) -> int:
+    return next((i for i, (a, b) in enumerate(zip(tokens, reference)) if a != b), min(len(tokens), len(reference)))
+
+
 def decode_benchmark(path: Path, steps: int, warmup: int, prefill_repeats: int = 10) -> dict:
     from leaf_amd import runtime
-    rng = np.random.default_rng(SEED + 1)
-    prompt = rng.integers(0, 32000, PROMPT_TOKENS).astype(np.uint32)
+    meta, arrays = golden()
+    prompt = config_prompt(meta["tinyllama"], 32000)
     context = PROMPT_TOKENS + 2 * (warmup + steps) + 8
     dec = runtime.Decoder(path, activation_bits=8, max_context=context, max_prefill=PROMPT_TOKENS)
     t = time.perf_counter()
-    token = dec.forward_into(prompt, None)
+    logits = dec.forward(prompt)
     prefill_ms = (time.perf_counter() - t) * 1e3
+    token = int(dec.last_argmax.value)
+    generated = [token]
     for _ in range(warmup):
         token = dec.forward_into([token], None)
+        generated.append(token)
     runtime.synchronize()
     start = time.perf_counter()
     tokens = []
@@ -95,6 +131,11 @@ def decode_benchmark(path: Path, steps: int, warmup: int, prefill_repeats: int =
         tokens.append(token)
     runtime.synchronize()
     elapsed = time.perf_counter() - start
+    generated += tokens
+    reference = arrays["tinyllama_tokens"].tolist()
+    fast = {"tokens_compared": min(len(generated), len(reference)),
+            "leading_tokens_identical": leading_agreement(generated, reference),
+            "prefill_logit_error": round(rel_error(logits, arrays["tinyllama_prefill_logits"]), 5)}
     # Same decode steps again with every launch bracketed by HIP events.
     dec.set_profiling(True)
     for _ in range(steps):
@@ -114,8 +155,33 @@ def decode_benchmark(path: Path, steps: int, warmup: int, prefill_repeats: int =
         warm.append((time.perf_counter() - t) * 1e3)
     dec.close()
     return {"elapsed_s": elapsed, "prefill_ms": prefill_ms, "profile": profile, "context_end": ctx_end,
-            "prefill_warm_ms": float(np.median(warm)) if warm else None,
-            "tokens": tokens[:8]}
+            "prefill_warm_ms": float(np.median(warm)) if warm else None, "fast": fast}
+
+
+def reference_numerics_run(path: Path) -> dict:
+    """The same greedy run with reference-order numerics: bit-exact logits, identical tokens."""
+    from leaf_amd import runtime
+    meta, arrays = golden()
+    m = meta["tinyllama"]
+    prompt = config_prompt(m, 32000)
+    dec = runtime.Decoder(path, activation_bits=8, max_context=len(prompt) + m["generate"] + 8,
+                          max_prefill=len(prompt), numerics="reference")
+    t = time.perf_counter()
+    first = dec.forward(prompt)
+    runtime.synchronize()
+    prefill_ms = (time.perf_counter() - t) * 1e3
+    tokens = [int(dec.last_argmax.value)]
+    start = time.perf_counter()
+    for _ in range(m["generate"] - 1):
+        tokens.append(dec.forward_into([tokens[-1]], None))
+    runtime.synchronize()
+    elapsed = time.perf_counter() - start
+    dec.close()
+    reference = arrays["tinyllama_tokens"].tolist()
+    bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)   # noqa: E731
+    return {"tokens_identical": f"{leading_agreement(tokens, reference)}/{len(reference)}",
+            "prefill_logits_bit_equal": bool(np.array_equal(bits(first), bits(arrays["tinyllama_prefill_logits"]))),
+            "decode_tok_s": round((len(tokens) - 1) / elapsed, 1), "prefill_ms": round(prefill_ms, 2)}
 
 
 def gemv_microbench(repeats: int = 20) -> dict:
@@ -203,37 +269,153 @@ def linear_microbench(tokens=(4, 16, 128, 512), repeats: int = 3) -> dict:
     return out
 
 
-def cpu_baseline(path: Path, budget_s: float = 30.0) -> dict | None:
-    """Reference CPU engine (built from the reference sources) on this host."""
+def config_benchmark(family: str, profile_steps: int = 32) -> dict:
+    """One benchmark configuration at its configured size, fast kernels: the
+    prefill (cold, then the median of three warm), the greedy decode of the
+    reference's run (per-step wall time), one more profiled pass of decode
+    steps and of the prefill for algorithmic bytes, operations and device time
+    per kernel class."""
+    from leaf_amd import runtime
+    meta_all, arrays = golden()
+    m = meta_all[family]
+    path = ensure_artifact(family)
+    dec = runtime.Decoder(path, m["activation_bits"], m["fp32_math"],
+                          max_context=m["prompt_tokens"] + m["generate"] + profile_steps + 8,
+                          max_prefill=m["prompt_tokens"])
+    vocab = dec.vocabulary_size
+    prompt = config_prompt(m, vocab)
+    t = time.perf_counter()
+    logits = dec.forward(prompt)
+    cold_ms = (time.perf_counter() - t) * 1e3
+    tokens = [int(dec.last_argmax.value)]
+    step_ms = []
+    for _ in range(m["generate"] - 1):
+        t = time.perf_counter()
+        tokens.append(dec.forward_into([tokens[-1]], None))
+        step_ms.append((time.perf_counter() - t) * 1e3)
+    dec.set_profiling(True)
+    token = tokens[-1]
+    for _ in range(profile_steps):
+        token = dec.forward_into([token], None)
+    decode_profile = dec.profile()
+    dec.set_profiling(False)
+    warm = []
+    for _ in range(3):
+        dec.reset()
+        runtime.synchronize()
+        t = time.perf_counter()
+        dec.forward_into(prompt, None)
+        runtime.synchronize()
+        warm.append((time.perf_counter() - t) * 1e3)
+    dec.reset()
+    dec.set_profiling(True)
+    dec.forward_into(prompt, None)
+    prefill_profile = dec.profile()
+    dec.close()
+    decode_ms = float(np.mean(step_ms))
+    bytes_per_token = sum(v["bytes"] for v in decode_profile.values()) / profile_steps
+    device_ms = sum(v["ms"] for v in decode_profile.values()) / profile_steps
+    top = max(decode_profile, key=lambda k: decode_profile[k]["ms"])
+    top_gbs = decode_profile[top]["bytes"] / max(decode_profile[top]["ms"], 1e-9) / 1e6
+    flops = sum(v["ops"] for v in prefill_profile.values())
+    prefill_ms = float(np.median(warm))
+    gemm = {k: v for k, v in prefill_profile.items() if k.startswith("gemm")}
+    gemm_ms = sum(v["ms"] for v in gemm.values())
+    gemm_tflops = sum(v["ops"] for v in gemm.values()) / max(gemm_ms, 1e-9) / 1e9
+    reference = arrays[f"{family}_tokens"].tolist()
+    return {
+        "workload": f"{family}: {m['prompt_tokens']}-token prompt + {m['generate']} greedy tokens, "
+                    f"activation bits {m['activation_bits']}, FP32 math {m['fp32_math']}",
+        "prefill_ms": round(cold_ms, 2), "prefill_warm_p50_ms": round(prefill_ms, 3),
+        "prefill_TFLOPs": round(flops / prefill_ms / 1e9, 2),
+        "prefill_gemm": {"ms": round(gemm_ms, 3), "TFLOPs": round(gemm_tflops, 2),
+                         "frac_f32_mfma": round(gemm_tflops / F32_PEAK_TFLOPS, 4)},
+        "decode_tok_s": round(1e3 / decode_ms, 1), "decode_p50_ms": round(float(np.median(step_ms)), 4),
+        "decode_mean_ms": round(decode_ms, 4), "bytes_per_token": round(bytes_per_token),
+        "decode_GBps": round(bytes_per_token / decode_ms / 1e6, 1),
+        "decode_frac_hbm": round(bytes_per_token / decode_ms / 1e6 / HBM_PEAK_GBS, 4),
+        "device_GBps": round(bytes_per_token / device_ms / 1e6, 1),
+        "dominant_kernel": {"class": top, "GBps": round(top_gbs, 1), "frac_hbm": round(top_gbs / HBM_PEAK_GBS, 4)},
+        "tokens_identical": f"{leading_agreement(tokens, reference)}/{len(reference)}",
+        "prefill_logit_error": float(f"{rel_error(logits, arrays[f'{family}_prefill_logits']):.3g}"),
+    }
+
+
+def measured_peaks() -> dict:
+    """Streaming bandwidth and MFMA rates measured on this device."""
+    out = {"datasheet": {"hbm_GBps": HBM_PEAK_GBS, "int8_mfma_TOPS": INT8_PEAK_TOPS, "bf16_mfma_TFLOPs": 2500.0,
+                         "f32_mfma_TFLOPs": F32_PEAK_TFLOPS}}
+    copy = ROOT / "leaf_amd" / "bin" / "hbm_copy"
+    mfma = ROOT / "leaf_amd" / "bin" / "mfma_peak"
+    if copy.exists():
+        run = subprocess.run([str(copy), "1024", "10"], capture_output=True, text=True, timeout=120)
+        if run.returncode == 0:
+            out["hbm_copy_GBps"] = float(run.stdout.split(",")[-1].split()[0])
+    if mfma.exists():
+        run = subprocess.run([str(mfma)], capture_output=True, text=True, timeout=120)
+        if run.returncode == 0:
+            for line in run.stdout.splitlines():
+                kind = line.split()[1]
+                rate = float(line.split("T/s")[0].split()[-1])
+                out[{"int8": "int8_mfma_TOPS", "bf16": "bf16_mfma_TFLOPs", "f32": "f32_mfma_TFLOPs"}[kind]] = rate
+    return out
+
+
+def host_cpu() -> dict:
+    allowed = len(os.sched_getaffinity(0))
+    model, flags = "unknown", []
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            if line.startswith("flags") and not flags:
+                have = set(line.split(":", 1)[1].split())
+                flags = [f for f in ("avx2", "fma", "avx_vnni", "avx512f", "avx512_vnni") if f in have]
+    except OSError:
+        pass
+    return {"allowed_cpus": allowed, "nproc": os.cpu_count(), "model": model, "flags": flags}
+
+
+def reference_cpu_run(path: Path, prompt: np.ndarray, generate: int, threads: int) -> dict | None:
+    """leaf_decoder bench-generate (main_decoder.cpp:278-298) of the reference build."""
     from leaf_amd.artifact import write_tokens
     ref = ROOT / "oracle" / "_ref" / "leaf_decoder"
-    cores = min(len(os.sched_getaffinity(0)), 16, 64)
-    rng = np.random.default_rng(SEED + 1)
-    prompt = rng.integers(0, 32000, PROMPT_TOKENS).astype(np.uint32)
-    generate = 9
+    if not ref.exists():
+        return None
     with tempfile.TemporaryDirectory() as tmp:
         req = Path(tmp) / "req.bin"
         write_tokens(req, [prompt.tolist()])
-        if ref.exists():
-            cmd = [str(ref), str(path), str(req), str(Path(tmp) / "l.bin"), str(Path(tmp) / "m.json"),
-                   "bench-generate", str(cores), "1", "0", str(generate), "0", "1", "8"]
-            t = time.perf_counter()
-            run = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
-            wall = time.perf_counter() - t
-            if run.returncode != 0:
-                log("reference CPU baseline failed:", run.stderr.strip())
-                return None
-            metrics = json.loads((Path(tmp) / "m.json").read_text())
-            decode = metrics["decode_samples_ms"]
-            return {"value": round(1e3 / float(np.mean(decode)), 3), "unit": "tok/s", "cores": cores,
-                    "kind": "reference",
-                    "sample": f"leaf_decoder bench-generate, {PROMPT_TOKENS}-token prompt + {generate - 1} decode "
-                              f"steps, {cores} threads; prefill {metrics['prefill_p50_ms']:.0f} ms, decode p50 "
-                              f"{metrics['decode_p50_ms']:.1f} ms/token; wall {wall:.1f}s"}
+        cmd = [str(ref), str(path), str(req), str(Path(tmp) / "l.bin"), str(Path(tmp) / "m.json"),
+               "bench-generate", str(threads), "1", "0", str(generate), "0", "1", "8"]
+        t = time.perf_counter()
+        run = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        wall = time.perf_counter() - t
+        if run.returncode != 0:
+            log("reference CPU baseline failed:", run.stderr.strip())
+            return None
+        metrics = json.loads((Path(tmp) / "m.json").read_text())
+    decode = metrics["decode_samples_ms"]
+    return {"value": round(1e3 / float(np.mean(decode)), 3), "unit": "tok/s", "cores": threads,
+            "sample": f"leaf_decoder bench-generate, {len(prompt)}-token prompt + {generate - 1} decode steps, "
+                      f"{threads} threads; prefill {metrics['prefill_p50_ms']:.0f} ms, decode p50 "
+                      f"{metrics['decode_p50_ms']:.1f} ms/token; wall {wall:.1f}s"}
+
+
+def cpu_baseline(path: Path, budget_s: float = 30.0) -> dict | None:
+    """Reference CPU engine (built from the reference sources) on this host:
+    all allowed cores (at most 64, the engine's pool limit, host_support.h:119)
+    on the 512-token prompt, and one core on its first 64 tokens."""
+    host = host_cpu()
+    prompt = config_prompt(golden()[0]["tinyllama"], 32000)
+    cores = min(host["allowed_cpus"], 64)
+    every = reference_cpu_run(path, prompt, 9, cores)
+    if every is not None:
+        one = reference_cpu_run(path, prompt[:64], 9, 1)
+        every.update({"kind": "reference", "one_core": one, "host": host})
+        return every
     # No reference build here: time the oracle (single-thread restatement).
     from oracle.bindings import oracle
     d = oracle().decoder(path, 8, False)
-    t = time.perf_counter()
     d.forward(prompt[:16])
     steps, token = 0, 0
     start = time.perf_counter()
@@ -241,7 +423,7 @@ def cpu_baseline(path: Path, budget_s: float = 30.0) -> dict | None:
         d.forward([token])
         steps += 1
     dt = (time.perf_counter() - start) / steps
-    return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+    return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port", "host": host,
             "sample": f"oracle decoder, 16-token prompt + {steps} decode steps"}
 
 
@@ -284,6 +466,9 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemv", action="store_true")
     parser.add_argument("--no-linear", action="store_true")
+    parser.add_argument("--no-configs", action="store_true")
+    parser.add_argument("--no-peaks", action="store_true")
+    parser.add_argument("--no-reference-numerics", action="store_true")
     parser.add_argument("--derive-traffic", type=Path, default=None)
     args = parser.parse_args()
     if args.derive_traffic is not None:
@@ -315,6 +500,20 @@ def main() -> int:
     traffic = None
     if TRAFFIC_FILE.exists() and "decode_step" in kernel:
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+    reference = None
+    if not args.no_reference_numerics:
+        log("reference-order numerics run ...")
+        reference = reference_numerics_run(path)
+    peaks = None
+    if not args.no_peaks:
+        log("measured peaks ...")
+        peaks = measured_peaks()
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        for family in ("gpt2", "qwen", "smollm2"):
+            log(f"configuration {family} ...")
+            configs[family] = config_benchmark(family)
     gemv = None
     if not args.no_gemv:
         log("GEMV microbenchmark ...")
@@ -342,7 +541,13 @@ def main() -> int:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(bytes_per_launch),
-                     "launches": g["launches"]},
+                     "launches": g["launches"],
+                     "measured_peak": peaks.get("hbm_copy_GBps") if peaks else None,
+                     "frac_of_measured": round(achieved / peaks["hbm_copy_GBps"], 4)
+                     if peaks and peaks.get("hbm_copy_GBps") else None},
+        "parity": {"fast": d["fast"], "reference_numerics": reference},
+        "peaks": peaks,
+        "configs": configs,
         "device_ms_per_step": device_ms,
         "gemv": gemv,
         "linear_w8a8": linear,

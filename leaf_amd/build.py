@@ -69,14 +69,17 @@ def build(verbose: bool = False) -> Path:
         if result.returncode != 0:
             raise RuntimeError(f"building leaf_decoder failed:\n{result.stderr}")
         exe_tmp.replace(EXECUTABLE)
-    if (CSRC / "hbm_copy.hip").exists():
-        # the copy of known size that calibrates the profiler's byte counters
-        probe = PACKAGE / "bin" / "hbm_copy"
+    # hbm_copy: the copy of known size that calibrates the profiler's byte
+    # counters and measures streaming bandwidth; mfma_peak: matrix-core rates
+    for tool in ("hbm_copy", "mfma_peak"):
+        if not (CSRC / f"{tool}.hip").exists():
+            continue
+        probe = PACKAGE / "bin" / tool
         probe.parent.mkdir(exist_ok=True)
-        cmd = [hipcc(), *HIPFLAGS, str(CSRC / "hbm_copy.hip"), "-o", str(probe.with_suffix(".tmp"))]
+        cmd = [hipcc(), *HIPFLAGS, str(CSRC / f"{tool}.hip"), "-o", str(probe.with_suffix(".tmp"))]
         result = subprocess.run(cmd, capture_output=True, text=True)
         if result.returncode != 0:
-            raise RuntimeError(f"building hbm_copy failed:\n{result.stderr}")
+            raise RuntimeError(f"building {tool} failed:\n{result.stderr}")
         probe.with_suffix(".tmp").replace(probe)
     if verbose:
         print(f"built {LIBRARY}")
