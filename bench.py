@@ -350,14 +350,19 @@ def measured_peaks() -> dict:
     if copy.exists():
         run = subprocess.run([str(copy), "1024", "10"], capture_output=True, text=True, timeout=120)
         if run.returncode == 0:
-            out["hbm_copy_GBps"] = float(run.stdout.split(",")[-1].split()[0])
+            for line in run.stdout.splitlines():
+                rate = float(line.split(",")[-1].split()[0])
+                out["hbm_copy_GBps" if line.startswith("hbm_copy") else "hbm_read_GBps"] = rate
     if mfma.exists():
         run = subprocess.run([str(mfma)], capture_output=True, text=True, timeout=120)
         if run.returncode == 0:
+            out["mfma_TOPS"] = {}
+            names = {"int8": "int8_mfma_TOPS", "bf16": "bf16_mfma_TFLOPs", "f32": "f32_mfma_TFLOPs"}
             for line in run.stdout.splitlines():
-                kind = line.split()[1]
+                kind, instruction = line.split()[1], line.split()[2]
                 rate = float(line.split("T/s")[0].split()[-1])
-                out[{"int8": "int8_mfma_TOPS", "bf16": "bf16_mfma_TFLOPs", "f32": "f32_mfma_TFLOPs"}[kind]] = rate
+                out["mfma_TOPS"][instruction] = rate
+                out[names[kind]] = max(out.get(names[kind], 0.0), rate)
     return out
 
 
@@ -542,9 +547,9 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": round(bytes_per_launch),
                      "launches": g["launches"],
-                     "measured_peak": peaks.get("hbm_copy_GBps") if peaks else None,
-                     "frac_of_measured": round(achieved / peaks["hbm_copy_GBps"], 4)
-                     if peaks and peaks.get("hbm_copy_GBps") else None},
+                     "measured_peak": peaks.get("hbm_read_GBps") if peaks else None,
+                     "frac_of_measured": round(achieved / peaks["hbm_read_GBps"], 4)
+                     if peaks and peaks.get("hbm_read_GBps") else None},
         "parity": {"fast": d["fast"], "reference_numerics": reference},
         "peaks": peaks,
         "configs": configs,

@@ -91,7 +91,10 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
 int decode_step_spans(int keys);
 // Blocks the step runs on (one per CU), or 0 when one block per CU cannot be resident.
 int decode_step_blocks(int device);
-// Launches one decode step (cooperative; `blocks` = CUs).  Returns the HIP status.
-hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream);
+// Launches one decode step (`blocks` = CUs), as a cooperative launch, which
+// guarantees every block is resident, or as a plain one of the same grid
+// (profilers that fail at process exit after cooperative launches).
+// Returns the HIP status.
+hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream, bool cooperative = true);
 
 }  // namespace leafhip

@@ -1573,12 +1573,17 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
            (ffn + blocks - 1) / blocks <= kGP * kB;
 }
 
-hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream) {
+hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream, bool cooperative) {
     StepParams p = params;
     void* args[] = {&p};
     const void* kernel = p.capture.x ? reinterpret_cast<const void*>(decode_step_kernel<true>)
                                      : reinterpret_cast<const void*>(decode_step_kernel<false>);
-    return hipLaunchCooperativeKernel(kernel, dim3(blocks), dim3(kT), args, 0, stream);
+    if (cooperative) return hipLaunchCooperativeKernel(kernel, dim3(blocks), dim3(kT), args, 0, stream);
+    // A plain launch of the same grid: one block per CU fits (decode_step_blocks
+    // checked the occupancy), so on an otherwise idle device every block is
+    // resident at once; if one were not, the others' bounded waits would
+    // abort the step with an error rather than hang.
+    return hipLaunchKernel(kernel, dim3(blocks), dim3(kT), args, 0, stream);
 }
 
 }  // namespace leafhip

@@ -6,8 +6,9 @@
 // bytes reads B and writes B, so rocprofv3's FETCH_SIZE / WRITE_SIZE of
 // hbm_copy_kernel give the factor that turns those counters into bytes for
 // any other kernel profiled the same way.  It also prints the copy rate
-// (read + write bytes per second), the streaming bandwidth this device
-// reaches.
+// (read + write bytes per second) and, from a second kernel, the rate of
+// reading the same buffer without writing: the streaming bandwidths this
+// device reaches.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -22,6 +23,16 @@ __global__ __launch_bounds__(256) void hbm_copy_kernel(const v4u* __restrict__ s
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
         __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// Streaming read: every 16-byte word once, folded into one word per thread
+// (written only if it matches an impossible value, so the loads stay live).
+__global__ __launch_bounds__(256) void hbm_read_kernel(const v4u* __restrict__ src, size_t n, v4u* sink) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    v4u acc = {0u, 0u, 0u, 0u};
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        acc ^= __builtin_nontemporal_load(src + i);
+    if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u) sink[0] = acc;
 }
 
 bool ok(hipError_t e, const char* what) {
@@ -61,6 +72,18 @@ int main(int argc, char** argv) {
     const double per = ms / repeats;
     std::printf("hbm_copy: %zu bytes per launch (read %zu + write %zu), %d launches, %.3f ms each, %.1f GB/s\n",
                 2 * bytes, bytes, bytes, repeats + 1, per, 2.0 * bytes / per / 1e6);
+    // the same buffer read without writes: the bound of read-dominated kernels
+    hbm_read_kernel<<<grid, block>>>(static_cast<const v4u*>(src), n, static_cast<v4u*>(dst));
+    if (!ok(hipGetLastError(), "launch") || !ok(hipDeviceSynchronize(), "sync")) return 1;
+    if (!ok(hipEventRecord(start, 0), "record")) return 1;
+    for (int r = 0; r < repeats; ++r)
+        hbm_read_kernel<<<grid, block>>>(static_cast<const v4u*>(src), n, static_cast<v4u*>(dst));
+    if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(stop, 0), "record") ||
+        !ok(hipEventSynchronize(stop), "sync"))
+        return 1;
+    if (!ok(hipEventElapsedTime(&ms, start, stop), "elapsed")) return 1;
+    std::printf("hbm_read: %zu bytes per launch, %d launches, %.3f ms each, %.1f GB/s\n", bytes, repeats + 1,
+                ms / repeats, double(bytes) / (ms / repeats) / 1e6);
     (void)hipFree(src);
     (void)hipFree(dst);
     return 0;

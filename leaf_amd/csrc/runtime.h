@@ -185,6 +185,7 @@ private:
     void decode_step(uint32_t id, float* host_logits, uint32_t* argmax);
     int step_blocks_ = 0;
     bool step_enabled_ = true;
+    bool step_cooperative_ = true;   // LEAF_DECODE_STEP_COOPERATIVE=0: plain launch
     bool step_token_valid_ = false;   // ids_[0] holds the previous step's argmax
     uint32_t step_token_ = 0;
     unsigned step_launch_ = 0;

@@ -118,6 +118,10 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t 
     fuse_quantize_ = !(fuse && std::string(fuse) == "0");
     const char* step = std::getenv("LEAF_DECODE_STEP");
     step_enabled_ = !(step && std::string(step) == "0") && !reference_;
+    // LEAF_DECODE_STEP_COOPERATIVE=0: launch the step as a plain grid (for
+    // profilers that fail at process exit after cooperative launches).
+    const char* coop = std::getenv("LEAF_DECODE_STEP_COOPERATIVE");
+    step_cooperative_ = !(coop && std::string(coop) == "0");
     // Graph-replayed decode sizes the reference-order attention for the whole cache.
     if (reference_ && int(std::min<uint32_t>(capacity, c.sliding_window ? c.sliding_window : capacity)) > reference_keys_)
         graphs_enabled_ = false;
@@ -527,7 +531,7 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
     *step_host_abort_ = 0;
     const double bytes = step_bytes_ + step_kv_bytes_ * double(length + 1);
     hipError_t launched = hipSuccess;
-    timed(Profiler::DecodeStep, bytes, 0, [&] { launched = launch_decode_step(p, step_blocks_, s); });
+    timed(Profiler::DecodeStep, bytes, 0, [&] { launched = launch_decode_step(p, step_blocks_, s, step_cooperative_); });
     hip_check(launched, "decode step launch");
     if (host_logits)
         hip_check(hipMemcpyAsync(host_logits, logits_.ptr, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s),
