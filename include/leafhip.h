@@ -80,6 +80,12 @@ lh_status lh_model_load_file(lh_context* context, const char* path, uint32_t act
  * for the duration of the call). */
 lh_status lh_model_load(lh_context* context, const void* artifact, size_t bytes, uint32_t activation_bits,
                         uint32_t fp32_math, lh_model** out);
+/* The artifact validation of lh_model_load alone, on the host (no device):
+ * LH_OK when the CPU reference's loader accepts the artifact (decoder.cpp:787-933)
+ * and its first use of each tensor would pass (decoder.cpp:975-1024), else
+ * the status and, in lh_last_error, the reference's message for the first
+ * problem.  No reference counterpart as a separate call. */
+lh_status lh_artifact_check(const void* artifact, size_t bytes, uint32_t activation_bits, uint32_t fp32_math);
 lh_status lh_model_get_info(const lh_model* model, lh_model_info* out);
 /* EOS token set (decoder.cpp:842-857; Decoder::is_eos_token, decoder.h:35). */
 lh_status lh_model_eos_tokens(const lh_model* model, uint32_t* out, size_t capacity, size_t* count);

@@ -67,6 +67,8 @@ class DecoderSpec:
     int8_group_size: int = 0        # 0 = one scale per row
     keep_fp32: frozenset = frozenset()
     source_bf16: bool = False       # v6: matrices stored as original BF16 bits
+    bf16_io: bool = False           # v5: embedding and head stored as BF16 bits, the rest FP32
+    smoothquant_alpha: float = 0.0  # > 0: SmoothQuant-calibrated linears with ".input_scale" tensors
     tied: bool = False              # lm_head shares the embedding payload
     attention_bias: bool = False    # q/k/v(/o) projection biases
     o_bias: bool = False
@@ -182,6 +184,10 @@ def _precision(spec: DecoderSpec, name: str, rows: int) -> int:
     # export_decoder.py:312-314
     if spec.source_bf16 and _bf16_matrix(name, rows, spec.layers) and name not in spec.keep_fp32:
         return 16
+    if spec.bf16_io and name in ("model.embed_tokens.weight", "lm_head.weight"):
+        return 16
+    if name.endswith(".input_scale"):
+        return 32
     if name.endswith(".weight") and rows > 1 and name not in spec.keep_fp32:
         return spec.bits
     return 32
@@ -194,6 +200,9 @@ def _version(spec: DecoderSpec) -> tuple[int, bytes]:
     version = 4 if len(eos_list) > 1 else 3 if spec.sliding_window else 2
     meta = struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list) if version == 4 else b""
     storage = 0
+    if spec.bf16_io:
+        version = storage = 5
+        meta = struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list)
     if spec.source_bf16:
         version = storage = 6
         meta = struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list)
@@ -203,6 +212,32 @@ def _version(spec: DecoderSpec) -> tuple[int, bytes]:
         meta = (ext + struct.pack(f"<{len(spec.rope_frequencies)}f", *spec.rope_frequencies)
                 + struct.pack(f"<{len(eos_list) + 1}I", len(eos_list), *eos_list))
     return version, meta
+
+
+def _calibrated(spec: DecoderSpec, name: str, rows: int) -> bool:
+    """The linears a SmoothQuant export calibrates: quantized matrices other
+    than the embeddings (export_decoder.py:285-296)."""
+    return bool(spec.smoothquant_alpha) and name.endswith(".weight") and rows > 1 and \
+        name not in spec.keep_fp32 and spec.bits in (8, 4) and \
+        not name.startswith(("model.embed_tokens.", "model.position_embeddings."))
+
+
+def channel_factors(weight: np.ndarray, activation_max: np.ndarray, alpha: float) -> np.ndarray:
+    """SmoothQuant per-input-channel factors s_j = max|X_j|^alpha / max|W_j|^(1-alpha)
+    (Xiao et al., 2022), bounded to [1e-4, 1e4]; the export multiplies W by s and
+    stores 1/s as the layer's ".input_scale" (export_decoder.py:108-118, 372-384)."""
+    weight_max = np.maximum(np.max(np.abs(weight), axis=0), 1e-5)
+    return np.clip(np.maximum(activation_max, 1e-5) ** alpha / weight_max ** (1 - alpha), 1e-4, 1e4).astype(np.float32)
+
+
+def synthetic_activation_max(seed: int, name: str, cols: int) -> np.ndarray:
+    """Seeded stand-in for calibration statistics: |N(0,1)| * 2 + 0.5 per input
+    channel, with 1% outlier channels x 20."""
+    key = sum((i + 1) * b for i, b in enumerate(name.encode())) % (1 << 31)
+    rng = np.random.default_rng([seed, key, 7])
+    maxima = np.abs(rng.standard_normal(cols)) * 2 + 0.5
+    maxima[rng.random(cols) < 0.01] *= 20
+    return maxima
 
 
 class _Init:
@@ -253,6 +288,14 @@ def write_artifact(path: str | Path, spec: DecoderSpec, seed: int = 0) -> dict:
     version, meta = _version(spec)
     shapes = tensor_shapes(spec)
     init = _Init(spec, seed)
+    # SmoothQuant: W * s is stored for each calibrated linear, 1/s as its input scale
+    smoothing = {}
+    for name, (rows, cols) in list(shapes.items()):
+        if _calibrated(spec, name, rows):
+            factors = channel_factors(init(name, rows, cols), synthetic_activation_max(seed, name, cols),
+                                      spec.smoothquant_alpha)
+            smoothing[name] = factors
+            shapes[name.removesuffix(".weight") + ".input_scale"] = (1, cols)
     descriptors, shared, offset = [], {}, 0
     for name, (rows, cols) in shapes.items():
         precision = _precision(spec, name, rows)
@@ -295,7 +338,14 @@ def write_artifact(path: str | Path, spec: DecoderSpec, seed: int = 0) -> dict:
                 continue
             row_bytes = cols * precision // 8
             groups = cols // group if group else 0
+            if name.endswith(".input_scale"):
+                inverse = (1.0 / smoothing[name.removesuffix(".input_scale") + ".weight"]).astype("<f4")
+                out.seek(base + start)
+                out.write(memoryview(np.ascontiguousarray(inverse)).cast("B"))
+                continue
             for first, array in init.blocks(source, rows, cols):
+                if source in smoothing:
+                    array = array * smoothing[source][None, :]
                 if precision == 32:
                     payload, scale_array = array, None
                 elif precision == 16:

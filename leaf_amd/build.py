@@ -22,7 +22,8 @@ LIBRARY = PACKAGE / "libleafhip.so"
 EXECUTABLE = PACKAGE / "bin" / "leaf_decoder"
 ARCH = os.environ.get("LEAF_HIP_ARCH", "gfx950")
 
-SOURCES = ["kernels.hip", "decode_step.hip", "reference_order.hip", "runtime.cpp", "session.cpp", "capi.cpp"]
+SOURCES = ["kernels.hip", "decode_step.hip", "reference_order.hip", "artifact_format.cpp", "runtime.cpp",
+           "session.cpp", "capi.cpp"]
 
 # -ffp-contract=off: every FMA in the kernels is explicit (fmaf), so the integer
 # epilogues keep the CPU path's separate roundings.  Packed FP32 instructions

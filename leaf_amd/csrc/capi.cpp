@@ -17,6 +17,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include "artifact_format.h"
 #include "runtime.h"
 
 struct lh_context { leafhip::Context impl; };
@@ -288,6 +289,13 @@ lh_status lh_model_load_file(lh_context* context, const char* path, uint32_t act
         }
         // Weights now live on the device; the host mapping is no longer needed.
         munmap(mapped, size);
+    });
+}
+
+lh_status lh_artifact_check(const void* artifact, size_t bytes, uint32_t activation_bits, uint32_t fp32_math) {
+    return guarded([&] {
+        require_arg(artifact != nullptr, "artifact bytes are required");
+        (void)leafhip::read_artifact(static_cast<const uint8_t*>(artifact), bytes, activation_bits, fp32_math);
     });
 }
 

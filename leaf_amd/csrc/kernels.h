@@ -37,7 +37,10 @@ enum Epilogue : int {
 void launch_embedding(const WeightView& table, const WeightView* positions, const uint32_t* ids, int tokens,
                       int position_base, float scale, float* hidden, hipStream_t stream,
                       const int* position_ptr = nullptr);
-void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream);
+// Rows are contiguous, or (rows_per_group > 0) in groups of rows_per_group
+// contiguous rows, group_stride floats from one group's start to the next.
+void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream,
+                 int rows_per_group = 0, size_t group_stride = 0);
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream);
 // norm_kernel + quantize_kernel in one launch (same q and scales, no f32 row in between)
 void launch_norm_quantize(const float* x, int rows, int width, const NormView& norm, int8_t* q, float* scales,
@@ -159,7 +162,7 @@ bool attention_decode_supported(int heads, int kv_heads, int dim);
 constexpr int kReferenceOrderMaxWidth = 16384;   // norm rows staged in LDS
 // norm() with sequential sums; false when width exceeds kReferenceOrderMaxWidth.
 bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
-                                 hipStream_t stream);
+                                 hipStream_t stream, int rows_per_group = 0, size_t group_stride = 0);
 // Most visible keys one query of the reference-order attention can score (LDS).
 int reference_order_attention_keys();
 // attention_impl order; `max_keys` bounds the visible keys of every query

@@ -90,10 +90,19 @@ __device__ __forceinline__ float apply_norm(float x, int c, const NormStats& st,
     return (x - st.mean) * st.scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
 }
 
-__global__ __launch_bounds__(kWideRow) void norm_kernel(const float* x, int width, NormView norm, float* y) {
+// Offset of row `row`: contiguous rows, or groups of rows_per_group rows
+// group_stride floats apart.
+__device__ __forceinline__ size_t row_offset(int row, int width, int rows_per_group, size_t group_stride) {
+    if (rows_per_group <= 0) return (size_t)row * width;
+    return (size_t)(row / rows_per_group) * group_stride + (size_t)(row % rows_per_group) * width;
+}
+
+__global__ __launch_bounds__(kWideRow) void norm_kernel(const float* x, int width, NormView norm, float* y,
+                                                        int rows_per_group, size_t group_stride) {
     __shared__ float scratch[16];
-    const float* in = x + (size_t)blockIdx.x * width;
-    float* out = y + (size_t)blockIdx.x * width;
+    const size_t at = row_offset(blockIdx.x, width, rows_per_group, group_stride);
+    const float* in = x + at;
+    float* out = y + at;
     const NormStats st = block_norm_stats(in, width, norm, scratch);
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = apply_norm(in[c], c, st, norm);
 }
@@ -1365,8 +1374,10 @@ __global__ void attention_merge_kernel(AttentionCall p, int splits) {
 // One query token.  A block owns one KV head and a span of keys: it stages the
 // K and V tiles of that span in LDS once (K rows padded by one float so lanes
 // walking keys hit distinct banks) and serves every query head of the group
-// from them (GQA by index, no repeat).  Scores keep the CPU's sequential dot
-// order.  Each block writes its (max, sum, out[dim]) per head; the last block
+// from them (GQA by index, no repeat).  Each score is two interleaved fused
+// chains over the head's dims, added at the end (the reference-order kernels
+// keep the CPU's single sequential chain).  Each block writes its
+// (max, sum, out[dim]) per head; the last block
 // of a KV head to finish (device-scope counter, reset by that block) merges
 // the spans of its heads, so no second launch is needed.
 constexpr int kTileFloats = 4096;                // K (or V) tile: keys * dim floats
@@ -1721,8 +1732,9 @@ void launch_embedding(const WeightView& table, const WeightView* positions, cons
                                                     position_base, scale, hidden, position_ptr);
 }
 
-void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream) {
-    norm_kernel<<<rows, kWideRow, 0, stream>>>(x, width, norm, y);
+void launch_norm(const float* x, int rows, int width, const NormView& norm, float* y, hipStream_t stream,
+                 int rows_per_group, size_t group_stride) {
+    norm_kernel<<<rows, kWideRow, 0, stream>>>(x, width, norm, y, rows_per_group, group_stride);
 }
 
 void launch_quantize(const float* x, int rows, int width, int8_t* q, float* scales, hipStream_t stream) {

@@ -47,12 +47,16 @@ constexpr int kRoBlock = 256;
 // One block per row.  The row is staged in LDS, every thread forms its
 // columns' squares (the same rounded products the CPU forms), and thread 0
 // adds them in column order.
-__global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int width, NormView norm, float* y) {
+__global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int width, NormView norm, float* y,
+                                                           int rows_per_group, size_t group_stride) {
     extern __shared__ float row[];        // [width] values, then [width] squares
     float* sq = row + width;
     __shared__ float stat[2];
-    const float* in = x + (size_t)blockIdx.x * width;
-    float* out = y + (size_t)blockIdx.x * width;
+    const size_t at = rows_per_group > 0 ? (size_t)(blockIdx.x / rows_per_group) * group_stride +
+                                               (size_t)(blockIdx.x % rows_per_group) * width
+                                         : (size_t)blockIdx.x * width;
+    const float* in = x + at;
+    float* out = y + at;
     for (int c = threadIdx.x; c < width; c += blockDim.x) row[c] = in[c];
     __syncthreads();
     float mean = 0.0f;
@@ -358,11 +362,11 @@ int g_norm_lds = 0, g_attention_lds = 0;
 
 // --------------------------------------------------------------- launchers ---
 bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, int rows_per_group, size_t group_stride) {
     if (width > kReferenceOrderMaxWidth) return false;
     const size_t lds = 2 * (size_t)width * sizeof(float);
     allow_lds(ro_norm_kernel, lds, g_norm_lds);
-    ro_norm_kernel<<<rows, kRoBlock, lds, stream>>>(x, width, norm, y);
+    ro_norm_kernel<<<rows, kRoBlock, lds, stream>>>(x, width, norm, y, rows_per_group, group_stride);
     return true;
 }
 

@@ -189,12 +189,13 @@ bool Session::prequantizes(const Linear& l, int tokens) const {
     return fuse_quantize_ && !reference_ && tokens > 1 && model.integer_linear(l) && !l.input_scale;
 }
 
-void Session::norm(const float* x, int rows, int width, const NormView& n, float* y) {
+void Session::norm(const float* x, int rows, int width, const NormView& n, float* y, int rows_per_group,
+                   size_t group_stride) {
     if (reference_) {
-        check(launch_norm_reference_order(x, rows, width, n, y, stream()), "reference-order norm rejected",
-              LH_ERROR_UNSUPPORTED);
+        check(launch_norm_reference_order(x, rows, width, n, y, stream(), rows_per_group, group_stride),
+              "reference-order norm rejected", LH_ERROR_UNSUPPORTED);
     } else {
-        launch_norm(x, rows, width, n, y, stream());
+        launch_norm(x, rows, width, n, y, stream(), rows_per_group, group_stride);
     }
 }
 
@@ -661,25 +662,24 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                 run_linear(L.qkv, normed, M, q, kStore, nullptr);
                 run_linear(L.k, normed, M, k, kStore, nullptr);
                 run_linear(L.v, normed, M, v, kStore, nullptr);
-                for (int t = 0; t < M; ++t) {
-                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width, q + size_t(t) * qw, qw * 4,
-                                             hipMemcpyDeviceToDevice, s), "qkv staging");
-                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width + qw, k + size_t(t) * kvw, kvw * 4,
-                                             hipMemcpyDeviceToDevice, s), "qkv staging");
-                    hip_check(hipMemcpyAsync(qkv + size_t(t) * qkv_width + qw + kvw, v + size_t(t) * kvw, kvw * 4,
-                                             hipMemcpyDeviceToDevice, s), "qkv staging");
-                }
+                // one strided copy per matrix into the [M, q|k|v] rows
+                const size_t pitch = size_t(qkv_width) * 4;
+                hip_check(hipMemcpy2DAsync(qkv, pitch, q, size_t(qw) * 4, size_t(qw) * 4, M,
+                                           hipMemcpyDeviceToDevice, s), "qkv staging");
+                hip_check(hipMemcpy2DAsync(qkv + qw, pitch, k, size_t(kvw) * 4, size_t(kvw) * 4, M,
+                                           hipMemcpyDeviceToDevice, s), "qkv staging");
+                hip_check(hipMemcpy2DAsync(qkv + qw + kvw, pitch, v, size_t(kvw) * 4, size_t(kvw) * 4, M,
+                                           hipMemcpyDeviceToDevice, s), "qkv staging");
             }
         }
         if (c.qk_norm) {
             // Q/K RMSNorm over each head's dim values (decoder.cpp:1327-1331).
             NormView qn{L.q_norm, nullptr, c.epsilon, 0, model.accurate ? 1 : 0};
             NormView kn{L.k_norm, nullptr, c.epsilon, 0, model.accurate ? 1 : 0};
-            for (int t = 0; t < M; ++t) {
-                float* row = qkv + size_t(t) * qkv_width;
-                norm(row, int(c.heads), dim, qn, row);
-                norm(row + qw, int(c.kv_heads), dim, kn, row + qw);
-            }
+            // every token's heads in one launch per tensor: rows of `dim`
+            // values, `heads` of them per token, tokens qkv_width apart
+            norm(qkv, M * int(c.heads), dim, qn, qkv, int(c.heads), size_t(qkv_width));
+            norm(qkv + qw, M * int(c.kv_heads), dim, kn, qkv + qw, int(c.kv_heads), size_t(qkv_width));
         }
         RopeKvCall rk;
         rk.qkv = qkv; rk.ld = qkv_width; rk.q_offset = 0; rk.k_offset = qw; rk.v_offset = qw + kvw;
@@ -766,12 +766,11 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                     float* g = proj_.as<float>();
                     run_linear(L.gate_up, normed, rows, act, kStore, nullptr);   // gate -> act (staging)
                     run_linear(L.up, normed, rows, g, kStore, nullptr);          // up -> proj (staging)
-                    for (int t = 0; t < rows; ++t) {
-                        hip_check(hipMemcpyAsync(gate_up + size_t(t) * 2 * f, act + size_t(t) * f, f * 4,
-                                                 hipMemcpyDeviceToDevice, s), "gate staging");
-                        hip_check(hipMemcpyAsync(gate_up + size_t(t) * 2 * f + f, g + size_t(t) * f, f * 4,
-                                                 hipMemcpyDeviceToDevice, s), "up staging");
-                    }
+                    const size_t pitch = size_t(2 * f) * 4, width = size_t(f) * 4;
+                    hip_check(hipMemcpy2DAsync(gate_up, pitch, act, width, width, rows, hipMemcpyDeviceToDevice, s),
+                              "gate staging");
+                    hip_check(hipMemcpy2DAsync(gate_up + f, pitch, g, width, width, rows, hipMemcpyDeviceToDevice, s),
+                              "up staging");
                 }
             }
             if (!fuse_act && !prequantizes(L.down, rows))

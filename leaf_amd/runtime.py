@@ -90,6 +90,7 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_model_load_file": ([vp, C.c_char_p, u32, u32, C.POINTER(vp)], i32),
         "lh_model_load": ([vp, vp, sz, u32, u32, C.POINTER(vp)], i32),
         "lh_model_get_info": ([vp, C.POINTER(ModelInfo)], i32),
+        "lh_artifact_check": ([vp, sz, u32, u32], i32),
         "lh_model_eos_tokens": ([vp, vp, sz, C.POINTER(sz)], i32),
         "lh_model_destroy": ([vp], i32),
         "lh_session_create": ([vp, C.POINTER(SessionOptions), C.POINTER(vp)], i32),
@@ -338,6 +339,14 @@ def linear_q(weight: DeviceWeight, q: DeviceArray, scales: DeviceArray, tokens: 
              acc: DeviceArray | None = None, stream=None) -> None:
     check(library().lh_linear_q(C.byref(weight.desc), q.ptr, scales.ptr, tokens, y.ptr,
                                 acc.ptr if acc is not None else None, stream))
+
+
+def artifact_check(artifact: bytes, activation_bits: int = 32, fp32_math: str = "fast") -> str | None:
+    """Validates LEAFDC bytes on the host: None when accepted, else the error text."""
+    lib = library()
+    buf = C.create_string_buffer(bytes(artifact), len(artifact))
+    status = lib.lh_artifact_check(buf, len(artifact), activation_bits, 1 if fp32_math == "accurate" else 0)
+    return None if status == LH_OK else lib.lh_last_error().decode()
 
 
 def set_kernel_numerics(numerics: str) -> None:

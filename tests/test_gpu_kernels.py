@@ -81,6 +81,24 @@ def test_w8a8_multi_token_bit_exact(rt, oracle, M):
     assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, b, x))
 
 
+@pytest.mark.parametrize("K,N", sorted(set(W8A8_LINEAR_SHAPES)))
+@pytest.mark.parametrize("M", [4, 16, 128, 512])
+def test_w8a8_config_grid_bit_exact(rt, oracle, K, N, M):
+    # The W8A8 microbenchmark configuration at every shape and token count:
+    # weights N(0, 0.02) quantized per output row, activations N(0, 1) with
+    # ~0.1% outliers x20 quantized per token; int32 accumulators and the
+    # dequantized outputs against quant_dot / quant_tile / quant_vnni_tile
+    # (decoder.cpp:536-702) as the oracle restates them.
+    rng = np.random.default_rng(20261201 + K * 13 + N * 7 + M)
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wq, ws = quantize(w, 8, K)
+    x = activations(rng, M, K)
+    y, acc = run_int_linear(rt, wq, ws, None, x, 8, K)
+    q, _ = oracle.quantize_rows(x)
+    assert np.array_equal(acc, oracle.int_accumulators(8, N, K, K, wq, q)), "int32 accumulators differ"
+    assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, None, x)), "dequantized outputs differ"
+
+
 def test_w8a8_prefill_gemm_512_tokens_bit_exact(rt, oracle):
     rng = np.random.default_rng(512)
     M, K, N = 512, 2048, 320
