@@ -215,7 +215,10 @@ private:
     bool fuse_quantize_ = true;   // LEAF_PREFILL_FUSE=0 turns the fused norm / activation quantization off
     bool reference_ = false;      // reference-order numerics (LH_NUMERICS_REFERENCE)
     int reference_keys_ = 0;      // most keys one query may see in reference order
-    void norm(const float* x, int rows, int width, const NormView& n, float* y);
+    // rows_per_group > 0: rows come in groups that many long, group_stride
+    // floats apart (Q/K norm over the heads of every token's q|k|v row)
+    void norm(const float* x, int rows, int width, const NormView& n, float* y, int rows_per_group = 0,
+              size_t group_stride = 0);
     void activation(const float* gate_up, int rows, int width, int gated, float* act);
     template <typename F> void timed(int kind, double bytes, double ops, F&& launch) {
         if (profiler.enabled) profiler.begin(stream());
