@@ -102,10 +102,19 @@ lh_status lh_model_destroy(lh_model* model);
  *    reference's bit for bit, hence identical greedy tokens, for decoders with
  *    SiLU or ReLU activations and fast FP32 math (GELU uses the device's
  *    erff / tanhf; accurate FP32 math is rejected).  Slower.
- *  DEFAULT: FAST, unless the environment variable LEAF_GPU_NUMERICS=reference. */
+ *    The CPU path sums the groups of a grouped INT8 linear over several
+ *    tokens in two ways, chosen by its host: fused multiply-adds
+ *    (quant_tile_avx, decoder.cpp:571-617) or, on AVX-VNNI hosts unless
+ *    LEAF_DISABLE_VNNI is set, a multiply and an add (quant_vnni_tile,
+ *    :661-702; selection at :780-782, 1022).  REFERENCE follows this host as
+ *    the CPU path would; REFERENCE_AVX2 / REFERENCE_VNNI pin either form.
+ *  DEFAULT: FAST, unless the environment variable LEAF_GPU_NUMERICS names a
+ *    mode: reference, reference-avx2 or reference-vnni. */
 #define LH_NUMERICS_DEFAULT 0
 #define LH_NUMERICS_FAST 1
 #define LH_NUMERICS_REFERENCE 2
+#define LH_NUMERICS_REFERENCE_AVX2 3
+#define LH_NUMERICS_REFERENCE_VNNI 4
 
 typedef struct lh_session_options {
     uint32_t max_context;  /* KV capacity in tokens; 0 = the artifact's max_positions */
@@ -178,10 +187,11 @@ lh_status lh_timer_stop(lh_timer* timer, lh_stream stream, double* milliseconds)
 
 /* ------------------------------------------------- kernel-level entry points
  * Numerics of this thread's later kernel-level calls (LH_NUMERICS_FAST or
- * LH_NUMERICS_REFERENCE, as for sessions): lh_rmsnorm, lh_layernorm,
- * lh_attention, lh_silu_gate, lh_activation and the FP paths of lh_linear,
- * lh_gemv_{f32,bf16,w8a32,w4a32} and lh_gemm_f32 follow it; the integer
- * paths are exact either way.  No reference counterpart. */
+ * one of the LH_NUMERICS_REFERENCE modes, as for sessions): lh_rmsnorm,
+ * lh_layernorm, lh_attention, lh_silu_gate, lh_activation and the FP paths
+ * of lh_linear, lh_gemv_{f32,bf16,w8a32,w4a32} and lh_gemm_f32 follow it;
+ * integer accumulators are exact in every mode, and grouped INT8 sums over
+ * several tokens take the mode's CPU form.  No reference counterpart. */
 lh_status lh_set_kernel_numerics(uint32_t numerics);
 /* y[i] = expf(x[i]) with the result glibc 2.35's expf returns on x86-64 with
  * FMA (the exp of the CPU path's softmax and SiLU, transformer.cpp:134,

@@ -115,6 +115,7 @@ unsigned* attention_counters(hipStream_t stream) {
 
 // Numerics of this thread's kernel-level calls (lh_set_kernel_numerics).
 thread_local bool t_reference_order = false;
+thread_local bool t_reference_vnni = false;   // grouped INT8 sums as quant_vnni_tile
 
 // Scratch of lh_linear_noalloc: a device array that exists from module load
 // to process end, one copy per GPU, so that entry point allocates nothing.
@@ -181,6 +182,7 @@ lh_status linear_impl(const lh_weight* weight, const float* x, const int8_t* q, 
         c.y = y;
         c.acc_out = acc;
         c.force_path = force_path;
+        c.unfused_group_sum = t_reference_vnni && c.integer_activations && c.w.bits == 8 && c.w.group <= 65536;
         if (c.integer_activations) {
             // quantized copy of x (when the kernel does not quantize in registers),
             // then room for 8 split-K partial sums of the output (prefill GEMM)
@@ -531,8 +533,10 @@ lh_status lh_timer_stop(lh_timer* timer, lh_stream stream, double* milliseconds)
 
 lh_status lh_set_kernel_numerics(uint32_t numerics) {
     return guarded([&] {
-        require_arg(numerics == LH_NUMERICS_FAST || numerics == LH_NUMERICS_REFERENCE, "unknown numerics mode");
-        t_reference_order = numerics == LH_NUMERICS_REFERENCE;
+        require_arg(numerics != LH_NUMERICS_DEFAULT, "unknown numerics mode");
+        const leafhip::NumericsMode mode = leafhip::resolve_numerics(numerics);
+        t_reference_order = mode.reference;
+        t_reference_vnni = mode.vnni;
     });
 }
 

@@ -94,6 +94,9 @@ struct LinearCall {
     int32_t* split_scratch = nullptr;   // split-K int32 sums for the W8A8 GEMM; may be null
     size_t split_capacity = 0;          // int32 elements available in split_scratch
     PairEpilogue pair;              // single-token paired epilogue (y unused when set)
+    // Integer path, tokens > 1: sum the groups as quant_vnni_tile does,
+    // res + ((float)acc * s_x) * s_w with two roundings, instead of fused.
+    bool unfused_group_sum = false;
 };
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
 // the call cannot run (missing scratch for the GEMM quantization).

@@ -687,12 +687,20 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
 }
 
 // ------------------------------------------------------ generic linear ---
+// res += ((float)acc * s_x) * s_w for one group: fused as quant_dot_avx and
+// quant_tile_avx compile it (target avx2,fma; decoder.cpp:568, 614), or two
+// roundings as in quant_vnni_tile (target avx2,avxvnni has no FMA; :699).
+__device__ __forceinline__ float group_term(int acc, float sx, float sw, float res, int unfused) {
+    const float term = (float)acc * sx;
+    return unfused ? __fadd_rn(res, __fmul_rn(term, sw)) : fmaf(term, sw, res);
+}
+
 // Any shape and storage: one thread per (token, row), sequential over columns.
-// Integer activations reproduce the CPU epilogue exactly, groups in order
-// with the fused accumulate of quant_dot_avx (decoder.cpp:568).
+// Integer activations reproduce the CPU epilogue exactly, groups in order.
 __global__ __launch_bounds__(kBlock) void linear_generic_kernel(WeightView w, const float* x, const int8_t* xq,
                                                                const float* xs, int tokens, int integer,
-                                                               float* y, int epilogue, int32_t* acc_out) {
+                                                               float* y, int epilogue, int32_t* acc_out,
+                                                               int unfused) {
     const size_t index = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (index >= (size_t)tokens * w.rows) return;
     const int t = (int)(index / w.rows), row = (int)(index % w.rows);
@@ -704,7 +712,7 @@ __global__ __launch_bounds__(kBlock) void linear_generic_kernel(WeightView w, co
             int acc = 0;
             for (int c = g * w.group; c < (g + 1) * w.group; ++c) acc += weight_int(w, row, c) * (int)xq[(size_t)t * K + c];
             if (acc_out) acc_out[((size_t)t * w.rows + row) * groups + g] = acc;
-            result = fmaf((float)acc * xs[t], w.scales[(size_t)row * groups + g], result);
+            result = group_term(acc, xs[t], w.scales[(size_t)row * groups + g], result, unfused);
         }
     } else {
         for (int c = 0; c < K; ++c) result = fmaf(weight_value(w, row, c), x[(size_t)t * K + c], result);
@@ -718,11 +726,11 @@ __global__ __launch_bounds__(kBlock) void linear_generic_kernel(WeightView w, co
 // with 16 consecutive K bytes at offset 16 * (l >> 4) of each 64-wide K step,
 // for both operands, so the exact integer sum does not depend on how the
 // hardware orders K inside the instruction.  Accumulators are exact; the
-// epilogue is the CPU path's per group: res = fma((float)acc * s_x, s_w, res).
+// epilogue is the CPU path's per group (group_term).
 __global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const int8_t* __restrict__ xq,
                                                           const float* __restrict__ xs, int tokens,
                                                           float* __restrict__ y, int epilogue,
-                                                          int32_t* __restrict__ acc_out) {
+                                                          int32_t* __restrict__ acc_out, int unfused) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = w.cols, N = w.rows;
     const int tile_m = blockIdx.y * 64 + (wave >> 1) * 32;   // tokens
@@ -772,8 +780,8 @@ __global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const i
                         const int t = tile_m + a * 16 + (lane >> 4) * 4 + i;
                         if (t < tokens && n < N) {
                             if (acc_out) acc_out[((size_t)t * N + n) * groups + g] = acc[a][b][i];
-                            res[a][b][i] = fmaf((float)acc[a][b][i] * xs[t], w.scales[(size_t)n * groups + g],
-                                                res[a][b][i]);
+                            res[a][b][i] = group_term(acc[a][b][i], xs[t], w.scales[(size_t)n * groups + g],
+                                                      res[a][b][i], unfused);
                         }
                     }
                     acc[a][b] = v4i{0, 0, 0, 0};
@@ -1862,11 +1870,12 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         }
         if (path == 3) {
             dim3 grid(ceil_div(w.rows, 64), ceil_div(c.tokens, 64));
-            gemm_int8_kernel<<<grid, kBlock, 0, stream>>>(w, xq, xs, c.tokens, c.y, c.epilogue, c.acc_out);
+            gemm_int8_kernel<<<grid, kBlock, 0, stream>>>(w, xq, xs, c.tokens, c.y, c.epilogue, c.acc_out,
+                                                          c.unfused_group_sum && c.tokens > 1);
             return 3;
         }
         linear_generic_kernel<<<ceil_div((size_t)c.tokens * w.rows, kBlock), kBlock, 0, stream>>>(
-            w, nullptr, xq, xs, c.tokens, 1, c.y, c.epilogue, c.acc_out);
+            w, nullptr, xq, xs, c.tokens, 1, c.y, c.epilogue, c.acc_out, c.unfused_group_sum && c.tokens > 1);
         return 2;
     }
     if (c.norm.kind >= 0) return -1;
@@ -1895,7 +1904,7 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         return 3;
     }
     linear_generic_kernel<<<ceil_div((size_t)c.tokens * w.rows, kBlock), kBlock, 0, stream>>>(
-        w, c.x, nullptr, nullptr, c.tokens, 0, c.y, c.epilogue, nullptr);
+        w, c.x, nullptr, nullptr, c.tokens, 0, c.y, c.epilogue, nullptr, 0);
     return 2;
 }
 

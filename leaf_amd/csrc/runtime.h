@@ -29,6 +29,17 @@ inline void check(bool ok, const std::string& message, lh_status code = LH_ERROR
 }
 void hip_check(hipError_t status, const char* what);
 
+// A numerics mode (LH_NUMERICS_*) resolved: whether the kernels follow the CPU
+// path's order, and whether grouped INT8 sums take quant_vnni_tile's form.
+// DEFAULT reads LEAF_GPU_NUMERICS; REFERENCE asks this host what the CPU path
+// would (AVX2, FMA and AVX-VNNI present, LEAF_DISABLE_VNNI unset or empty:
+// decoder.cpp:773, 780-782).  Throws on an unknown mode.
+struct NumericsMode {
+    bool reference = false;
+    bool vnni = false;
+};
+NumericsMode resolve_numerics(uint32_t numerics);
+
 struct DeviceBuffer {
     void* ptr = nullptr;
     size_t bytes = 0;
@@ -214,6 +225,7 @@ private:
     bool prequantizes(const Linear& l, int tokens) const;
     bool fuse_quantize_ = true;   // LEAF_PREFILL_FUSE=0 turns the fused norm / activation quantization off
     bool reference_ = false;      // reference-order numerics (LH_NUMERICS_REFERENCE)
+    bool reference_vnni_ = false; // grouped INT8 sums as quant_vnni_tile (two roundings)
     int reference_keys_ = 0;      // most keys one query may see in reference order
     // rows_per_group > 0: rows come in groups that many long, group_stride
     // floats apart (Q/K norm over the heads of every token's q|k|v row)

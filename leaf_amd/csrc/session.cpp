@@ -62,17 +62,41 @@ Profiler::~Profiler() {
     for (auto e : events_) (void)hipEventDestroy(e);
 }
 
+NumericsMode resolve_numerics(uint32_t numerics) {
+    if (numerics == LH_NUMERICS_DEFAULT) {
+        const char* env = std::getenv("LEAF_GPU_NUMERICS");
+        const std::string name = env ? env : "";
+        numerics = name == "reference" ? LH_NUMERICS_REFERENCE
+                 : name == "reference-avx2" ? LH_NUMERICS_REFERENCE_AVX2
+                 : name == "reference-vnni" ? LH_NUMERICS_REFERENCE_VNNI : LH_NUMERICS_FAST;
+    }
+    NumericsMode mode;
+    switch (numerics) {
+    case LH_NUMERICS_FAST: break;
+    case LH_NUMERICS_REFERENCE: {
+        mode.reference = true;
+        const char* disabled = std::getenv("LEAF_DISABLE_VNNI");
+#ifndef __HIP_DEVICE_COMPILE__   // x86 feature bits exist in the host pass only
+        __builtin_cpu_init();
+        mode.vnni = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") &&
+                    __builtin_cpu_supports("avxvnni") && !(disabled && disabled[0]);
+#endif
+        break;
+    }
+    case LH_NUMERICS_REFERENCE_AVX2: mode.reference = true; break;
+    case LH_NUMERICS_REFERENCE_VNNI: mode.reference = mode.vnni = true; break;
+    default: throw Error(LH_ERROR_INVALID_ARGUMENT, "Leaf decoder: unknown numerics mode");
+    }
+    return mode;
+}
+
 Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t numerics) : model(m) {
     const Config& c = m.config;
     capacity = max_context ? std::min(max_context, c.max_positions) : c.max_positions;
     check(capacity > 0, "session capacity must be positive", LH_ERROR_INVALID_ARGUMENT);
-    check(numerics <= LH_NUMERICS_REFERENCE, "unknown numerics mode", LH_ERROR_INVALID_ARGUMENT);
-    if (numerics == LH_NUMERICS_DEFAULT) {
-        const char* env = std::getenv("LEAF_GPU_NUMERICS");
-        reference_ = env && std::string(env) == "reference";
-    } else {
-        reference_ = numerics == LH_NUMERICS_REFERENCE;
-    }
+    const NumericsMode mode = resolve_numerics(numerics);
+    reference_ = mode.reference;
+    reference_vnni_ = mode.vnni && m.activation_bits == 8;
     if (reference_) {
         // The accurate FP32 policy sums its GEMMs in 256-column blocks
         // (accurate_fp32.h); the reference-order kernels follow dot_avx only.
@@ -218,6 +242,7 @@ void Session::run_linear(const Linear& l, const float* x, int tokens, float* y, 
     call.norm_scratch = normed_.as<float>();
     call.split_scratch = split_.as<int32_t>();
     call.split_capacity = split_.bytes / sizeof(int32_t);
+    call.unfused_group_sum = reference_vnni_ && l.view.bits == 8 && l.view.group <= 65536;
     if (l.input_scale) {
         // SmoothQuant input factors (decoder.cpp:1008-1019) before quantization.
         launch_scale_columns(x, tokens, l.view.cols, l.input_scale, scaled_.as<float>(), stream());

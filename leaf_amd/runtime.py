@@ -50,7 +50,7 @@ class SessionOptions(C.Structure):
 
 
 # Floating-point order of a session or of kernel-level calls (include/leafhip.h).
-NUMERICS = {"default": 0, "fast": 1, "reference": 2}
+NUMERICS = {"default": 0, "fast": 1, "reference": 2, "reference-avx2": 3, "reference-vnni": 4}
 
 
 class Weight(C.Structure):
@@ -350,7 +350,7 @@ def artifact_check(artifact: bytes, activation_bits: int = 32, fp32_math: str = 
 
 
 def set_kernel_numerics(numerics: str) -> None:
-    """Numerics of this thread's kernel-level calls: "fast" or "reference"."""
+    """Numerics of this thread's kernel-level calls: "fast", "reference", "reference-avx2" or "reference-vnni"."""
     check(library().lh_set_kernel_numerics(NUMERICS[numerics]))
 
 

@@ -68,3 +68,31 @@ def full_artifacts(tmp_path_factory):
             cache[family] = path
         return cache[family]
     return get
+
+
+@pytest.fixture(scope="session")
+def golden_features():
+    import json
+    import numpy as np
+    with np.load(ROOT / "tests" / "golden" / "features.npz", allow_pickle=False) as data:
+        arrays = {k: data[k] for k in data.files}
+    meta = json.loads((ROOT / "tests" / "golden" / "features.json").read_text())
+    return arrays, meta
+
+
+@pytest.fixture(scope="session")
+def feature_artifacts(tmp_path_factory, golden_features):
+    """Reduced artifacts of the operator and storage features, written on first use."""
+    from leaf_amd.artifact import write_artifact
+    from tests.golden.make_golden import feature_spec
+    root = tmp_path_factory.mktemp("features")
+    _, meta = golden_features
+    cache = {}
+
+    def get(name):
+        if name not in cache:
+            path = root / f"{name}.leaf"
+            write_artifact(path, feature_spec(name, meta[name]["eos_tokens"]), seed=meta[name]["seed"])
+            cache[name] = path
+        return cache[name]
+    return get

@@ -7,6 +7,7 @@ outputs.  Regenerate with
 
     make -C oracle && python tests/golden/make_golden.py          # kernels, reduced decoders
     make -C oracle && python tests/golden/make_golden.py --full   # configured sizes (minutes)
+    make -C oracle && python tests/golden/make_golden.py --features   # artifact and operator features
 """
 from __future__ import annotations
 
@@ -151,6 +152,106 @@ def decoder_vectors(tmp: Path) -> tuple[dict, dict]:
     return arrays, meta
 
 
+# Operator and storage features beyond the four families, each on a reduced
+# model: name -> (preset, overrides, activation bits, FP32 math, prompt tokens,
+# chunk, generated tokens).  The reference binary runs the prompt in chunks
+# with all logits kept (verify/chunked mode), then the real Decoder's greedy
+# loop; the fixture keeps five logit rows and the tokens.
+STATIC_FREQUENCIES = tuple(float(np.float32(0.9 / (1 + 3 * i))) for i in range(16))   # in (0, 1]
+FEATURE_CASES = {
+    # SmoothQuant: calibrated .input_scale factors scale the columns before quantization
+    "smoothquant": ("tinyllama", dict(norm_jitter=0.1, smoothquant_alpha=0.5), 8, "fast", 40, 13, 10),
+    # INT8 with 64-column scale groups (int8_group_size)
+    "int8_group64": ("tinyllama", dict(norm_jitter=0.1, int8_group_size=64), 8, "fast", 40, 13, 10),
+    # LEAFDC05: BF16 embedding and head, FP32 elsewhere
+    "bf16_io": ("tinyllama", dict(norm_jitter=0.1, bits=32, bf16_io=True, keep_fp32=frozenset()), 32, "fast",
+                40, 13, 10),
+    # LEAFDC07: per-head Q/K RMSNorm and static RoPE frequencies
+    "qk_norm_static_rope": ("tinyllama", dict(norm_jitter=0.1, bits=32, keep_fp32=frozenset(), qk_norm=1,
+                                              rope_frequencies=STATIC_FREQUENCIES), 32, "fast", 40, 13, 10),
+    # LEAFDC04: several EOS ids, the generation stops on a non-primary one
+    # (ids chosen by make_golden from a greedy run, stored in the metadata)
+    "multi_eos": ("tinyllama", dict(norm_jitter=0.1), 8, "fast", 40, 13, 16),
+    # exact-erf GELU (activation 1), ungated, LayerNorm with biases
+    "gelu_erf": ("gpt2", dict(bias_std=0.05, norm_jitter=0.1, activation=1), 32, "fast", 40, 13, 10),
+    # ReLU, ungated MLP
+    "relu": ("tinyllama", dict(norm_jitter=0.1, bits=32, keep_fp32=frozenset(), activation=3, gated=0), 32,
+             "fast", 40, 13, 10),
+    # parallel residual, rotary on half of each head, LayerNorm with biases, QKV biases
+    "parallel_partial_rotary": ("tinyllama", dict(norm_jitter=0.1, bits=32, keep_fp32=frozenset(),
+                                                  parallel_residual=1, rotary_dim=16, norm=1, norm_bias=True,
+                                                  attention_bias=True, bias_std=0.05), 32, "fast", 40, 13, 10),
+    # learned positions read at an offset, scaled embeddings, ReLU
+    "learned_offset_scaled": ("gpt2", dict(bias_std=0.05, norm_jitter=0.1, position_offset=2,
+                                           embedding_scale=4.0, activation=3), 32, "fast", 40, 13, 10),
+    # no position encoding and no final norm, W8A8
+    "no_position_no_final_norm": ("tinyllama", dict(norm_jitter=0.1, position=2, final_norm=0), 8, "fast",
+                                  40, 13, 10),
+    # LEAFDC03 sliding window of 8 keys, W8A8
+    "window8": ("tinyllama", dict(norm_jitter=0.1, sliding_window=8), 8, "fast", 40, 13, 10),
+    # 8,300-token context (split-K decode attention beyond 8k keys), INT4 weights
+    "long_context": ("qwen", dict(bias_std=0.05, max_positions=8320), 32, "fast", 8300, 1024, 8),
+}
+
+
+def feature_spec(name: str, eos_tokens=None):
+    family, overrides, *_ = FEATURE_CASES[name]
+    spec = dataclasses.replace(models.PRESETS[family](reduced=True), **overrides)
+    if eos_tokens:
+        spec = dataclasses.replace(spec, eos=int(eos_tokens[0]), eos_tokens=tuple(int(t) for t in eos_tokens))
+    return spec
+
+
+def feature_rows(prompt_tokens: int, chunk: int) -> list[int]:
+    rows = {0, chunk - 1, min(chunk, prompt_tokens - 1), prompt_tokens - 2, prompt_tokens - 1}
+    if prompt_tokens > 4352:
+        rows |= {4351, 4352, 8191, 8192} & set(range(prompt_tokens))
+    return sorted(rows)
+
+
+def feature_vectors(tmp: Path, ref: Reference, names) -> tuple[dict, dict]:
+    arrays, meta = {}, {}
+    for name in names:
+        family, overrides, bits, math, length, chunk, limit = FEATURE_CASES[name]
+        eos = None
+        if name == "multi_eos":
+            # greedy tokens without EOS, then a stop id that first appears at
+            # position >= 3 as the second of three EOS ids
+            art = tmp / "probe.leaf"
+            write_artifact(art, feature_spec(name), seed=101)
+            prompt = np.random.default_rng(7).integers(0, feature_spec(name).vocab, length).astype(np.uint32)
+            free, _ = ref.greedy(art, prompt, limit, activation_bits=bits, vocab=feature_spec(name).vocab)
+            free = free.tolist()
+            stop_at = next(i for i in range(3, len(free)) if free[i] not in free[:i])
+            unused = [t for t in range(1, 1000) if t not in free][:2]
+            eos = [unused[0], free[stop_at], unused[1]]
+        spec = feature_spec(name, eos)
+        art = tmp / f"{name}.leaf"
+        write_artifact(art, spec, seed=101)
+        prompt = np.random.default_rng(7).integers(0, spec.vocab, length).astype(np.uint32)
+        req, logits = tmp / "req.bin", tmp / "out.logits"
+        write_tokens(req, [prompt.tolist()])
+        cmd = [str(REF_BIN), str(art), str(req), str(logits), str(tmp / "m.json"), "chunked", "8", "1", "0", "16",
+               "0", str(chunk), str(bits), f"--fp32-math={math}"]
+        subprocess.run(cmd, check=True, capture_output=True)
+        rows = feature_rows(length, chunk)
+        all_logits = np.memmap(logits, np.float32, mode="r").reshape(-1, spec.vocab)
+        arrays[f"{name}_logits_rows"] = np.array(all_logits[rows])
+        del all_logits
+        tokens, _ = ref.greedy(art, prompt, limit, activation_bits=bits, accurate=math == "accurate",
+                               vocab=spec.vocab)
+        if name == "multi_eos":
+            assert len(tokens) == stop_at + 1 and int(tokens[-1]) == eos[1], (tokens, eos)
+        arrays[f"{name}_prompt"] = prompt
+        arrays[f"{name}_tokens"] = np.asarray(tokens, np.uint32)
+        meta[name] = {"artifact_sha256": artifact_digest(art), "activation_bits": bits, "fp32_math": math,
+                      "seed": 101, "prompt_seed": 7, "rows": rows, "chunk": chunk, "generate": limit,
+                      "eos_tokens": eos, "version": int(art.read_bytes()[7]) - ord("0")}
+        print(f"{name}: LEAFDC0{meta[name]['version']}, {len(tokens)} tokens", flush=True)
+        art.unlink()
+    return arrays, meta
+
+
 # The benchmark configurations at their configured sizes: (prompt tokens,
 # greedy tokens, prompt seed).  Artifacts: models.PRESETS[family]() written
 # with FULL_ARTIFACT_SEED.  The real reference Decoder runs the greedy loop;
@@ -204,6 +305,14 @@ def main() -> None:
         meta["reference_cpu_features"] = ref.features
         (OUT / "full_configs.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
         print("full_configs.npz", (OUT / "full_configs.npz").stat().st_size, "bytes")
+        return
+    if "--features" in sys.argv:
+        with tempfile.TemporaryDirectory() as tmp:
+            arrays, meta = feature_vectors(Path(tmp), ref, FEATURE_CASES)
+        np.savez_compressed(OUT / "features.npz", **arrays)
+        meta["reference_cpu_features"] = ref.features
+        (OUT / "features.json").write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
+        print("features.npz", (OUT / "features.npz").stat().st_size, "bytes")
         return
     kernels = kernel_vectors(ref)
     np.savez_compressed(OUT / "kernels.npz", **kernels)

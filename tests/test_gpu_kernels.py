@@ -152,6 +152,32 @@ def test_golden_w8a8_vectors_on_gpu(rt, golden_kernels):
             assert bits_equal(y, g[f"w8a8_{tag}_m{M}_y"]), (tag, M)
 
 
+def test_grouped_int8_sums_follow_the_cpu_form(rt, oracle, golden_kernels):
+    # Over several tokens the CPU sums INT8 scale groups with fused
+    # multiply-adds (quant_tile_avx) or, on AVX-VNNI hosts, with a multiply and
+    # an add (quant_vnni_tile); the kernel-level numerics pin either form.
+    g = golden_kernels
+    try:
+        for mode, policy, key in (("reference-vnni", 1, "yvnni"), ("reference-avx2", 0, "y")):
+            rt.set_kernel_numerics(mode)
+            w, s = g["w8a8_g64_w"], g["w8a8_g64_s"]
+            for M in (2, 5):
+                y, _ = run_int_linear(rt, w, s, None, g[f"w8a8_g64_m{M}_x"], 8, 64, acc=False)
+                assert bits_equal(y, g[f"w8a8_g64_m{M}_{key}"]), (mode, M)
+            # tokens 2..4 run the generic kernel, 67 the grouped MFMA GEMM
+            rng = np.random.default_rng(64)
+            for M, K, N in ((3, 256, 9), (67, 512, 70)):
+                wq, ws = quantize(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02), 8, 64)
+                b = rng.standard_normal(N, dtype=np.float32)
+                x = activations(rng, M, K)
+                y, _ = run_int_linear(rt, wq, ws, b, x, 8, 64, acc=False)
+                oracle.set_vnni_policy(policy)
+                assert bits_equal(y, oracle.linear_int(8, N, K, 64, wq, ws, b, x)), (mode, M)
+    finally:
+        rt.set_kernel_numerics("fast")
+        oracle.set_vnni_policy(0)
+
+
 def fp_case(bits, w, K):
     if bits == 32:
         return w, None, 0

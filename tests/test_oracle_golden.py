@@ -186,6 +186,44 @@ def test_decoder_matches_reference_binary(oracle, golden_decoders, artifacts, fa
     assert d.generate(prompt, 10) == arrays[f"{family}_tokens"].tolist()
 
 
+FEATURES = ["smoothquant", "int8_group64", "bf16_io", "qk_norm_static_rope", "multi_eos", "gelu_erf", "relu",
+            "parallel_partial_rotary", "learned_offset_scaled", "no_position_no_final_norm", "window8",
+            "long_context"]
+
+
+@pytest.mark.parametrize("name", FEATURES)
+def test_decoder_features_match_reference_binary(oracle, golden_features, feature_artifacts, name):
+    # the reference ran on a host with AVX-VNNI (reference_cpu_features bit 1):
+    # grouped INT8 sums over several tokens are unfused there (quant_vnni_tile)
+    arrays, meta = golden_features
+    m = meta[name]
+    path = feature_artifacts(name)
+    assert hashlib.sha256(path.read_bytes()).hexdigest() == m["artifact_sha256"], "artifact writer drifted"
+    prompt = arrays[f"{name}_prompt"]
+    oracle.set_vnni_policy(1 if meta["reference_cpu_features"] & 2 else 0)
+    try:
+        d = oracle.decoder(path, m["activation_bits"], m["fp32_math"] == "accurate")
+        rows = []
+        for pos in range(0, len(prompt), m["chunk"]):
+            out = d.forward(prompt[pos:pos + m["chunk"]], all_logits=True)
+            rows += [out[r - pos] for r in m["rows"] if pos <= r < pos + len(out)]
+        assert bits_equal(np.stack(rows), arrays[f"{name}_logits_rows"])
+        d.reset()
+        assert d.generate(prompt, m["generate"]) == arrays[f"{name}_tokens"].tolist()
+        d.close()
+    finally:
+        oracle.set_vnni_policy(0)
+
+
+def test_multi_eos_fixture_stops_on_a_secondary_id(golden_features):
+    arrays, meta = golden_features
+    m = meta["multi_eos"]
+    tokens = arrays["multi_eos_tokens"].tolist()
+    # stopped before the limit, on the second of three EOS ids, none earlier
+    assert len(tokens) < m["generate"] and tokens[-1] == m["eos_tokens"][1]
+    assert not set(tokens[:-1]) & set(m["eos_tokens"])
+
+
 def test_w8a8_logits_move_with_norm_summation_order(oracle, tmp_path):
     """The tolerance band of W8A8 decoder comparisons, measured on the oracle alone.
 
