@@ -98,6 +98,17 @@ struct LinearCall {
     // res + ((float)acc * s_x) * s_w with two roundings, instead of fused.
     bool unfused_group_sum = false;
 };
+// W8A8 prefill GEMM on int8 MFMA (gemm_w8a8.hip) for per-row weight scales:
+// y[t, n] = ((float)sum_k xq[t, k] W[n, k] * xs[t]) * w_scales[n] + bias[n]
+// (kStore) or y += that (kAccumulate).  K % 128 == 0.  Blocks own tile_m (64
+// or 128) tokens x 128 rows; with splits > 1 the K range is split and the
+// exact int32 sums go to partial[split][t][n] instead of y (acc_out and the
+// epilogue are then the split epilogue's).
+bool gemm_w8a8_mfma_supported(int K);
+void launch_gemm_w8a8_mfma(const int8_t* W, const float* w_scales, const float* bias, const int8_t* xq,
+                           const float* xs, int M, int N, int K, float* y, int epilogue, int32_t* acc_out,
+                           int tile_m, int splits, int32_t* partial, hipStream_t stream);
+
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
 // the call cannot run (missing scratch for the GEMM quantization).
 int launch_linear(const LinearCall& call, hipStream_t stream);

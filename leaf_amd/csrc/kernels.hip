@@ -801,116 +801,10 @@ __global__ __launch_bounds__(kBlock) void gemm_int8_kernel(WeightView w, const i
         }
 }
 
-// ----------------------------- W8A8 prefill, per-row scales: tiled MFMA ---
-// Y[t, n] = ((float)sum_k Xq[t, k] W[n, k] * s_x[t]) * s_w[n] + b[n] for
-// per-row weight scales (group = K, the export default) and K % 128 == 0.
-// A block owns 128 tokens x 128 weight rows; its four waves own 64 x 64 each
-// as 4 x 4 tiles of v_mfma_i32_16x16x64_i8 (operand layout as in
-// gemm_int8_kernel: lane l feeds row l % 16 with K bytes 16 (l / 16) .. +15 of
-// each 64-byte step).  K advances 128 bytes per stage: both 128 x 128 operand
-// tiles go to LDS (rows padded to 160 bytes: the hardware counter reads no
-// bank conflicts there, against one per LDS cycle at 144), double-buffered,
-// and the next stage waits in registers while this one feeds the MFMAs.  Two
-// blocks share a CU (80 KB of LDS each), so one block's loads overlap the
-// other's MFMAs.  The integer sums are exact and the epilogue is the CPU
-// path's, so results are bit-identical to it.
-constexpr int kGemmTile = 128;                 // tokens and rows per block
-constexpr int kGemmStage = 128;                // K bytes per stage
-constexpr int kGemmRow = kGemmStage + 32;      // padded LDS row (measured free of bank conflicts)
-constexpr int kGemmLoads = kGemmTile * kGemmStage / 16 / kBlock;   // 16-byte loads per thread per operand
-
-__device__ __forceinline__ void gemm_stage_load(const int8_t* xq, const int8_t* W, int K, int tokens, int N, int m0,
-                                                int n0, int k0, v4i (&ra)[kGemmLoads], v4i (&rb)[kGemmLoads]) {
-#pragma unroll
-    for (int j = 0; j < kGemmLoads; ++j) {
-        const int f = threadIdx.x + kBlock * j, row = f / (kGemmStage / 16), col = (f % (kGemmStage / 16)) * 16;
-        // Rows past the token or weight count read row 0 instead: their
-        // sums are never stored, and no select waits on the load here.
-        const int t = m0 + row, n = n0 + row;
-        ra[j] = *(const v4i*)(xq + (size_t)(t < tokens ? t : 0) * K + k0 + col);
-        rb[j] = __builtin_nontemporal_load((const v4i*)(W + (size_t)(n < N ? n : 0) * K + k0 + col));
-    }
-}
-__device__ __forceinline__ void gemm_stage_store(int8_t* la, int8_t* lb, const v4i (&ra)[kGemmLoads],
-                                                 const v4i (&rb)[kGemmLoads]) {
-#pragma unroll
-    for (int j = 0; j < kGemmLoads; ++j) {
-        const int f = threadIdx.x + kBlock * j, row = f / (kGemmStage / 16), col = (f % (kGemmStage / 16)) * 16;
-        *(v4i*)(la + row * kGemmRow + col) = ra[j];
-        *(v4i*)(lb + row * kGemmRow + col) = rb[j];
-    }
-}
-
-// Split K (blockIdx.z = split of `splits`, each `split_stages` stages long):
-// with `partial` set, a block stores its int32 sums to partial[split][t][n]
-// and gemm_w8a8_split_epilogue adds the splits (exactly, in split order) and
-// applies the epilogue; without it, the block applies the epilogue itself.
-__global__ __launch_bounds__(kBlock, 2) void gemm_w8a8_tile_kernel(WeightView w, const int8_t* __restrict__ xq,
-                                                               const float* __restrict__ xs, int tokens,
-                                                               float* __restrict__ y, int epilogue,
-                                                               int32_t* __restrict__ acc_out, int split_stages,
-                                                               int32_t* __restrict__ partial) {
-    __shared__ __align__(16) int8_t lds[2][2][kGemmTile * kGemmRow];   // [buffer][activations | weights]
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int K = w.cols, N = w.rows;
-    const int m0 = blockIdx.y * kGemmTile, n0 = blockIdx.x * kGemmTile;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int li = lane & 15, lk = (lane >> 4) * 16;
-    const int8_t* W = (const int8_t*)w.data;
-    v4i acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    v4i ra[kGemmLoads], rb[kGemmLoads];
-    const int stages = split_stages;
-    const int kb = blockIdx.z * split_stages * kGemmStage;   // this split's first K byte
-    gemm_stage_load(xq, W, K, tokens, N, m0, n0, kb, ra, rb);
-    gemm_stage_store(lds[0][0], lds[0][1], ra, rb);
-    __syncthreads();
-    for (int s = 0; s < stages; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < stages) gemm_stage_load(xq, W, K, tokens, N, m0, n0, kb + (s + 1) * kGemmStage, ra, rb);
-        const int8_t* A = lds[buf][0];
-        const int8_t* B = lds[buf][1];
-#pragma unroll
-        for (int kk = 0; kk < kGemmStage / 64; ++kk) {
-            v4i af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *(const v4i*)(A + (wm + 16 * i + li) * kGemmRow + 64 * kk + lk);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bf[j] = *(const v4i*)(B + (wn + 16 * j + li) * kGemmRow + 64 * kk + lk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        // the other buffer was last read before the previous barrier
-        if (s + 1 < stages) gemm_stage_store(lds[buf ^ 1][0], lds[buf ^ 1][1], ra, rb);
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + wn + 16 * j + li;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
-                if (t < tokens && n < N) {
-                    if (partial) {
-                        partial[((size_t)blockIdx.z * tokens + t) * N + n] = acc[i][j][r];
-                    } else {
-                        if (acc_out) acc_out[(size_t)t * N + n] = acc[i][j][r];
-                        const float res = fmaf((float)acc[i][j][r] * xs[t], w.scales[n], 0.0f);
-                        store_out(y, (size_t)t * N + n, res, bias_at(w, n), epilogue);
-                    }
-                }
-            }
-        }
-}
-
+// ---------------------- W8A8 prefill, per-row scales: split-K epilogue ---
+// The MFMA GEMM (gemm_w8a8.hip) stores each K split's exact int32 sums to
+// partial[split][t][n]; this adds them in split order and applies the CPU
+// path's epilogue, so results are bit-identical to an unsplit run.
 __global__ __launch_bounds__(kBlock) void gemm_w8a8_split_epilogue(WeightView w, const float* __restrict__ xs,
                                                                   int tokens, const int32_t* __restrict__ partial,
                                                                   int splits, float* __restrict__ y, int epilogue,
@@ -1839,22 +1733,26 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
             if (w.bits == 8) launch_gemv_int<8>(c, xq, xs, stream); else launch_gemv_int<4>(c, xq, xs, stream);
             return 1;
         }
-        if (path == 3 && w.group == K && K % kGemmStage == 0) {
-            const int tiles = ceil_div(w.rows, kGemmTile) * ceil_div(c.tokens, kGemmTile);
-            const int steps = K / 64;
-            // Split K until the grid covers the CUs once (measured ahead of twice),
-            // each split a whole number of stages, when a workspace is given.
+        if (path == 3 && w.group == K && gemm_w8a8_mfma_supported(K)) {
+            // Tiles of 128 tokens (64 for short inputs) x 128 rows.  Grids
+            // short of the 256 CUs split K: in two for K <= 4096 at 64 tiles
+            // or more (measured ahead of three and four at 2048 x 2048-2560,
+            // 512 tokens), up to four otherwise, each split at least two
+            // 128-byte stages, when a workspace for the int32 sums is given.
+            const int tile_m = c.tokens <= 64 ? 64 : 128;
+            const int tiles = ceil_div(w.rows, 128) * ceil_div(c.tokens, tile_m);
+            const int stages = K / 128;
             int splits = 1;
-            const int stages = steps / (kGemmStage / 64);
-            while (c.split_scratch && tiles * splits < 256 && stages % (2 * splits) == 0 &&
-                   stages / (2 * splits) >= 2 && (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
-                splits *= 2;
-            dim3 grid(ceil_div(w.rows, kGemmTile), ceil_div(c.tokens, kGemmTile), splits);
+            if (c.split_scratch && tiles < 192) {
+                const int cap = (K > 4096 || tiles < 64) ? 4 : 2;
+                while (2 * splits <= cap && tiles * 2 * splits <= 512 && stages >= 4 * splits &&
+                       (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
+                    splits *= 2;
+            }
             int32_t* partial = splits > 1 ? c.split_scratch : nullptr;
-            gemm_w8a8_tile_kernel<<<grid, kBlock, 0, stream>>>(w, xq, xs, c.tokens, c.y, c.epilogue, c.acc_out,
-                                                              stages / splits, partial);
+            launch_gemm_w8a8_mfma((const int8_t*)w.data, w.scales, w.bias, xq, xs, c.tokens, w.rows, K, c.y,
+                                  c.epilogue, c.acc_out, tile_m, splits, partial, stream);
             if (partial) {
-                const int blocks = std::min(ceil_div((size_t)c.tokens * w.rows, kBlock), 4096);
                 const bool vec = w.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(c.y) & 15) == 0 &&
                                  (reinterpret_cast<uintptr_t>(partial) & 15) == 0 &&
                                  (reinterpret_cast<uintptr_t>(c.acc_out) & 15) == 0;
@@ -1863,8 +1761,9 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
                                                 0, stream>>>(w, xs, c.tokens, partial, splits, c.y, c.epilogue,
                                                              c.acc_out);
                 else
-                    gemm_w8a8_split_epilogue<<<blocks, kBlock, 0, stream>>>(w, xs, c.tokens, partial, splits, c.y,
-                                                                            c.epilogue, c.acc_out);
+                    gemm_w8a8_split_epilogue<<<std::min(ceil_div((size_t)c.tokens * w.rows, kBlock), 4096), kBlock, 0,
+                                               stream>>>(w, xs, c.tokens, partial, splits, c.y, c.epilogue,
+                                                         c.acc_out);
             }
             return 3;
         }

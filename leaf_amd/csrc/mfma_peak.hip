@@ -2,8 +2,10 @@
 //
 //   mfma_peak [iterations]
 //
-// Every CU runs 16 waves; each wave issues `iterations` rounds of eight
-// independent accumulator chains of one MFMA instruction, operands held in
+// Every CU runs 16 waves; each wave issues `iterations` rounds of independent
+// accumulator chains of one MFMA instruction (sixteen for the 16x16 shapes,
+// eight for the 32x32 ones: fewer 16x16 chains leave the pipe waiting on each
+// result, 8 chains measured 2.5 against 4.4 POPS for int8), operands held in
 // registers, so nothing but the matrix cores limits the rate.  Prints one line
 // per instruction: dense operations per second (2 m n k per instruction).
 // The prefill GEMMs' utilisation is reported against these measured rates
@@ -20,7 +22,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-constexpr int kChains = 8;
+constexpr int kChains = 16;
 
 __global__ __launch_bounds__(256) void mfma_i8_kernel(int iterations, int* sink) {
     const v4i a = {(int)threadIdx.x, 1, 2, 3}, b = {3, 2, 1, (int)threadIdx.x};
