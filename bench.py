@@ -153,9 +153,25 @@ def decode_benchmark(path: Path, steps: int, warmup: int, prefill_repeats: int =
         dec.forward_into(prompt, None)
         runtime.synchronize()
         warm.append((time.perf_counter() - t) * 1e3)
+    # One more prefill with every launch bracketed by HIP events: device time,
+    # operations and TOPS per kernel class.
+    dec.reset()
+    dec.set_profiling(True)
+    dec.forward_into(prompt, None)
+    runtime.synchronize()
+    prefill_classes = {}
+    for name, v in dec.profile().items():
+        entry = {"launches": v["launches"], "ms": round(v["ms"], 4)}
+        if v["ops"] > 0 and v["ms"] > 0:
+            rate = v["ops"] / v["ms"] / 1e9          # TOPS (or TFLOP/s)
+            peak = INT8_PEAK_TOPS if name == "gemm_w8a8" else F32_PEAK_TFLOPS
+            entry.update({"T_per_s": round(rate, 1), "frac_peak": round(rate / peak, 4)})
+        prefill_classes[name] = entry
+    dec.set_profiling(False)
     dec.close()
     return {"elapsed_s": elapsed, "prefill_ms": prefill_ms, "profile": profile, "context_end": ctx_end,
-            "prefill_warm_ms": float(np.median(warm)) if warm else None, "fast": fast}
+            "prefill_warm_ms": float(np.median(warm)) if warm else None, "fast": fast,
+            "prefill_classes": prefill_classes}
 
 
 def reference_numerics_run(path: Path) -> dict:
@@ -184,8 +200,29 @@ def reference_numerics_run(path: Path) -> dict:
             "decode_tok_s": round((len(tokens) - 1) / elapsed, 1), "prefill_ms": round(prefill_ms, 2)}
 
 
+def _replayed_us(calls: list, replays: int) -> float:
+    """Microseconds per call of `calls` (closures that take a stream), captured
+    once into a HIP graph and replayed: the GPU runs them back to back, so the
+    figure is device time, not the Python caller's launch rate."""
+    from leaf_amd import runtime
+    stream = runtime.Stream()
+    for call in calls[:3]:
+        call(stream.handle)          # any scratch grows before the capture
+    stream.synchronize()
+    graph = runtime.Graph(stream, lambda: [call(stream.handle) for call in calls])
+    graph.launch()
+    stream.synchronize()
+    timer = runtime.Timer(stream.handle)
+    for _ in range(replays):
+        graph.launch()
+    ms = timer.stop()
+    graph.close()
+    stream.close()
+    return ms * 1e3 / (replays * len(calls))
+
+
 def gemv_microbench(repeats: int = 20) -> dict:
-    """W8A8 GEMV at M = 1 over >= 1 GiB of rotating weight copies."""
+    """W8A8 GEMV at M = 1 over >= 1 GiB of rotating weight copies, graph-replayed."""
     from leaf_amd import runtime
     from leaf_amd.models import W8A8_LINEAR_SHAPES
     rng = np.random.default_rng(SEED + 2)
@@ -200,19 +237,11 @@ def gemv_microbench(repeats: int = 20) -> dict:
     for (K, N) in shapes:
         x = runtime.DeviceArray.of(rng.standard_normal((1, K), dtype=np.float32))
         y = runtime.DeviceArray((1, N), np.float32)
-        ws = weights[(K, N)]
-        for w in ws[:4]:
-            runtime.linear(w, x, 1, 8, y)
-        timer = runtime.Timer()
-        launches = 0
-        for r in range(repeats):
-            for w in ws:
-                runtime.linear(w, x, 1, 8, y)
-                launches += 1
-        ms = timer.stop() / launches
+        calls = [lambda st, w=w: runtime.linear(w, x, 1, 8, y, stream=st) for w in weights[(K, N)]]
+        us = _replayed_us(calls, repeats)
         algorithmic = N * K + 4 * N + K + 4 * N
-        results[f"{K}x{N}"] = {"us": round(ms * 1e3, 3), "GBps": round(algorithmic / ms / 1e6, 1),
-                               "frac": round(algorithmic / ms / 1e6 / HBM_PEAK_GBS, 3)}
+        results[f"{K}x{N}"] = {"us": round(us, 3), "GBps": round(algorithmic / us / 1e3, 1),
+                               "frac": round(algorithmic / us / 1e3 / HBM_PEAK_GBS, 3)}
     total_bytes = sum(K * N + 8 * N + K for K, N in W8A8_LINEAR_SHAPES)
     total_us = sum(results[f"{K}x{N}"]["us"] for K, N in W8A8_LINEAR_SHAPES)
     results["layer_set"] = {"GBps": round(total_bytes / total_us / 1e3, 1), "copies": copies,
@@ -227,9 +256,10 @@ def linear_microbench(tokens=(4, 16, 128, 512), repeats: int = 3) -> dict:
     """W8A8 linear at the TinyLlama shapes for M > 1 tokens: per-token int8
     activations (quantized beforehand, as the decoder's norm epilogues leave
     them), per-row int8 weights, the split-K epilogue included, rotating
-    >= 1 GiB of weight copies.  Reported per shape as microseconds per call,
-    int8 TOPS against the 5.0 POPS dense peak, and the bytes of the call
-    (N*K + 8N + M*K + 4M + 4MN) per microsecond."""
+    >= 1 GiB of weight copies, graph-replayed (device time per call).
+    Reported per shape as microseconds per call, int8 TOPS against the 5.0
+    POPS dense peak, and the bytes of the call (N*K + 8N + M*K + 4M + 4MN)
+    per microsecond."""
     from leaf_amd import runtime
     from leaf_amd.models import W8A8_LINEAR_SHAPES
     rng = np.random.default_rng(SEED + 3)
@@ -248,21 +278,13 @@ def linear_microbench(tokens=(4, 16, 128, 512), repeats: int = 3) -> dict:
             q = runtime.DeviceArray.of(rng.integers(-127, 128, (M, K), dtype=np.int8))
             xs = runtime.DeviceArray.of((rng.random(M, dtype=np.float32) * 1e-2 + 1e-3).astype(np.float32))
             y = runtime.DeviceArray((M, N), np.float32)
-            ws = weights[(K, N)]
-            for w in ws[:3]:
-                runtime.linear_q(w, q, xs, M, y)
-            timer = runtime.Timer()
-            launches = 0
-            for _ in range(repeats):
-                for w in ws:
-                    runtime.linear_q(w, q, xs, M, y)
-                    launches += 1
-            ms = timer.stop() / launches
+            calls = [lambda st, w=w: runtime.linear_q(w, q, xs, M, y, stream=st) for w in weights[(K, N)]]
+            us = _replayed_us(calls, repeats)
             ops = 2.0 * M * N * K
             traffic = N * K + 8 * N + M * K + 4 * M + 4 * M * N
-            row[f"{K}x{N}"] = {"us": round(ms * 1e3, 2), "TOPS": round(ops / ms / 1e9, 1),
-                               "frac_mfma": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
-                               "GBps": round(traffic / ms / 1e6, 1)}
+            row[f"{K}x{N}"] = {"us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
+                               "frac_mfma": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                               "GBps": round(traffic / us / 1e3, 1)}
         out[f"M={M}"] = row
     for s in weights.values():
         s.clear()
@@ -541,7 +563,8 @@ def main() -> int:
                                "decode", "layers": 22, "hidden": 2048, "heads": 32, "kv_heads": 4, "ffn": 5632,
                    "vocab": 32000, "prompt_tokens": PROMPT_TOKENS, "context_end": d["context_end"],
                    "prefill_ms": round(d["prefill_ms"], 2),
-                   "prefill_warm_p50_ms": round(d["prefill_warm_ms"], 3) if d["prefill_warm_ms"] else None},
+                   "prefill_warm_p50_ms": round(d["prefill_warm_ms"], 3) if d["prefill_warm_ms"] else None,
+                   "prefill_classes": d["prefill_classes"]},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -7,10 +7,17 @@
 // K % 128 == 0.  The integer sums are exact and the epilogue is the CPU
 // path's expression, so every output is bit-identical to it.
 //
-// Tiling.  A block owns BM tokens x 128 weight rows; each of its waves owns a
-// 64 x 64 sub-tile as 2 x 2 v_mfma_i32_32x32x32_i8 accumulators (4
-// independent chains per wave keep the matrix pipe issuing back to back).
-// K advances 128 bytes per pipeline stage.
+// Tiling.  A block of four waves (2 x 2) owns 64 TM weight rows x 64 TN
+// tokens; each wave a TM x TN grid of v_mfma_i32_32x32x32_i8 tiles.  The
+// weight rows are the MFMA's A operand and the tokens its B operand, so a
+// lane of an output tile holds one token and, per group of four results,
+// four consecutive weight rows: the epilogue writes 16-byte vectors (with
+// the tokens as A it would write single words, and a wave may keep only 63
+// memory instructions in flight, which made the output drain, not the
+// matrix cores, the limit).  Tiles with fewer than four MFMA tiles per wave
+// keep two accumulator sets, alternate k-steps between them and add them at
+// the end (exact integer sums), so consecutive MFMAs never depend on each
+// other.  K advances 128 bytes per pipeline stage.
 //
 // Operand staging.  global_load_lds_dwordx4 moves each lane's 16 bytes from
 // global memory straight into LDS (no register round trip), NSTAGE - 1
@@ -20,12 +27,7 @@
 // segment c of row r sits in slot c ^ (r % 8) of its 128-byte LDS row (XOR
 // swizzle).  An MFMA operand (32 rows x 32 K bytes; lane l holds row l % 32,
 // segment 2 step + l / 32) then reads eight different slots across any eight
-// consecutive rows: no LDS bank conflicts.  A stage is [A rows | B rows].
-//
-// Issue order.  Per stage a wave issues 16 MFMAs, 16 operand reads and its
-// share of the next stage's loads; sched_barrier fences pin an order in which
-// consecutive MFMAs use different accumulators and the loads and later reads
-// sit between MFMA pairs, so the matrix pipe does not wait for issue bursts.
+// consecutive rows: no LDS bank conflicts.  A stage is [weight rows | tokens].
 //
 // Waiting.  Loads retire in order per wave, and every iteration issues one
 // stage, so "stage s landed" is vmcnt <= (NSTAGE - 2) stages of loads; each
@@ -44,14 +46,11 @@
 #include "device_common.h"
 #include "kernels.h"
 
-#include <type_traits>
-
 namespace leafhip {
 namespace {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int kTileN = 128;     // weight rows per block
 constexpr int kStageK = 128;    // K bytes per pipeline stage
 constexpr int kChunkBytes = 1024;
 
@@ -73,24 +72,31 @@ __device__ __forceinline__ void block_barrier_lds() {
     asm volatile("" ::: "memory");
 }
 
-template <int BM, int NSTAGE>
-__global__ __launch_bounds__(BM / 64 * 2 * 64) void gemm_w8a8_mfma_kernel(
+// One output element: the CPU path's epilogue, stored or added to y.
+__device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
+    return fmaf((float)acc * sx, sw, 0.0f) + b;
+}
+
+template <int TM, int TN, int NSTAGE>
+__global__ __launch_bounds__(256) void gemm_w8a8_mfma_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ w_scales, const float* __restrict__ bias,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, int M, int N, int K, float* __restrict__ y,
-    int epilogue, int32_t* __restrict__ acc_out, int splits, int32_t* __restrict__ partial) {
-    constexpr int kWaves = BM / 64 * 2;
-    constexpr int kChunksA = BM / 8;                        // 8 rows x 128 K bytes per chunk
-    constexpr int kChunks = kChunksA + kTileN / 8;
-    constexpr int kLoads = kChunks / kWaves;                 // 16-byte loads per lane per stage
+    int epilogue, int32_t* __restrict__ acc_out, int splits, int32_t* __restrict__ partial, bool vec) {
+    constexpr int BN = 64 * TM, BM = 64 * TN;                 // weight rows, tokens per block
+    constexpr int kChunksW = BN / 8;                          // 8 rows x 128 K bytes per chunk
+    constexpr int kChunks = kChunksW + BM / 8;
+    constexpr int kLoads = kChunks / 4;                       // 16-byte loads per lane per stage
     constexpr int kStageBytes = kChunks * kChunkBytes;
-    static_assert(kChunks % kWaves == 0, "chunks must divide among the waves");
+    constexpr int kSets = TM * TN >= 4 ? 1 : 2;               // accumulator sets (alternating k-steps)
+    static_assert(kChunks % 4 == 0, "chunks must divide among the waves");
+    static_assert((NSTAGE - 2) * kLoads < 64, "vmcnt holds at most 63");
     __shared__ __align__(1024) int8_t lds[NSTAGE * kStageBytes];
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     // ---- work item
     const int mt = (M + BM - 1) / BM;
-    const int nt = (N + kTileN - 1) / kTileN;
+    const int nt = (N + BN - 1) / BN;
     const int units = nt * splits;
     int m_tile, unit;
     {
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(BM / 64 * 2 * 64) void gemm_w8a8_mfma_kernel(
         }
     }
     const int n_tile = unit / splits, split = unit % splits;
-    const int m0 = m_tile * BM, n0 = n_tile * kTileN;
+    const int m0 = m_tile * BM, n0 = n_tile * BN;
     const int total_stages = K / kStageK;
     const int s_begin = split * total_stages / splits, s_end = (split + 1) * total_stages / splits;
     const int ns = s_end - s_begin;
@@ -115,194 +121,201 @@ __global__ __launch_bounds__(BM / 64 * 2 * 64) void gemm_w8a8_mfma_kernel(
     int dst[kLoads];
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-        const int c = j * kWaves + wave;
-        const bool is_a = c < kChunksA;
-        const int cc = is_a ? c : c - kChunksA;
+        const int c = j * 4 + wave;
+        const bool is_w = c < kChunksW;
+        const int cc = is_w ? c : c - kChunksW;
         const int row = cc * 8 + (lane >> 3);
         const int koff = ((lane & 7) ^ (lane >> 3)) * 16 + s_begin * kStageK;   // swizzled 16-byte segment
-        if (is_a) {
-            const int t = m0 + row < M ? m0 + row : M - 1;   // rows past the end are never stored
-            src[j] = xq + (size_t)t * K + koff;
-        } else {
-            const int n = n0 + row < N ? n0 + row : N - 1;
+        if (is_w) {
+            const int n = n0 + row < N ? n0 + row : N - 1;    // rows past the end are never stored
             src[j] = W + (size_t)n * K + koff;
+        } else {
+            const int t = m0 + row < M ? m0 + row : M - 1;
+            src[j] = xq + (size_t)t * K + koff;
         }
         dst[j] = c * kChunkBytes;
     }
 
-    // ---- accumulators: wave sub-tile rows wm.., cols wn..
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    v16i acc[2][2];
+    // ---- accumulators: wave sub-tile rows wn.., tokens wm..
+    const int wn = (wave >> 1) * 32 * TM, wm = (wave & 1) * 32 * TN;
+    v16i acc[kSets][TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < kSets; ++q)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[q][i][j][r] = 0;
 
     // Operand read offsets within a stage buffer.  Lane l reads row l % 32 of
-    // a 32-row operand, 16-byte K segment 2 step + l / 32, stored at slot
-    // segment ^ (row % 8) of its 128-byte LDS row.
-    const int row_off = ((lane & 31) >> 3) * kChunkBytes + (lane & 7) * 128;
+    // a 32-row operand (row r of the stage sits at r * 128), 16-byte K
+    // segment 2 step + l / 32, stored at slot segment ^ (row % 8).
+    const int row_off = (lane & 31) * 128;
     int seg_off[4];
 #pragma unroll
     for (int step = 0; step < 4; ++step) seg_off[step] = ((2 * step + (lane >> 5)) ^ (lane & 7)) * 16;
-    int a_off[2], b_off[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        a_off[i] = (wm + 32 * i) * 128 + row_off;
-        b_off[i] = kChunksA * kChunkBytes + (wn + 32 * i) * 128 + row_off;
-    }
     {
         // Stages past the split's end load the first 16 bytes of the
         // activations (an L1 hit) into a buffer nobody reads again, so every
         // iteration issues exactly one stage.
-        auto issue = [&](int stage, int buffer) {
-            const bool real = stage < ns;
-#pragma unroll
-            for (int j = 0; j < kLoads; ++j)
-                __builtin_amdgcn_global_load_lds((void*)(real ? src[j] + stage * kStageK : xq),
-                                                 (lds_ptr_t)(lds + buffer * kStageBytes + dst[j]), 16, 0, 0);
-        };
         auto issue_one = [&](int j, int stage, int buffer) {
             __builtin_amdgcn_global_load_lds((void*)(stage < ns ? src[j] + stage * kStageK : xq),
                                              (lds_ptr_t)(lds + buffer * kStageBytes + dst[j]), 16, 0, 0);
         };
-        for (int s = 0; s < NSTAGE - 1; ++s) issue(s, s);
+        for (int s = 0; s < NSTAGE - 1; ++s)
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) issue_one(j, s, s);
         for (int s = 0; s < ns; ++s) {
             wait_vmcnt<(NSTAGE - 2) * kLoads>();
             block_barrier_lds();
             const int8_t* base = lds + (s % NSTAGE) * kStageBytes;
             const int next = s + NSTAGE - 1, next_buffer = next % NSTAGE;
-            v4i fa[4][2], fb[4][2];
-            auto read = [&](int step, int i) {
-                const int koff = seg_off[step];
-                fa[step][i] = *(const v4i*)(base + a_off[i] + koff);
-                fb[step][i] = *(const v4i*)(base + b_off[i] + koff);
-            };
-            // The first two k-steps' operands, then eight MFMA pairs, each
-            // followed by a share of the next stage's loads and (first four)
-            // the last two k-steps' operands.
+            // Per k-step: TM weight and TN token operand reads, TM x TN MFMAs,
+            // then a quarter of the next stage's loads.
 #pragma unroll
-            for (int step = 0; step < 2; ++step)
+            for (int step = 0; step < 4; ++step) {
+                v4i fw[TM], fx[TN];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) read(step, i);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < TM; ++i) fw[i] = *(const v4i*)(base + (wn + 32 * i) * 128 + row_off + seg_off[step]);
 #pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                const int step = g >> 1, i = g & 1;
-                acc[i][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[step][i], fb[step][0], acc[i][0], 0, 0, 0);
-                acc[i][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[step][i], fb[step][1], acc[i][1], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < TN; ++j)
+                    fx[j] = *(const v4i*)(base + kChunksW * kChunkBytes + (wm + 32 * j) * 128 + row_off + seg_off[step]);
 #pragma unroll
-                for (int j = g * kLoads / 8; j < (g + 1) * kLoads / 8; ++j) issue_one(j, next, next_buffer);
-                if (g < 4) read(2 + (g >> 1), g & 1);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[step % kSets][i][j] =
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[i], fx[j], acc[step % kSets][i][j], 0, 0, 0);
+#pragma unroll
+                for (int j = step * kLoads / 4; j < (step + 1) * kLoads / 4; ++j) issue_one(j, next, next_buffer);
             }
         }
         wait_vmcnt<0>();
     }
+    if (kSets == 2) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[0][i][j] += acc[kSets - 1][i][j];
+    }
 
-    // ---- epilogue: lane holds column n = .. + lane % 32 and rows 8 (r/4) + 4 (lane/32) + r % 4.
-    if (m0 + BM <= M && n0 + kTileN <= N) {
-        // whole tile in range: straight-line stores, every operand load issued first
-        const int tb = m0 + wm + 4 * (lane >> 5);
-        const int nb = n0 + wn + (lane & 31);
-        if (partial) {
-            int32_t* out = partial + (size_t)split * M * N + nb;
+    // ---- epilogue.  Output tile (i, j): lane holds token m0 + wm + 32 j +
+    // lane % 32 and, for g = 0..3, rows n0 + wn + 32 i + 8 g + 4 (lane / 32)
+    // + 0..3 in acc[.][4 g + 0..3].  `vec`: N % 4 == 0 and every output,
+    // scale and bias pointer 16-byte aligned, so four rows move as one vector.
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < TN; ++j) {
+        const int t = m0 + wm + 32 * j + (lane & 31);
+        if (t >= M) continue;
+        const float sx = partial ? 0.0f : xs[t];
+        const size_t row_base = (size_t)t * N;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    int32_t* row = out + (size_t)(tb + 32 * i + 8 * (r >> 2) + (r & 3)) * N;
-                    row[0] = acc[i][0][r];
-                    row[32] = acc[i][1][r];
-                }
-            return;
-        }
-        const float sw0 = w_scales[nb], sw1 = w_scales[nb + 32];
-        const float b0 = bias ? bias[nb] : 0.0f, b1 = bias ? bias[nb + 32] : 0.0f;
-        float* yb = y + nb;
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            float sx[16];
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn + 32 * i + 8 * g + 4 * (lane >> 5);
+                const v4i a = v4i{acc[0][i][j][4 * g], acc[0][i][j][4 * g + 1], acc[0][i][j][4 * g + 2],
+                                  acc[0][i][j][4 * g + 3]};
+                if (vec && n + 3 < N) {
+                    if (partial) {
+                        *(v4i*)(partial + (size_t)split * M * N + row_base + n) = a;
+                        continue;
+                    }
+                    if (acc_out) *(v4i*)(acc_out + row_base + n) = a;
+                    const v4f sw = *(const v4f*)(w_scales + n);
+                    const v4f b = bias ? *(const v4f*)(bias + n) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                    v4f o;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sx[r] = xs[tb + 32 * i + 8 * (r >> 2) + (r & 3)];
-            if (acc_out) {
+                    for (int q = 0; q < 4; ++q) o[q] = dequant(a[q], sx, sw[q], b[q]);
+                    float* out = y + row_base + n;
+                    if (epilogue == kAccumulate) {
+                        const v4f prev = *(const v4f*)out;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    int32_t* row = acc_out + (size_t)(tb + 32 * i + 8 * (r >> 2) + (r & 3)) * N + nb;
-                    row[0] = acc[i][0][r];
-                    row[32] = acc[i][1][r];
-                }
-            }
-            if (epilogue == kAccumulate) {
-                float prev[16][2];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float* row = yb + (size_t)(tb + 32 * i + 8 * (r >> 2) + (r & 3)) * N;
-                    prev[r][0] = row[0];
-                    prev[r][1] = row[32];
-                }
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float* row = yb + (size_t)(tb + 32 * i + 8 * (r >> 2) + (r & 3)) * N;
-                    row[0] = prev[r][0] + (fmaf((float)acc[i][0][r] * sx[r], sw0, 0.0f) + b0);
-                    row[32] = prev[r][1] + (fmaf((float)acc[i][1][r] * sx[r], sw1, 0.0f) + b1);
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float* row = yb + (size_t)(tb + 32 * i + 8 * (r >> 2) + (r & 3)) * N;
-                    row[0] = fmaf((float)acc[i][0][r] * sx[r], sw0, 0.0f) + b0;
-                    row[32] = fmaf((float)acc[i][1][r] * sx[r], sw1, 0.0f) + b1;
-                }
-            }
-        }
-        return;
-    }
-    // edge tile: per-element bounds
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + 32 * j + (lane & 31);
-        if (n >= N) continue;
-        const float sw = partial ? 0.0f : w_scales[n];
-        const float b = (partial || !bias) ? 0.0f : bias[n];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t >= M) continue;
-                const int a = acc[i][j][r];
-                const size_t o = (size_t)t * N + n;
-                if (partial) {
-                    partial[(size_t)split * M * N + o] = a;
+                        for (int q = 0; q < 4; ++q) o[q] = prev[q] + o[q];
+                    }
+                    *(v4f*)out = o;
                 } else {
-                    if (acc_out) acc_out[o] = a;
-                    const float v = fmaf((float)a * xs[t], sw, 0.0f) + b;
-                    y[o] = epilogue == kAccumulate ? y[o] + v : v;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (n + q >= N) continue;
+                        const size_t o = row_base + n + q;
+                        if (partial) {
+                            partial[(size_t)split * M * N + o] = a[q];
+                            continue;
+                        }
+                        if (acc_out) acc_out[o] = a[q];
+                        const float v = dequant(a[q], sx, w_scales[n + q], bias ? bias[n + q] : 0.0f);
+                        y[o] = epilogue == kAccumulate ? y[o] + v : v;
+                    }
                 }
             }
     }
+}
+
+template <int TM, int TN, int NSTAGE>
+void launch_tiles(const int8_t* W, const float* w_scales, const float* bias, const int8_t* xq, const float* xs,
+                  int M, int N, int K, float* y, int epilogue, int32_t* acc_out, int splits, int32_t* partial,
+                  hipStream_t stream) {
+    auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vec = N % 4 == 0 && aligned(w_scales) && aligned(bias) && aligned(y) && aligned(acc_out) &&
+                     aligned(partial);
+    const dim3 grid(((M + 64 * TN - 1) / (64 * TN)) * ((N + 64 * TM - 1) / (64 * TM)) * splits);
+    gemm_w8a8_mfma_kernel<TM, TN, NSTAGE><<<grid, 256, 0, stream>>>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue,
+                                                                     acc_out, splits, partial, vec);
 }
 
 }  // namespace
 
 bool gemm_w8a8_mfma_supported(int K) { return K % kStageK == 0 && K > 0; }
 
+GemmTiles gemm_w8a8_tiles(int M, int N, int K, size_t split_capacity) {
+    // Large outputs (the stacked gate|up projection of a 512-token prefill)
+    // take 128 weight rows x 256 tokens per block; everything else 64 x 64,
+    // which puts the most blocks on the CUs.  A grid still short of 128
+    // blocks (few tokens) splits K, each split at least four 128-byte stages,
+    // when the workspace holds the int32 sums.
+    GemmTiles g;
+    auto count = [&](int bn, int bm) { return ((N + bn - 1) / bn) * ((M + bm - 1) / bm); };
+    if (M >= 256 && count(128, 256) >= 128) {
+        g.rows = 128;
+        g.tokens = 256;
+    } else {
+        g.rows = 64;
+        g.tokens = 64;
+    }
+    const int tiles = count(g.rows, g.tokens);
+    const int stages = K / kStageK;
+    g.splits = 1;
+    while (tiles * g.splits < 128 && stages >= 8 * g.splits &&
+           (size_t)(2 * g.splits) * M * N <= split_capacity)
+        g.splits *= 2;
+    return g;
+}
+
 void launch_gemm_w8a8_mfma(const int8_t* W, const float* w_scales, const float* bias, const int8_t* xq,
                            const float* xs, int M, int N, int K, float* y, int epilogue, int32_t* acc_out,
-                           int tile_m, int splits, int32_t* partial, hipStream_t stream) {
-    const int nt = (N + kTileN - 1) / kTileN;
-    if (tile_m == 64) {
-        const dim3 grid(((M + 63) / 64) * nt * splits);
-        gemm_w8a8_mfma_kernel<64, 6><<<grid, 128, 0, stream>>>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue,
-                                                                acc_out, splits, partial);
-    } else {
-        const dim3 grid(((M + 127) / 128) * nt * splits);
-        gemm_w8a8_mfma_kernel<128, 4><<<grid, 256, 0, stream>>>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue,
-                                                                 acc_out, splits, partial);
+                           const GemmTiles& tiles, int32_t* partial, hipStream_t stream) {
+    const int splits = partial ? tiles.splits : 1;
+    const int shape = tiles.rows * 1000 + tiles.tokens;
+    switch (shape) {
+    case 128256:
+        launch_tiles<2, 4, 3>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+        break;
+    case 256128:
+        launch_tiles<4, 2, 3>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+        break;
+    case 128128:
+        launch_tiles<2, 2, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+        break;
+    case 128064:
+        launch_tiles<2, 1, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+        break;
+    case 64128:
+        launch_tiles<1, 2, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+        break;
+    default:
+        launch_tiles<1, 1, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
     }
 }
 

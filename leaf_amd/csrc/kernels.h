@@ -100,14 +100,21 @@ struct LinearCall {
 };
 // W8A8 prefill GEMM on int8 MFMA (gemm_w8a8.hip) for per-row weight scales:
 // y[t, n] = ((float)sum_k xq[t, k] W[n, k] * xs[t]) * w_scales[n] + bias[n]
-// (kStore) or y += that (kAccumulate).  K % 128 == 0.  Blocks own tile_m (64
-// or 128) tokens x 128 rows; with splits > 1 the K range is split and the
-// exact int32 sums go to partial[split][t][n] instead of y (acc_out and the
-// epilogue are then the split epilogue's).
+// (kStore) or y += that (kAccumulate).  K % 128 == 0.  Blocks own
+// tiles.rows weight rows x tiles.tokens tokens; with partial set the K range
+// is split tiles.splits ways and the exact int32 sums go to
+// partial[split][t][n] instead of y (acc_out and the epilogue are then the
+// split epilogue's).
+struct GemmTiles {
+    int rows = 64, tokens = 64, splits = 1;
+};
 bool gemm_w8a8_mfma_supported(int K);
+// The tile shape and K split for an M x N x K product; splits > 1 only when
+// 2 * splits * M * N int32 sums fit in split_capacity.
+GemmTiles gemm_w8a8_tiles(int M, int N, int K, size_t split_capacity);
 void launch_gemm_w8a8_mfma(const int8_t* W, const float* w_scales, const float* bias, const int8_t* xq,
                            const float* xs, int M, int N, int K, float* y, int epilogue, int32_t* acc_out,
-                           int tile_m, int splits, int32_t* partial, hipStream_t stream);
+                           const GemmTiles& tiles, int32_t* partial, hipStream_t stream);
 
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
 // the call cannot run (missing scratch for the GEMM quantization).

@@ -1734,24 +1734,11 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
             return 1;
         }
         if (path == 3 && w.group == K && gemm_w8a8_mfma_supported(K)) {
-            // Tiles of 128 tokens (64 for short inputs) x 128 rows.  Grids
-            // short of the 256 CUs split K: in two for K <= 4096 at 64 tiles
-            // or more (measured ahead of three and four at 2048 x 2048-2560,
-            // 512 tokens), up to four otherwise, each split at least two
-            // 128-byte stages, when a workspace for the int32 sums is given.
-            const int tile_m = c.tokens <= 64 ? 64 : 128;
-            const int tiles = ceil_div(w.rows, 128) * ceil_div(c.tokens, tile_m);
-            const int stages = K / 128;
-            int splits = 1;
-            if (c.split_scratch && tiles < 192) {
-                const int cap = (K > 4096 || tiles < 64) ? 4 : 2;
-                while (2 * splits <= cap && tiles * 2 * splits <= 512 && stages >= 4 * splits &&
-                       (size_t)(2 * splits) * c.tokens * w.rows <= c.split_capacity)
-                    splits *= 2;
-            }
-            int32_t* partial = splits > 1 ? c.split_scratch : nullptr;
+            const GemmTiles tiles = gemm_w8a8_tiles(c.tokens, w.rows, K, c.split_scratch ? c.split_capacity : 0);
+            int32_t* partial = tiles.splits > 1 ? c.split_scratch : nullptr;
+            const int splits = tiles.splits;
             launch_gemm_w8a8_mfma((const int8_t*)w.data, w.scales, w.bias, xq, xs, c.tokens, w.rows, K, c.y,
-                                  c.epilogue, c.acc_out, tile_m, splits, partial, stream);
+                                  c.epilogue, c.acc_out, tiles, partial, stream);
             if (partial) {
                 const bool vec = w.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(c.y) & 15) == 0 &&
                                  (reinterpret_cast<uintptr_t>(partial) & 15) == 0 &&

@@ -736,17 +736,26 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         {
             // KV bytes read: keys and values of every visible position, per query row.
             const double kv_bytes = 2.0 * 4.0 * c.kv_heads * dim * double(position + M) * (M == 1 ? 1 : 0.5 * M);
+            // Operations: q.k and p.v (2 flops each per dimension) over the keys
+            // each query row sees (position + t + 1, at most the window).
+            double visible = 0.0;
+            for (int t = 0; t < M; ++t) {
+                double keys = double(position) + t + 1;
+                if (c.sliding_window) keys = std::min(keys, double(c.sliding_window));
+                visible += keys;
+            }
+            const double attention_ops = 4.0 * c.heads * dim * visible;
             if (reference_) {
                 int keys = position_ptr ? int(capacity) : int(position) + M;
                 if (c.sliding_window) keys = std::min(keys, int(c.sliding_window));
                 check(keys <= reference_keys_, "reference-order attention: too many keys for one query",
                       LH_ERROR_UNSUPPORTED);
-                timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M, [&] {
+                timed(Profiler::Attention, kv_bytes, attention_ops, [&] {
                     check(launch_attention_reference_order(at, keys, s), "attention launch rejected",
                           LH_ERROR_UNSUPPORTED);
                 });
             } else {
-                timed(Profiler::Attention, kv_bytes, 4.0 * c.heads * dim * double(position + M) * M,
+                timed(Profiler::Attention, kv_bytes, attention_ops,
                       [&] { check(launch_attention(at, s), "attention launch rejected", LH_ERROR_UNSUPPORTED); });
             }
         }
