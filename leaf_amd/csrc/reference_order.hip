@@ -43,6 +43,39 @@ namespace {
 
 constexpr int kRoBlock = 256;
 
+// Sum of v[0..n) in index order, one rounding per addition (the CPU's
+// scalar loop).  Values are read 64 at a time into registers before they are
+// added: a read inside the dependent chain would add an LDS round trip to
+// every step.
+__device__ __forceinline__ float sequential_sum(const float* v, int n) {
+    float s = 0.0f;
+    int k = 0;
+    for (; k + 64 <= n; k += 64) {
+        float e[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s += e[j];
+    }
+    for (; k < n; ++k) s += v[k];
+    return s;
+}
+
+// The same in double (accurate_rms_square_sum, accurate_fp32.h:6-13).
+__device__ __forceinline__ double sequential_sum_f64(const float* v, int n) {
+    double s = 0.0;
+    int k = 0;
+    for (; k + 64 <= n; k += 64) {
+        float e[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s += (double)e[j];
+    }
+    for (; k < n; ++k) s += (double)v[k];
+    return s;
+}
+
 // ------------------------------------------------------------------ norm ---
 // One block per row.  The row is staged in LDS, every thread forms its
 // columns' squares (the same rounded products the CPU forms), and thread 0
@@ -61,11 +94,7 @@ __global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int w
     __syncthreads();
     float mean = 0.0f;
     if (norm.kind == 1) {
-        if (threadIdx.x == 0) {
-            float s = 0.0f;
-            for (int c = 0; c < width; ++c) s += row[c];
-            stat[0] = s / (float)width;
-        }
+        if (threadIdx.x == 0) stat[0] = sequential_sum(row, width) / (float)width;
         __syncthreads();
         mean = stat[0];
     }
@@ -76,23 +105,7 @@ __global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int w
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float square;
-        if (accurate) {
-            double total = 0.0;
-            for (int c = 0; c < width; ++c) total += (double)sq[c];
-            square = (float)total;
-        } else {
-            square = 0.0f;
-            int c = 0;
-            for (; c + 4 <= width; c += 4) {
-                const v4f s4 = *reinterpret_cast<const v4f*>(sq + c);
-                square += s4[0];
-                square += s4[1];
-                square += s4[2];
-                square += s4[3];
-            }
-            for (; c < width; ++c) square += sq[c];
-        }
+        const float square = accurate ? (float)sequential_sum_f64(sq, width) : sequential_sum(sq, width);
         stat[1] = 1.0f / sqrtf(square / (float)width + norm.epsilon);
     }
     __syncthreads();
@@ -151,12 +164,8 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
     }
     for (int k = threadIdx.x; k < n; k += blockDim.x) sc[k] = libm_expf(sc[k] - maximum);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        // masked keys add exp(-inf) = 0, which leaves the sum unchanged
-        float den = 0.0f;
-        for (int k = 0; k < n; ++k) den += sc[k];
-        den_shared = den;
-    }
+    // masked keys add exp(-inf) = 0, which leaves the sum unchanged
+    if (threadIdx.x == 0) den_shared = sequential_sum(sc, n);
     __syncthreads();
     const float den = den_shared;
     for (int k = threadIdx.x; k < n; k += blockDim.x) sc[k] = sc[k] / den;
@@ -178,6 +187,149 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
         for (; k < n; ++k) acc += sc[k] * vr[(size_t)k * dim];
         o[d] = acc;
     }
+}
+
+// Single-token attention at head dim 64 (decode): the same arithmetic as
+// ro_attention_kernel, arranged so that no dependent sum waits on memory.
+//   * Scores: thread k takes keys k, k + 256, ...; the next key's row loads
+//     into registers while the current one is summed (q . k in column order,
+//     q read from LDS).
+//   * Output: output[d] = (...(p_0 v_0[d]) + p_1 v_1[d]) + ...) in key order.
+//     The products are independent of the running sum, so all threads form
+//     them for a chunk of kRoChunk keys (coalesced V loads, one chunk ahead
+//     in registers) and write them to an LDS buffer; wave 0 then adds a
+//     chunk's products in key order (lane d, output element d) while the
+//     other threads fill the second buffer.
+constexpr int kRoChunk = 128;
+constexpr int kRoDecodeDim = 64;
+constexpr int kRoChunkF4 = kRoChunk * kRoDecodeDim / 4 / kRoBlock;   // float4 per thread per chunk
+
+__global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(AttentionCall p) {
+    constexpr int D = kRoDecodeDim;
+    extern __shared__ float lds[];
+    float* qs = lds;                          // [D]
+    float* prod = lds + D;                    // [2][kRoChunk][D] products p_k * v_k[d]
+    float* sc = prod + 2 * kRoChunk * D;      // [visible keys]: scores, then e, then p
+    __shared__ float red[kRoBlock / kWave];
+    __shared__ float den_shared;
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int position = p.position_ptr ? *p.position_ptr : p.position;
+    const int end = position + 1;
+    const int begin = (p.window && end > p.window) ? end - p.window : 0;
+    const int n = end - begin;
+    const int kvh = h / (p.heads / p.kv_heads);
+    const float* q = p.q_heads + (size_t)h * D;
+    const float* K = p.keys + ((size_t)kvh * p.capacity + begin) * D;
+    const float* V = p.values + ((size_t)kvh * p.capacity + begin) * D;
+    float* o = p.out + (size_t)h * D;
+    if (tid < D) qs[tid] = q[tid];
+    __syncthreads();
+
+    // ---- scores (q . k) * scale * scale and their maximum
+    float m = -INFINITY;
+    {
+        v4f cur[D / 4], nxt[D / 4];
+        auto load_row = [&](v4f (&dst)[D / 4], int k) {
+            const v4f* src = reinterpret_cast<const v4f*>(K + (size_t)k * D);
+#pragma unroll
+            for (int j = 0; j < D / 4; ++j) dst[j] = src[j];
+        };
+        if (tid < n) load_row(cur, tid);
+        for (int k = tid; k < n; k += kRoBlock) {
+            if (k + kRoBlock < n) load_row(nxt, k + kRoBlock);
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < D / 4; ++j) {
+                const v4f q4 = *reinterpret_cast<const v4f*>(qs + 4 * j);
+                s += q4[0] * cur[j][0];
+                s += q4[1] * cur[j][1];
+                s += q4[2] * cur[j][2];
+                s += q4[3] * cur[j][3];
+            }
+            s = s * p.scale * p.scale;
+            sc[k] = s;
+            m = m < s ? s : m;   // NaN never becomes the maximum (std::max)
+#pragma unroll
+            for (int j = 0; j < D / 4; ++j) cur[j] = nxt[j];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float other = __shfl_xor(m, off, kWave);
+        m = m < other ? other : m;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float maximum = red[0];
+    for (int w = 1; w < kRoBlock / kWave; ++w) maximum = maximum < red[w] ? red[w] : maximum;
+    if (!isfinite(maximum)) {
+        // fully masked (or infinite) row: the CPU leaves the zero-filled output
+        if (tid < D) o[tid] = 0.0f;
+        return;
+    }
+    // every thread exponentiates the scores it formed (no barrier needed)
+    for (int k = tid; k < n; k += kRoBlock) sc[k] = libm_expf(sc[k] - maximum);
+
+    // ---- V chunks: thread t holds float4 f = t + kRoBlock i of the chunk
+    // (key f / 16, columns 4 (f % 16) ..)
+    v4f vv[kRoChunkF4];
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kRoChunkF4; ++i) {
+            const int f = tid + kRoBlock * i, key = k0 + f / (D / 4);
+            vv[i] = key < n ? *reinterpret_cast<const v4f*>(V + (size_t)key * D + 4 * (f % (D / 4)))
+                            : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    auto store_products = [&](int k0, int buffer) {
+        float* dst = prod + buffer * kRoChunk * D;
+#pragma unroll
+        for (int i = 0; i < kRoChunkF4; ++i) {
+            const int f = tid + kRoBlock * i, key = f / (D / 4);
+            const float pk = k0 + key < n ? sc[k0 + key] : 0.0f;
+            v4f r;
+            r[0] = pk * vv[i][0];
+            r[1] = pk * vv[i][1];
+            r[2] = pk * vv[i][2];
+            r[3] = pk * vv[i][3];
+            *reinterpret_cast<v4f*>(dst + 4 * f) = r;
+        }
+    };
+    load_chunk(0);
+    __syncthreads();   // every e is written
+    // masked keys add exp(-inf) = 0, which leaves the sum unchanged
+    if (tid == 0) den_shared = sequential_sum(sc, n);
+    __syncthreads();
+    const float den = den_shared;
+    for (int k = tid; k < n; k += kRoBlock) sc[k] = sc[k] / den;
+    __syncthreads();   // every p is written
+    store_products(0, 0);
+    const int chunks = (n + kRoChunk - 1) / kRoChunk;
+    if (chunks > 1) load_chunk(kRoChunk);
+    float acc = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        __syncthreads();   // chunk c's products are in buffer c % 2
+        if (tid < D) {
+            // output[d] += p * v[d] in key order (16 products at a time into registers)
+            const float* pr = prod + (c & 1) * kRoChunk * D + tid;
+            const int rows = min(kRoChunk, n - c * kRoChunk);
+            int k = 0;
+            for (; k + 16 <= rows; k += 16) {
+                float t[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) t[j] = pr[(k + j) * D];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc += t[j];
+            }
+            for (; k < rows; ++k) acc += pr[k * D];
+        }
+        if (c + 1 < chunks) {
+            store_products((c + 1) * kRoChunk, (c + 1) & 1);
+            if (c + 2 < chunks) load_chunk((c + 2) * kRoChunk);
+        }
+    }
+    if (tid < D) o[tid] = acc;
 }
 
 // ------------------------------------------------------------ activation ---
@@ -348,15 +500,21 @@ __global__ __launch_bounds__(kRoBlock) void ro_gemm_kernel(WeightView w, const f
     }
 }
 
-// Dynamic LDS beyond the default 64 KiB must be allowed per kernel first.
+// Dynamic LDS beyond the default 64 KiB must be allowed per kernel first
+// (up to the 160 KiB of a CU less the kernel's static arrays); false when the
+// runtime refuses the size.
 template <typename K>
-void allow_lds(K kernel, size_t bytes, int& allowed) {
-    if (bytes <= 65536 || (int)bytes <= allowed) return;
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    allowed = 160 * 1024;
+bool allow_lds(K kernel, size_t bytes, int& allowed) {
+    if (bytes <= 65536 || (int)bytes <= allowed) return true;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    allowed = (int)bytes;
+    return true;
 }
-int g_norm_lds = 0, g_attention_lds = 0;
+int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0;
 
 }  // namespace
 
@@ -365,17 +523,25 @@ bool launch_norm_reference_order(const float* x, int rows, int width, const Norm
                                  hipStream_t stream, int rows_per_group, size_t group_stride) {
     if (width > kReferenceOrderMaxWidth) return false;
     const size_t lds = 2 * (size_t)width * sizeof(float);
-    allow_lds(ro_norm_kernel, lds, g_norm_lds);
+    if (!allow_lds(ro_norm_kernel, lds, g_norm_lds)) return false;
     ro_norm_kernel<<<rows, kRoBlock, lds, stream>>>(x, width, norm, y, rows_per_group, group_stride);
     return true;
 }
 
-int reference_order_attention_keys() { return (160 * 1024 - 4096) / 4 - 256; }
+// LDS of the decode kernel (the larger one): q, two product buffers, the
+// scores; 1 KiB stays for the static arrays.
+int reference_order_attention_keys() { return (160 * 1024 - 1024) / 4 - kRoDecodeDim - 2 * kRoChunk * kRoDecodeDim; }
 
 bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipStream_t stream) {
     if (max_keys > reference_order_attention_keys() || p.dim > 256) return false;
+    if (p.tokens == 1 && p.dim == kRoDecodeDim) {
+        const size_t lds = ((size_t)kRoDecodeDim + 2 * kRoChunk * kRoDecodeDim + max_keys) * sizeof(float);
+        if (!allow_lds(ro_attention_decode_kernel, lds, g_attention_decode_lds)) return false;
+        ro_attention_decode_kernel<<<p.heads, kRoBlock, lds, stream>>>(p);
+        return true;
+    }
     const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
-    allow_lds(ro_attention_kernel, lds, g_attention_lds);
+    if (!allow_lds(ro_attention_kernel, lds, g_attention_lds)) return false;
     dim3 grid(p.heads, p.tokens);
     ro_attention_kernel<<<grid, kRoBlock, lds, stream>>>(p);
     return true;
