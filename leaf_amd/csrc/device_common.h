@@ -97,4 +97,37 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// Sum of v[0..n) in index order, one rounding per addition (a CPU's scalar
+// loop).  Values are read 64 at a time into registers before they are
+// added: a read inside the dependent chain would add an LDS round trip to
+// every step.
+__device__ __forceinline__ float sequential_sum(const float* v, int n) {
+    float s = 0.0f;
+    int k = 0;
+    for (; k + 64 <= n; k += 64) {
+        float e[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s += e[j];
+    }
+    for (; k < n; ++k) s += v[k];
+    return s;
+}
+
+// The same in double (the accurate RMS square sum).
+__device__ __forceinline__ double sequential_sum_f64(const float* v, int n) {
+    double s = 0.0;
+    int k = 0;
+    for (; k + 64 <= n; k += 64) {
+        float e[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s += (double)e[j];
+    }
+    for (; k < n; ++k) s += (double)v[k];
+    return s;
+}
+
 }  // namespace leafhip

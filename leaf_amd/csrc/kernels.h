@@ -26,6 +26,7 @@ struct NormView {
     float epsilon = 0.0f;
     int kind = -1;                  // -1 none, 0 RMS, 1 LayerNorm
     int accurate = 0;               // RMS square sum in double (accurate_fp32.h:6-13)
+    int sequential = 0;             // mean and square sums in column order (decoder.cpp:706-727)
 };
 
 enum Epilogue : int {
@@ -70,6 +71,7 @@ struct PairEpilogue {
     float* values = nullptr;
     int width = 0, activation = 0;
     float* act = nullptr;
+    int reference = 0;              // gated: SiLU with the CPU's libm expf (libm_expf.h)
 };
 
 // y[t, row] for t < tokens.  integer_activations selects W8A8/W4A8 (bits 8/4):

@@ -12,6 +12,7 @@
 // MFMA (int8 for W8A8, f32 otherwise).
 #include "device_common.h"
 #include "kernels.h"
+#include "libm_expf.h"
 
 #include <math.h>
 
@@ -328,9 +329,13 @@ struct RowSlice {
 
 // Normalize (optionally) and quantize the row into lds_q; returns the
 // per-token activation scale (decoder.cpp:706-727, 1028-1043).
+//
+// With `seq` (a K-float LDS buffer) and norm.sequential, the mean and square
+// sums are those of the CPU's norm(): every thread writes its columns' terms
+// to seq and one lane adds them in column order.
 template <int V>
 __device__ float block_norm_quantize(RowSlice<V>& r, int K, const NormView& norm, int8_t* lds_q, float* red,
-                                     double* dred) {
+                                     double* dred, float* seq = nullptr) {
     const int tid = threadIdx.x;
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 v[V];
@@ -340,7 +345,40 @@ __device__ float block_norm_quantize(RowSlice<V>& r, int K, const NormView& norm
         in[i] = 4 * (tid + kBlock * i) < K;
         v[i] = in[i] ? r.x[i] : zero;
     }
-    if (norm.kind >= 0) {
+    if (norm.kind >= 0 && seq && norm.sequential) {
+        // terms into seq, one lane's sum in column order, broadcast through red
+        auto column_sum = [&](auto term, bool in_double) {
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+                if (in[i]) *(float4*)(seq + 4 * (tid + kBlock * i)) = term(v[i]);
+            __syncthreads();
+            if (tid == 0) red[0] = in_double ? (float)sequential_sum_f64(seq, K) : sequential_sum(seq, K);
+            __syncthreads();
+            const float total = red[0];
+            __syncthreads();   // seq and red are free again
+            return total;
+        };
+        float mean = 0.0f;
+        if (norm.kind == 1) mean = column_sum([](float4 x) { return x; }, false) / (float)K;
+        const bool accurate = norm.kind == 0 && norm.accurate;
+        const float square = column_sum(
+            [&](float4 x) {
+                if (!accurate) x = make_float4(x.x - mean, x.y - mean, x.z - mean, x.w - mean);
+                return make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
+            },
+            accurate);
+        const float scale = 1.0f / sqrtf(square / (float)K + norm.epsilon);
+        const bool use_beta = norm.beta != nullptr;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const float4 g = r.g[i], b = use_beta ? r.b[i] : zero;
+            v[i].x = (v[i].x - mean) * scale * g.x + b.x;
+            v[i].y = (v[i].y - mean) * scale * g.y + b.y;
+            v[i].z = (v[i].z - mean) * scale * g.z + b.z;
+            v[i].w = (v[i].w - mean) * scale * g.w + b.w;
+            if (!in[i]) v[i] = zero;
+        }
+    } else if (norm.kind >= 0) {
         float mean = 0.0f;
         if (norm.kind == 1) {
             float s = 0.0f;
@@ -444,10 +482,16 @@ __device__ __forceinline__ float activate_value(int activation, float x) {
     return x < 0.0f ? 0.0f : x;
 }
 
+// The activation with the CPU's libm expf in the SiLU (bit-equal to the CPU's).
+__device__ __forceinline__ float activate_value_reference(int activation, float x) {
+    if (activation == 0) return x / (1.0f + libm_expf(-x));
+    return activate_value(activation, x);
+}
+
 // Final values (bias included) of rows r0 and r1 of a paired epilogue.
 __device__ __forceinline__ void pair_store(const PairEpilogue& e, int r0, float v0, int r1, float v1) {
     if (e.mode == kPairGated) {
-        e.act[r0] = v1 * activate_value(e.activation, v0);
+        e.act[r0] = v1 * (e.reference ? activate_value_reference(e.activation, v0) : activate_value(e.activation, v0));
         return;
     }
     const int position = e.position_ptr ? *e.position_ptr : e.position;
@@ -467,13 +511,15 @@ __device__ __forceinline__ void pair_store(const PairEpilogue& e, int r0, float 
     }
 }
 
-template <int BITS, int RPW, int MAXJ, int EPI>
+template <int BITS, int RPW, int MAXJ, int EPI, bool SEQ = false>
 __global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, const float* __restrict__ x, NormView norm,
                                                                float* __restrict__ y, int epilogue,
                                                                int32_t* __restrict__ acc_out, PairEpilogue pe) {
     static_assert(EPI == kPairNone || RPW == 2, "paired epilogues compute two rows per wave");
     constexpr int E = BITS == 8 ? 16 : 32;          // weight values per 16-byte chunk
     __shared__ __align__(16) int8_t lds_q[kFusedMaxK];
+    // the row's terms for sequential sums (K <= MAXJ * 64 * E columns)
+    __shared__ __align__(16) float lds_seq[SEQ ? (MAXJ * kWave * E < kFusedMaxK ? MAXJ * kWave * E : kFusedMaxK) : 4];
     __shared__ float red[16];
     __shared__ double dred[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -518,7 +564,7 @@ __global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, co
     __builtin_amdgcn_sched_barrier(0);
     // Chunks past the row end carry zero activations (below), so the clamped
     // duplicate weights they loaded add nothing.
-    const float sx = block_norm_quantize<V>(slice, K, norm, lds_q, red, dred);
+    const float sx = block_norm_quantize<V>(slice, K, norm, lds_q, red, dred, SEQ ? lds_seq : nullptr);
     if (row_first >= w.rows) return;
     uint32_t xq[MAXJ][E / 4];
 #pragma unroll
@@ -1564,16 +1610,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
 
 int ceil_div(size_t a, size_t b) { return (int)((a + b - 1) / b); }
 
-template <int BITS, int RPW, int EPI>
-void launch_fused_int_rpw(const LinearCall& c, int jn, hipStream_t stream) {
+template <int BITS, int RPW, int EPI, bool SEQ>
+void launch_fused_int_seq(const LinearCall& c, int jn, hipStream_t stream) {
     const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
-#define LEAF_FUSED(J) gemv_int_fused_kernel<BITS, RPW, J, EPI><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, \
-        c.epilogue, c.acc_out, c.pair)
+#define LEAF_FUSED(J) gemv_int_fused_kernel<BITS, RPW, J, EPI, SEQ><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, \
+        c.y, c.epilogue, c.acc_out, c.pair)
     if (jn <= 1) LEAF_FUSED(1);
     else if (jn <= 2) LEAF_FUSED(2);
     else if (jn <= 4) LEAF_FUSED(4);
     else LEAF_FUSED(6);
 #undef LEAF_FUSED
+}
+
+template <int BITS, int RPW, int EPI>
+void launch_fused_int_rpw(const LinearCall& c, int jn, hipStream_t stream) {
+    if (c.norm.kind >= 0 && c.norm.sequential) launch_fused_int_seq<BITS, RPW, EPI, true>(c, jn, stream);
+    else launch_fused_int_seq<BITS, RPW, EPI, false>(c, jn, stream);
 }
 
 template <int BITS>
@@ -1696,7 +1748,11 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         const bool fusable = linear_fuses(c);
         if (!fusable) {
             if (!c.norm_scratch || !c.x) return -1;
-            launch_norm(c.x, c.tokens, w.cols, c.norm, c.norm_scratch, stream);
+            if (c.norm.sequential) {
+                if (!launch_norm_reference_order(c.x, c.tokens, w.cols, c.norm, c.norm_scratch, stream)) return -1;
+            } else {
+                launch_norm(c.x, c.tokens, w.cols, c.norm, c.norm_scratch, stream);
+            }
             c.x = c.norm_scratch;
             c.norm = NormView();
         }

@@ -43,39 +43,6 @@ namespace {
 
 constexpr int kRoBlock = 256;
 
-// Sum of v[0..n) in index order, one rounding per addition (the CPU's
-// scalar loop).  Values are read 64 at a time into registers before they are
-// added: a read inside the dependent chain would add an LDS round trip to
-// every step.
-__device__ __forceinline__ float sequential_sum(const float* v, int n) {
-    float s = 0.0f;
-    int k = 0;
-    for (; k + 64 <= n; k += 64) {
-        float e[64];
-#pragma unroll
-        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
-#pragma unroll
-        for (int j = 0; j < 64; ++j) s += e[j];
-    }
-    for (; k < n; ++k) s += v[k];
-    return s;
-}
-
-// The same in double (accurate_rms_square_sum, accurate_fp32.h:6-13).
-__device__ __forceinline__ double sequential_sum_f64(const float* v, int n) {
-    double s = 0.0;
-    int k = 0;
-    for (; k + 64 <= n; k += 64) {
-        float e[64];
-#pragma unroll
-        for (int j = 0; j < 64; ++j) e[j] = v[k + j];
-#pragma unroll
-        for (int j = 0; j < 64; ++j) s += (double)e[j];
-    }
-    for (; k < n; ++k) s += (double)v[k];
-    return s;
-}
-
 // ------------------------------------------------------------------ norm ---
 // One block per row.  The row is staged in LDS, every thread forms its
 // columns' squares (the same rounded products the CPU forms), and thread 0

@@ -651,8 +651,11 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* qkv = qkv_.as<float>();
         float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
         float* values = keys + plane;
-        const bool fuse_in = !reference_ && M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv &&
-                             !L.qkv.input_scale;
+        const bool fuse_in = M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv && !L.qkv.input_scale;
+        // In reference order the fused GEMV sums the norm in column order
+        // (and the RoPE pair epilogue is the rope kernel's arithmetic).
+        NormView input_norm = L.input_norm;
+        input_norm.sequential = reference_ ? 1 : 0;
         // Single-token W8A8: one launch normalizes, quantizes, projects q|k|v,
         // rotates and appends k, v to the cache.
         PairEpilogue rope;
@@ -663,12 +666,12 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         rope.q_heads = q_heads_.as<float>(); rope.keys = keys; rope.values = values;
         rope.position_ptr = position_ptr;
         const bool fuse_rope = fuse_in && !c.qk_norm && dim % 2 == 0 &&
-                               linear_fuses([&] { LinearCall t = make_call(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
+                               linear_fuses([&] { LinearCall t = make_call(L.qkv, hidden, M, qkv, kStore, &input_norm);
                                                   t.pair = rope; return t; }());
         if (fuse_rope) {
-            run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm, &rope);
+            run_linear(L.qkv, hidden, M, qkv, kStore, &input_norm, &rope);
         } else if (fuse_in) {
-            run_linear(L.qkv, hidden, M, qkv, kStore, &L.input_norm);
+            run_linear(L.qkv, hidden, M, qkv, kStore, &input_norm);
         } else if (L.stacked_qkv && prequantizes(L.qkv, M)) {
             // norm + per-token quantization in one launch, then the GEMM
             timed(Profiler::Other, 0, 0, [&] {
@@ -772,21 +775,24 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* act = act_.as<float>();
         const int f = int(c.intermediate);
         if (c.gated) {
-            const bool fuse_post = !reference_ && rows == 1 && model.integer_linear(L.gate_up) &&
-                                   L.stacked_gate_up && !L.gate_up.input_scale;
+            const bool fuse_post = rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up &&
+                                   !L.gate_up.input_scale;
+            NormView post_norm = L.post_norm;
+            post_norm.sequential = reference_ ? 1 : 0;
             PairEpilogue gated;
             gated.mode = kPairGated;
             gated.width = f;
             gated.activation = int(c.activation);
             gated.act = act;
+            gated.reference = reference_ ? 1 : 0;
             const bool fuse_act = fuse_post &&
                                   linear_fuses([&] { LinearCall t = make_call(L.gate_up, hid, rows, gate_up, kStore,
-                                                                              &L.post_norm);
+                                                                              &post_norm);
                                                      t.pair = gated; return t; }());
             if (fuse_act) {
-                run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm, &gated);
+                run_linear(L.gate_up, hid, rows, gate_up, kStore, &post_norm, &gated);
             } else if (fuse_post) {
-                run_linear(L.gate_up, hid, rows, gate_up, kStore, &L.post_norm);
+                run_linear(L.gate_up, hid, rows, gate_up, kStore, &post_norm);
             } else if (L.stacked_gate_up && prequantizes(L.gate_up, rows)) {
                 timed(Profiler::Other, 0, 0, [&] {
                     launch_norm_quantize(hid, rows, h, L.post_norm, xq_.as<int8_t>(), xs_.as<float>(), s);
