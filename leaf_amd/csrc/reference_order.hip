@@ -162,14 +162,17 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 //     into registers while the current one is summed (q . k in column order,
 //     q read from LDS).
 //   * Output: output[d] = (...(p_0 v_0[d]) + p_1 v_1[d]) + ...) in key order.
-//     The products are independent of the running sum, so all threads form
-//     them for a chunk of kRoChunk keys (coalesced V loads, one chunk ahead
-//     in registers) and write them to an LDS buffer; wave 0 then adds a
+//     The products are independent of the running sum.  The V rows of up to
+//     kRoRound keys are loaded into registers (all threads, coalesced) while
+//     the exponentials and the denominator are formed; then, chunk by chunk,
+//     all threads write p_k * v_k[d] into an LDS buffer and wave 0 adds a
 //     chunk's products in key order (lane d, output element d) while the
 //     other threads fill the second buffer.
-constexpr int kRoChunk = 128;
+constexpr int kRoChunk = 128;                                          // keys per product buffer
 constexpr int kRoDecodeDim = 64;
-constexpr int kRoChunkF4 = kRoChunk * kRoDecodeDim / 4 / kRoBlock;   // float4 per thread per chunk
+constexpr int kRoChunkF4 = kRoChunk * kRoDecodeDim / 4 / kRoBlock;    // float4 per thread per chunk (8)
+constexpr int kRoRoundChunks = 5;
+constexpr int kRoRound = kRoChunk * kRoRoundChunks;                    // keys whose V rows sit in registers
 
 __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(AttentionCall p) {
     constexpr int D = kRoDecodeDim;
@@ -235,65 +238,65 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
         if (tid < D) o[tid] = 0.0f;
         return;
     }
-    // every thread exponentiates the scores it formed (no barrier needed)
-    for (int k = tid; k < n; k += kRoBlock) sc[k] = libm_expf(sc[k] - maximum);
 
-    // ---- V chunks: thread t holds float4 f = t + kRoBlock i of the chunk
-    // (key f / 16, columns 4 (f % 16) ..)
-    v4f vv[kRoChunkF4];
-    auto load_chunk = [&](int k0) {
+    // ---- V rows of a round: thread t holds float4 f = t + kRoBlock i (key
+    // r0 + f / 16, columns 4 (f % 16) ..); chunk c of the round is
+    // vv[kRoChunkF4 c .. kRoChunkF4 (c + 1))
+    v4f vv[kRoRoundChunks * kRoChunkF4];
+    auto load_round = [&](int r0) {
 #pragma unroll
-        for (int i = 0; i < kRoChunkF4; ++i) {
-            const int f = tid + kRoBlock * i, key = k0 + f / (D / 4);
+        for (int i = 0; i < kRoRoundChunks * kRoChunkF4; ++i) {
+            const int f = tid + kRoBlock * i, key = r0 + f / (D / 4);
             vv[i] = key < n ? *reinterpret_cast<const v4f*>(V + (size_t)key * D + 4 * (f % (D / 4)))
                             : v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
-    auto store_products = [&](int k0, int buffer) {
-        float* dst = prod + buffer * kRoChunk * D;
-#pragma unroll
-        for (int i = 0; i < kRoChunkF4; ++i) {
-            const int f = tid + kRoBlock * i, key = f / (D / 4);
-            const float pk = k0 + key < n ? sc[k0 + key] : 0.0f;
-            v4f r;
-            r[0] = pk * vv[i][0];
-            r[1] = pk * vv[i][1];
-            r[2] = pk * vv[i][2];
-            r[3] = pk * vv[i][3];
-            *reinterpret_cast<v4f*>(dst + 4 * f) = r;
-        }
-    };
-    load_chunk(0);
+    load_round(0);   // lands while the exponentials and the denominator are formed
+    // every thread exponentiates the scores it formed
+    for (int k = tid; k < n; k += kRoBlock) sc[k] = libm_expf(sc[k] - maximum);
     __syncthreads();   // every e is written
     // masked keys add exp(-inf) = 0, which leaves the sum unchanged
     if (tid == 0) den_shared = sequential_sum(sc, n);
     __syncthreads();
     const float den = den_shared;
     for (int k = tid; k < n; k += kRoBlock) sc[k] = sc[k] / den;
-    __syncthreads();   // every p is written
-    store_products(0, 0);
-    const int chunks = (n + kRoChunk - 1) / kRoChunk;
-    if (chunks > 1) load_chunk(kRoChunk);
+
     float acc = 0.0f;
-    for (int c = 0; c < chunks; ++c) {
-        __syncthreads();   // chunk c's products are in buffer c % 2
-        if (tid < D) {
-            // output[d] += p * v[d] in key order (16 products at a time into registers)
-            const float* pr = prod + (c & 1) * kRoChunk * D + tid;
-            const int rows = min(kRoChunk, n - c * kRoChunk);
-            int k = 0;
-            for (; k + 16 <= rows; k += 16) {
-                float t[16];
+    for (int r0 = 0; r0 < n; r0 += kRoRound) {
+        if (r0 > 0) load_round(r0);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) t[j] = pr[(k + j) * D];
+        for (int c = 0; c < kRoRoundChunks; ++c) {
+            const int k0 = r0 + c * kRoChunk;
+            if (k0 >= n) break;
+            __syncthreads();   // wave 0 is done with this buffer (and, first time, every p is written)
+            float* dst = prod + (c & 1) * kRoChunk * D;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) acc += t[j];
+            for (int i = 0; i < kRoChunkF4; ++i) {
+                const int f = tid + kRoBlock * i, key = k0 + f / (D / 4);
+                const float pk = key < n ? sc[key] : 0.0f;
+                const v4f v = vv[kRoChunkF4 * c + i];
+                v4f r;
+                r[0] = pk * v[0];
+                r[1] = pk * v[1];
+                r[2] = pk * v[2];
+                r[3] = pk * v[3];
+                *reinterpret_cast<v4f*>(dst + 4 * f) = r;
             }
-            for (; k < rows; ++k) acc += pr[k * D];
-        }
-        if (c + 1 < chunks) {
-            store_products((c + 1) * kRoChunk, (c + 1) & 1);
-            if (c + 2 < chunks) load_chunk((c + 2) * kRoChunk);
+            __syncthreads();   // the chunk's products are written
+            if (tid < D) {
+                // output[d] += p * v[d] in key order (16 products at a time into registers)
+                const float* pr = dst + tid;
+                const int rows = min(kRoChunk, n - k0);
+                int k = 0;
+                for (; k + 16 <= rows; k += 16) {
+                    float t[16];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) t[j] = pr[(k + j) * D];
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc += t[j];
+                }
+                for (; k < rows; ++k) acc += pr[k * D];
+            }
         }
     }
     if (tid < D) o[tid] = acc;
