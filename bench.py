@@ -25,7 +25,9 @@ Beside it:
   peaks         measured streaming bandwidth (leaf_amd/bin/hbm_copy, 1 GiB) and
                 MFMA rates (leaf_amd/bin/mfma_peak) beside the datasheet;
   gemv          standalone W8A8 GEMV at the TinyLlama shapes (M = 1), rotating
-                >= 1 GiB of weight copies so the 256 MiB MALL cannot serve them;
+                >= 1 GiB of weight copies so the 256 MiB MALL cannot serve them,
+                graph-replayed; and one launch over about 1 GiB of rows per
+                weight format (W8A8, FP32, BF16, INT4 g32): the streaming rate;
   linear_w8a8   the same shapes at M = 4, 16, 128 and 512 tokens (the prefill
                 GEMM at 512): us per call, int8 TOPS against the 5.0 POPS peak;
   configs       the other benchmark configurations at their configured sizes
@@ -250,6 +252,42 @@ def gemv_microbench(repeats: int = 20) -> dict:
         for w in s:
             del w
     return results
+
+
+def gemv_streaming(repeats: int = 5) -> dict:
+    """One M = 1 GEMV launch over about 1 GiB of weight rows per weight format
+    (K = 2048): the kernels' own streaming rate, free of the per-launch
+    latency that dominates the 0.5-12 MB matrices of a decoder layer.  Bytes
+    per launch: N*K*bits/8 + 4*N*K/group (scales) + activations + outputs."""
+    from leaf_amd import runtime
+    rng = np.random.default_rng(SEED + 4)
+    K = 2048
+    out = {}
+    # (name, weight bits, activation bits, rows, group)
+    formats = [("w8a8", 8, 8, 1 << 19, K), ("fp32", 32, 32, 1 << 17, 0), ("bf16", 16, 32, 1 << 18, 0),
+               ("int4_g32", 4, 32, 1 << 19, 32)]
+    for name, bits, act_bits, N, group in formats:
+        row_bytes = K * bits // 8
+        tile = rng.integers(0, 256, (256, row_bytes), dtype=np.uint8)
+        if bits == 32:
+            tile = (0.02 * rng.standard_normal((256, K))).astype(np.float32).view(np.uint8)
+        elif bits == 16:
+            tile = ((0.02 * rng.standard_normal((256, K))).astype(np.float32).view(np.uint32) >> 16).astype(
+                np.uint16).view(np.uint8)
+        data = np.resize(tile, (N, row_bytes))
+        scales = None
+        if bits in (8, 4):
+            scales = (rng.random((N, K // group), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+        w = runtime.DeviceWeight(data, bits, K, scales, group)
+        del data
+        x = runtime.DeviceArray.of(rng.standard_normal((1, K), dtype=np.float32))
+        y = runtime.DeviceArray((1, N), np.float32)
+        us = _replayed_us([lambda st: runtime.linear(w, x, 1, act_bits, y, stream=st)], repeats)
+        nbytes = N * row_bytes + (4 * N * (K // group) if group else 0) + 4 * K + 4 * N
+        out[name] = {"rows": N, "bytes": nbytes, "us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
+        del w
+    return out
 
 
 def linear_microbench(tokens=(4, 16, 128, 512), repeats: int = 3) -> dict:
@@ -545,6 +583,8 @@ def main() -> int:
     if not args.no_gemv:
         log("GEMV microbenchmark ...")
         gemv = gemv_microbench()
+        log("GEMV streaming rate ...")
+        gemv["streaming_1GiB"] = gemv_streaming()
     linear = None
     if not args.no_linear:
         log("W8A8 linear microbenchmark ...")

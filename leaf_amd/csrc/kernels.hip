@@ -708,6 +708,16 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
                 for (int t = 0; t < T; ++t)
 #pragma unroll
                     for (int e = 0; e < E; ++e) acc[r][t] = fmaf(wf[e], xv[t][e], acc[r][t]);
+            } else if (piece == E) {
+                // one scale group covers the chunk: unrolled, the same sums
+                const float s = w.scales[(size_t)row * groups + (c * E) / w.group];
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    float part = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) part = fmaf(wf[e], xv[t][e], part);
+                    acc[r][t] = fmaf(part, s, acc[r][t]);
+                }
             } else {
                 for (int p0 = 0; p0 < E; p0 += piece) {
                     const float s = w.scales[(size_t)row * groups + (c * E + p0) / w.group];
@@ -1661,9 +1671,14 @@ void launch_gemv_int(const LinearCall& c, const int8_t* xq, const float* xs, hip
 
 template <int BITS, int T>
 void launch_gemv_fp_t(const LinearCall& c, hipStream_t stream) {
-    constexpr int RPW = 2;
-    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
-    gemv_fp_kernel<BITS, T, RPW><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.y, c.epilogue);
+    // A wave reads the whole activation row from L1 / L2 for its rows: int4 /
+    // int8 rows are 4-8x shorter in bytes than the row they multiply, so a
+    // wave takes four of them when the grid still covers the CUs.
+    constexpr int RPW = (BITS <= 8) ? 4 : 2;
+    const int rpw = (RPW == 4 && c.w.rows < 4 * 4096) ? 2 : RPW;
+    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * rpw);
+    if (rpw == 4) gemv_fp_kernel<BITS, T, 4><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.y, c.epilogue);
+    else gemv_fp_kernel<BITS, T, 2><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.y, c.epilogue);
 }
 
 template <int BITS>
