@@ -694,14 +694,19 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
         for (int r = 0; r < RPW; ++r) {
             const int row = min(row_first + r, w.rows - 1);
             const uint4 wv = load_stream16((const uint4*)(base + (size_t)row * row_bytes) + c);
-            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+            // int4: flipping each nibble's sign bit (xor 8) gives u = value + 8 in
+            // 0..15; the float with bits 0x4B000000 | u is 2^23 + u exactly, so
+            // subtracting 2^23 + 8 leaves the signed value, exactly
+            const uint32_t words[4] = {BITS == 4 ? wv.x ^ 0x88888888u : wv.x, BITS == 4 ? wv.y ^ 0x88888888u : wv.y,
+                                       BITS == 4 ? wv.z ^ 0x88888888u : wv.z, BITS == 4 ? wv.w ^ 0x88888888u : wv.w};
             float wf[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 if constexpr (BITS == 32) wf[e] = __uint_as_float(words[e]);
                 else if constexpr (BITS == 16) wf[e] = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
                 else if constexpr (BITS == 8) wf[e] = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
-                else wf[e] = (float)nibble((words[e / 8] >> (8 * ((e / 2) & 3))) & 0xFFu, e & 1);
+                else  // nibble e: bits 4 (e % 8) of word e / 8 (low nibble = even column)
+                    wf[e] = __uint_as_float(0x4B000000u | ((words[e / 8] >> (4 * (e & 7))) & 0xFu)) - 8388616.0f;
             }
             if constexpr (BITS == 32 || BITS == 16) {
 #pragma unroll
