@@ -111,9 +111,13 @@ def test_w8a8_prefill_gemm_512_tokens_bit_exact(rt, oracle):
     assert bits_equal(y, oracle.linear_int(8, N, K, K, wq, ws, None, x))
 
 
-@pytest.mark.parametrize("M,K,N", [(300, 5632, 200), (130, 2048, 2560), (512, 2048, 1408), (17, 768, 129)])
+@pytest.mark.parametrize("M,K,N", [(300, 5632, 200), (130, 2048, 2560), (512, 2048, 1408), (17, 768, 129),
+                                   (300, 256, 16448), (512, 2048, 11264)])
 def test_w8a8_tiled_gemm_edges_bit_exact(rt, oracle, M, K, N):
-    # 128 x 128 tiles cut by the token and row counts; K from 768 to 5632
+    # Tiles cut by the token and row counts, K from 256 to 5632: 64 x 64 tiles
+    # (with split K for the short inputs), and 128 rows x 256 tokens for the
+    # large outputs (16448 rows: 129 row tiles, the last one partial; 11264:
+    # the stacked gate|up projection of a 512-token TinyLlama prefill)
     rng = np.random.default_rng(M * 31 + N)
     w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
     wq, ws = quantize(w, 8, K)
