@@ -523,6 +523,139 @@ def derive_traffic(base: Path, kernel: str = "decode_step_kernel") -> dict:
     return out
 
 
+def _db_counters(db: Path) -> list:
+    """Per-dispatch counter values of a rocprofv3 --pmc run (rocpd SQLite output),
+    in dispatch order: [(kernel name, blocks, {counter: value})]."""
+    import sqlite3
+    con = sqlite3.connect(str(db))
+    rows = con.execute("select dispatch_id, kernel_name, grid_size, workgroup_size, counter_name, value "
+                       "from counters_collection order by dispatch_id").fetchall()
+    con.close()
+    out: dict = {}
+    for dispatch, name, grid, group, counter, value in rows:
+        entry = out.setdefault(dispatch, (name, grid // max(group, 1), {}))
+        entry[2][counter] = entry[2].get(counter, 0.0) + value
+    return [out[k] for k in sorted(out)]
+
+
+# The four W8A8 GEMMs of a TinyLlama prefill layer, in launch order, at 512
+# tokens: (name, rows, K).
+PREFILL_GEMMS = (("qkv", 2560, 2048), ("o", 2048, 2048), ("gate_up", 11264, 2048), ("down", 2048, 5632))
+
+
+def derive_prefill_counters(base: Path) -> dict:
+    """MFMA utilisation and HBM bytes per prefill GEMM shape from rocprofv3 --pmc
+    runs under `base` (each a directory holding one *_results.db):
+      mfma/      SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE of the bench
+                 (decode + prefills, no microbenchmarks)
+      fetch/ write/        FETCH_SIZE / WRITE_SIZE of the same run
+      peak/      the same three counters over leaf_amd/bin/mfma_peak (the MFMA issue loop)
+      copy_fetch/ copy_write/   FETCH_SIZE / WRITE_SIZE over leaf_amd/bin/hbm_copy 1024
+    MFMA busy fractions are scaled so that the int8 32x32x32 issue loop reads
+    its measured share of the datasheet rate."""
+    def db(name):
+        return next((base / name).glob("*.db"))
+
+    def gemms(entries):
+        # Label the prefill GEMM dispatches: q|k|v runs 320 blocks of 64 x 64
+        # tiles, gate|up 128 x 256 tiles; o and down both run 256 blocks and
+        # follow q|k|v and gate|up respectively (the last layer, trimmed to
+        # one row, runs only its q|k|v as a GEMM).
+        out, previous = [], None
+        for name, blocks, values in entries:
+            if "gemm_w8a8_mfma_kernel" not in name:
+                continue
+            if "<2, 4, 3>" in name:
+                label = "gate_up"
+            elif blocks == 320:
+                label = "qkv"
+            elif blocks == 256 and previous in ("qkv", "gate_up"):
+                label = "o" if previous == "qkv" else "down"
+            else:
+                previous = None
+                continue
+            out.append((label, values))
+            previous = label
+        return out
+
+    peak = [v for name, _, v in _db_counters(db("peak")) if "mfma_i8_32" in name]
+    peak_busy = max(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["GRBM_GUI_ACTIVE"] for v in peak)
+    peak_cu = max(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["SQ_BUSY_CU_CYCLES"] for v in peak)
+    copy = {}
+    for counter, sub in (("FETCH_SIZE", "copy_fetch"), ("WRITE_SIZE", "copy_write")):
+        vals = [v[counter] for name, _, v in _db_counters(db(sub)) if "hbm_copy_kernel" in name]
+        copy[counter] = COPY_BYTES / (sum(vals) / len(vals))
+    table = {}
+    for label, values in gemms(_db_counters(db("mfma"))):
+        t = table.setdefault(label, {"mfma": [], "cu": [], "fetch": [], "write": []})
+        t["mfma"].append(values["SQ_VALU_MFMA_BUSY_CYCLES"] / values["GRBM_GUI_ACTIVE"] / peak_busy)
+        t["cu"].append(values["SQ_VALU_MFMA_BUSY_CYCLES"] / values["SQ_BUSY_CU_CYCLES"] / peak_cu)
+    for counter, sub, key in (("FETCH_SIZE", "fetch", "fetch"), ("WRITE_SIZE", "write", "write")):
+        for label, values in gemms(_db_counters(db(sub))):
+            table[label][key].append(values[counter] * copy[counter])
+    out = {"peak_reference": "leaf_amd/bin/mfma_peak v_mfma_i32_32x32x32_i8 loop", "shapes": {}}
+    for name, rows, K in PREFILL_GEMMS:
+        t = table[name]
+        mean = lambda v: sum(v) / len(v)   # noqa: E731
+        out["shapes"][name] = {
+            "M": 512, "N": rows, "K": K, "dispatches": len(t["mfma"]),
+            "mfma_busy_of_peak_loop_wall": round(mean(t["mfma"]), 4),
+            "mfma_busy_of_peak_loop_cu_busy": round(mean(t["cu"]), 4),
+            "fetch_bytes": round(mean(t["fetch"])), "write_bytes": round(mean(t["write"])),
+            # weights, row scales and biases, int8 activations and their scales; f32 outputs
+            "algorithmic_read_bytes": rows * K + 8 * rows + 512 * K + 4 * 512,
+            "algorithmic_write_bytes": 4 * 512 * rows}
+    return out
+
+
+def summarize_trace(db: Path, top: int = 25) -> str:
+    """Markdown tables from a rocprofv3 --kernel-trace run (rocpd SQLite output):
+    the top kernels by total time, and the prefill W8A8 GEMMs by shape (labelled
+    as in derive_prefill_counters) with int8 TOPS against the datasheet peak."""
+    import re
+    import sqlite3
+    con = sqlite3.connect(str(db))
+    rows = con.execute("select name, grid_x / workgroup_x, duration from kernels order by start").fetchall()
+    con.close()
+    clean = lambda n: re.sub(r"leafhip::|\(anonymous namespace\)::", "", n).split("(")[0]   # noqa: E731
+    totals: dict = {}
+    for name, blocks, duration in rows:
+        t = totals.setdefault(clean(name), [0, 0.0])
+        t[0] += 1
+        t[1] += duration
+    all_ns = sum(t[1] for t in totals.values())
+    lines = ["| Kernel | Calls | Total ms | Average us | % of kernel time |", "|---|---:|---:|---:|---:|"]
+    for name, (calls, ns) in sorted(totals.items(), key=lambda kv: -kv[1][1])[:top]:
+        lines.append(f"| `{name}` | {calls} | {ns / 1e6:.2f} | {ns / calls / 1e3:.2f} | {100 * ns / all_ns:.1f} |")
+    shapes = {g[0]: (g[1], g[2]) for g in PREFILL_GEMMS}
+    times: dict = {}
+    previous = None
+    for name, blocks, duration in rows:
+        if "gemm_w8a8_mfma_kernel" not in name:
+            continue
+        if "<2, 4, 3>" in name:
+            label = "gate_up"
+        elif blocks == 320:
+            label = "qkv"
+        elif blocks == 256 and previous in ("qkv", "gate_up"):
+            label = "o" if previous == "qkv" else "down"
+        else:
+            previous = None
+            continue
+        times.setdefault(label, []).append(duration)
+        previous = label
+    lines += ["", "| Prefill GEMM (512 tokens) | N x K | Dispatches | Average us | int8 TOPS | of 5.0 POPS |",
+              "|---|---|---:|---:|---:|---:|"]
+    for label, (rows_n, K) in shapes.items():
+        d = times.get(label)
+        if not d:
+            continue
+        us = sum(d) / len(d) / 1e3
+        tops = 2.0 * 512 * rows_n * K / us / 1e6
+        lines.append(f"| {label} | {rows_n} x {K} | {len(d)} | {us:.2f} | {tops:.0f} | {tops / INT8_PEAK_TOPS:.3f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -535,7 +668,15 @@ def main() -> int:
     parser.add_argument("--no-peaks", action="store_true")
     parser.add_argument("--no-reference-numerics", action="store_true")
     parser.add_argument("--derive-traffic", type=Path, default=None)
+    parser.add_argument("--derive-prefill-counters", type=Path, default=None)
+    parser.add_argument("--summarize-trace", type=Path, default=None)
     args = parser.parse_args()
+    if args.summarize_trace is not None:
+        print(summarize_trace(args.summarize_trace))
+        return 0
+    if args.derive_prefill_counters is not None:
+        print(json.dumps(derive_prefill_counters(args.derive_prefill_counters), indent=1))
+        return 0
     if args.derive_traffic is not None:
         traffic = derive_traffic(args.derive_traffic)
         TRAFFIC_FILE.write_text(json.dumps(traffic, indent=1) + "\n")
