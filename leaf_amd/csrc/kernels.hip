@@ -327,19 +327,18 @@ struct RowSlice {
     }
 };
 
-// Normalize (optionally) and quantize the row into lds_q; returns the
-// per-token activation scale (decoder.cpp:706-727, 1028-1043).
+// The row slice of this thread, normalized when norm.kind >= 0 (in v; in[i]
+// marks float4 slots inside the row, the others are zero).  The block
+// reductions run in a fixed order (decoder.cpp:706-727).
 //
 // With `seq` (a K-float LDS buffer) and norm.sequential, the mean and square
 // sums are those of the CPU's norm(): every thread writes its columns' terms
 // to seq and one lane adds them in column order.
 template <int V>
-__device__ float block_norm_quantize(RowSlice<V>& r, int K, const NormView& norm, int8_t* lds_q, float* red,
-                                     double* dred, float* seq = nullptr) {
+__device__ __forceinline__ void block_norm(RowSlice<V>& r, int K, const NormView& norm, float* red, double* dred, float* seq,
+                           float4 (&v)[V], bool (&in)[V]) {
     const int tid = threadIdx.x;
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 v[V];
-    bool in[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         in[i] = 4 * (tid + kBlock * i) < K;
@@ -418,6 +417,17 @@ __device__ float block_norm_quantize(RowSlice<V>& r, int K, const NormView& norm
             if (!in[i]) v[i] = zero;
         }
     }
+}
+
+// Normalize (optionally) and quantize the row into lds_q; returns the
+// per-token activation scale (decoder.cpp:706-727, 1028-1043).
+template <int V>
+__device__ float block_norm_quantize(RowSlice<V>& r, int K, const NormView& norm, int8_t* lds_q, float* red,
+                                     double* dred, float* seq = nullptr) {
+    const int tid = threadIdx.x;
+    float4 v[V];
+    bool in[V];
+    block_norm<V>(r, K, norm, red, dred, seq, v, in);
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < V; ++i)
@@ -744,6 +754,108 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
             const float a = wave_sum_f32(acc[r][t]);
             if (lane == 0 && row < w.rows) store_out(y, (size_t)t * w.rows + row, a, bias_at(w, row), epilogue);
         }
+    }
+}
+
+// ---------------------------------- FP decode GEMV with the norm fused in ---
+// One token of an FP32 / BF16 / weight-only INT8 / INT4 linear whose input is
+// normalized first (the q|k|v and gate|up inputs): every block normalizes the
+// row itself (block_norm, the fused integer GEMV's order) into LDS, so no
+// separate norm launch or round trip through memory is needed; the weight
+// chunks of the wave's rows are requested before the norm starts.  Per row
+// the sums are gemv_fp_kernel's (lane-strided chunks, groups summed then
+// scaled), then one wave sum.  Paired epilogues fuse RoPE with the KV append
+// (q|k|v) or the gated activation (gate|up), as in the integer GEMV.
+// Quantized weights need scale groups of whole 16-byte chunks.
+template <int BITS, int RPW, int MAXJ, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, const float* __restrict__ x,
+                                                              NormView norm, float* __restrict__ y, int epilogue,
+                                                              PairEpilogue pe) {
+    static_assert(EPI == kPairNone || RPW == 2, "paired epilogues compute two rows per wave");
+    constexpr int E = 128 / BITS;                    // weight values per 16-byte chunk
+    constexpr int V = kFusedMaxV;                    // float4 of the row per thread
+    __shared__ __align__(16) float lds_x[kFusedMaxK];
+    __shared__ float red[16];
+    __shared__ double dred[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = w.cols, nch = K / E;
+    const int wave_index = blockIdx.x * (kBlock / kWave) + wave;
+    const int row_first = wave_index * RPW;
+    int rows_of[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rows_of[r] = row_first + r;
+    if constexpr (EPI != kPairNone) {
+        if (row_first < w.rows) pair_rows(pe, wave_index, rows_of[0], rows_of[1]);
+    }
+    RowSlice<V> slice;
+    slice.issue(x, K, norm);
+    const int groups = (BITS == 8 || BITS == 4) ? K / w.group : 1;
+    uint4 wv[RPW][MAXJ];
+    float ws[RPW][MAXJ];
+    const uint8_t* base = (const uint8_t*)w.data;
+    const size_t row_bytes = (size_t)K * BITS / 8;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = min(rows_of[r], w.rows - 1);
+        const uint4* rp = (const uint4*)(base + (size_t)row * row_bytes);
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = min(lane + kWave * j, nch - 1);
+            wv[r][j] = load_stream16(rp + c);
+            if constexpr (BITS == 8 || BITS == 4) ws[r][j] = w.scales[(size_t)row * groups + (c * E) / w.group];
+        }
+    }
+    float4 v[V];
+    bool in[V];
+    block_norm<V>(slice, K, norm, red, dred, nullptr, v, in);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+        if (in[i]) *(float4*)(lds_x + 4 * (threadIdx.x + kBlock * i)) = v[i];
+    __syncthreads();
+    if (row_first >= w.rows) return;
+    float vals[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + kWave * j;
+            if (c >= nch) continue;
+            float xv[E];
+#pragma unroll
+            for (int k = 0; k < E / 4; ++k) {
+                const float4 q = *(const float4*)(lds_x + c * E + 4 * k);
+                xv[4 * k] = q.x; xv[4 * k + 1] = q.y; xv[4 * k + 2] = q.z; xv[4 * k + 3] = q.w;
+            }
+            const uint32_t words[4] = {BITS == 4 ? wv[r][j].x ^ 0x88888888u : wv[r][j].x,
+                                       BITS == 4 ? wv[r][j].y ^ 0x88888888u : wv[r][j].y,
+                                       BITS == 4 ? wv[r][j].z ^ 0x88888888u : wv[r][j].z,
+                                       BITS == 4 ? wv[r][j].w ^ 0x88888888u : wv[r][j].w};
+            float part = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                float wf;
+                if constexpr (BITS == 32) wf = __uint_as_float(words[e]);
+                else if constexpr (BITS == 16) wf = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
+                else if constexpr (BITS == 8) wf = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
+                else wf = __uint_as_float(0x4B000000u | ((words[e / 8] >> (4 * (e & 7))) & 0xFu)) - 8388616.0f;
+                if constexpr (BITS == 32 || BITS == 16) acc = fmaf(wf, xv[e], acc);
+                else part = fmaf(wf, xv[e], part);
+            }
+            if constexpr (BITS == 8 || BITS == 4) acc = fmaf(part, ws[r][j], acc);
+        }
+        const int row = rows_of[r];
+        const float a = wave_sum_f32(acc);
+        vals[r] = row < w.rows ? a + bias_at(w, row) : 0.0f;
+        if constexpr (EPI == kPairNone) {
+            if (lane == 0 && row < w.rows) {
+                const float prev = epilogue == kAccumulate ? y[row] : 0.0f;
+                y[row] = epilogue == kAccumulate ? prev + vals[r] : vals[r];
+            }
+        }
+    }
+    if constexpr (EPI != kPairNone) {
+        if (lane == 0) pair_store(pe, rows_of[0], vals[0], rows_of[1], vals[1]);
     }
 }
 
@@ -1657,6 +1769,27 @@ void launch_fused_int(const LinearCall& c, hipStream_t stream) {
     else launch_fused_int_rpw<BITS, 1, kPairNone>(c, jn, stream);
 }
 
+template <int BITS, int RPW, int EPI>
+void launch_fused_fp_rpw(const LinearCall& c, int jn, hipStream_t stream) {
+    const int grid = ceil_div(c.w.rows, (kBlock / kWave) * RPW);
+#define LEAF_FUSED_FP(J) gemv_fp_fused_kernel<BITS, RPW, J, EPI><<<grid, kBlock, 0, stream>>>(c.w, c.x, c.norm, c.y, \
+        c.epilogue, c.pair)
+    if (jn <= 1) LEAF_FUSED_FP(1);
+    else if (jn <= 2) LEAF_FUSED_FP(2);
+    else if (jn <= 4) LEAF_FUSED_FP(4);
+    else LEAF_FUSED_FP(8);
+#undef LEAF_FUSED_FP
+}
+
+template <int BITS>
+void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
+    constexpr int E = 128 / BITS;
+    const int jn = (c.w.cols / E + kWave - 1) / kWave;
+    if (c.pair.mode == kPairRopeKv) return launch_fused_fp_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
+    if (c.pair.mode == kPairGated) return launch_fused_fp_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    launch_fused_fp_rpw<BITS, 2, kPairNone>(c, jn, stream);
+}
+
 template <int BITS, int T>
 void launch_gemv_int_t(const LinearCall& c, const int8_t* xq, const float* xs, hipStream_t stream) {
     constexpr int RPW = 2;
@@ -1749,10 +1882,24 @@ void launch_scale_columns(const float* x, int rows, int width, const float* fact
     scale_columns_kernel<<<std::min(ceil_div(count, kBlock), 4096), kBlock, 0, stream>>>(x, width, count, factors, y);
 }
 
+// The single-token FP GEMV with the norm (and a paired epilogue) fused in:
+// whole 16-byte chunks, at most 8 per lane, scale groups of whole chunks.
+bool fp_fuses(const LinearCall& c) {
+    const WeightView& w = c.w;
+    if (c.integer_activations || c.tokens != 1 || !c.x || c.xq) return false;
+    if (w.bits != 32 && w.bits != 16 && w.bits != 8 && w.bits != 4) return false;
+    const int E = 128 / w.bits;
+    const bool quantized = w.bits == 8 || w.bits == 4;
+    return w.cols % E == 0 && w.cols <= kFusedMaxK && w.cols / E <= 8 * kWave && (!quantized || w.group % E == 0) &&
+           (c.force_path == 0 || c.force_path == 1) && (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 && (c.pair.mode == kPairNone || w.rows % 2 == 0);
+}
+
 bool linear_fuses(const LinearCall& c) {
     const WeightView& w = c.w;
     const int E8 = w.bits == 8 ? 16 : 32;
-    return c.integer_activations && (w.bits == 8 || w.bits == 4) && c.tokens == 1 && c.x && !c.xq &&
+    if (!c.integer_activations) return fp_fuses(c);
+    return (w.bits == 8 || w.bits == 4) && c.tokens == 1 && c.x && !c.xq &&
            w.group == w.cols && w.cols % E8 == 0 && w.cols <= kFusedMaxK &&
            (c.force_path == 0 || c.force_path == 1) && (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 && (c.pair.mode == kPairNone || w.rows % 2 == 0);
@@ -1839,6 +1986,15 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         linear_generic_kernel<<<ceil_div((size_t)c.tokens * w.rows, kBlock), kBlock, 0, stream>>>(
             w, nullptr, xq, xs, c.tokens, 1, c.y, c.epilogue, c.acc_out, c.unfused_group_sum && c.tokens > 1);
         return 2;
+    }
+    if ((c.norm.kind >= 0 || c.pair.mode != kPairNone) && fp_fuses(c)) {
+        switch (w.bits) {
+        case 32: launch_fused_fp<32>(c, stream); break;
+        case 16: launch_fused_fp<16>(c, stream); break;
+        case 8: launch_fused_fp<8>(c, stream); break;
+        default: launch_fused_fp<4>(c, stream); break;
+        }
+        return 1;
     }
     if (c.norm.kind >= 0) return -1;
     const bool group_ok = !quantized || (w.group % E == 0) || (E % w.group == 0);

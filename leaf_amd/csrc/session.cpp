@@ -651,9 +651,12 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* qkv = qkv_.as<float>();
         float* keys = kv_.as<float>() + size_t(layer) * 2 * plane;
         float* values = keys + plane;
-        const bool fuse_in = M == 1 && model.integer_linear(L.qkv) && L.stacked_qkv && !L.qkv.input_scale;
-        // In reference order the fused GEMV sums the norm in column order
-        // (and the RoPE pair epilogue is the rope kernel's arithmetic).
+        // Single-token q|k|v: the GEMV normalizes its input itself (integer or
+        // FP weights; FP only with the fast kernels).  In reference order the
+        // fused integer GEMV sums the norm in column order (and the RoPE pair
+        // epilogue is the rope kernel's arithmetic).
+        const bool fuse_in = M == 1 && L.stacked_qkv && !L.qkv.input_scale &&
+                             (model.integer_linear(L.qkv) || !reference_);
         NormView input_norm = L.input_norm;
         input_norm.sequential = reference_ ? 1 : 0;
         // Single-token W8A8: one launch normalizes, quantizes, projects q|k|v,
@@ -775,8 +778,8 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         float* act = act_.as<float>();
         const int f = int(c.intermediate);
         if (c.gated) {
-            const bool fuse_post = rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up &&
-                                   !L.gate_up.input_scale;
+            const bool fuse_post = rows == 1 && L.stacked_gate_up && !L.gate_up.input_scale &&
+                                   (model.integer_linear(L.gate_up) || !reference_);
             NormView post_norm = L.post_norm;
             post_norm.sequential = reference_ ? 1 : 0;
             PairEpilogue gated;
@@ -816,8 +819,15 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             if (!fuse_act && !prequantizes(L.down, rows))
                 timed(Profiler::Other, 0, 0, [&] { activation(gate_up, rows, f, 1, act); });
         } else {
-            norm(hid, rows, h, L.post_norm, normed);
-            run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
+            // ungated MLP: a single-token FP up projection normalizes its input itself
+            const bool fuse_up = rows == 1 && !reference_ && !model.integer_linear(L.up) &&
+                                 linear_fuses(make_call(L.up, hid, rows, gate_up, kStore, &L.post_norm));
+            if (fuse_up) {
+                run_linear(L.up, hid, rows, gate_up, kStore, &L.post_norm);
+            } else {
+                norm(hid, rows, h, L.post_norm, normed);
+                run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
+            }
             activation(gate_up, rows, f, 0, act);
         }
         const bool down_q = c.gated && prequantizes(L.down, rows) &&
@@ -840,6 +850,14 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
     const int head_rows = all_logits ? M : 1;
     // `hidden` now points at the rows the head reads: all rows, or the last one.
     const float* x = hidden;
+    // a single-row FP head normalizes its input itself (fast kernels)
+    const bool fuse_head = c.final_norm && head_rows == 1 && !reference_ && !model.integer_linear(model.head) &&
+                           linear_fuses(make_call(model.head, hidden, 1, logits_.as<float>(), kStore,
+                                                  &model.final_norm));
+    if (fuse_head) {
+        run_linear(model.head, hidden, 1, logits_.as<float>(), kStore, &model.final_norm);
+        return;
+    }
     if (c.final_norm) {
         norm(hidden, head_rows, h, model.final_norm, normed);
         x = normed;
