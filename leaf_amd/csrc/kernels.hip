@@ -1599,10 +1599,46 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(AttentionCall 
 }
 
 // Merge for decode spans written without in-kernel merging: one wave per head.
-__global__ __launch_bounds__(kWave) void attention_merge_spans_kernel(AttentionCall p, int splits) {
-    const int h = blockIdx.x;
-    const size_t stride = (size_t)p.dim + 2;
-    merge_head_spans(p.partial + (size_t)h * splits * stride, splits, p.dim, p.out + (size_t)h * p.dim, threadIdx.x);
+// Merge of one query head's span partials (max, sum, unnormalized output)
+// by a block of 256 threads: the spans' weights exp(m_s - m) once per span
+// into LDS, then 256 / dim groups of dim threads each sum every group-th
+// span's outputs (many loads in flight per thread, not one chain of loads
+// per output element), combined at the end.
+constexpr int kMergeThreads = 256;
+__global__ __launch_bounds__(kMergeThreads) void attention_merge_spans_kernel(AttentionCall p, int splits) {
+    extern __shared__ float w_s[];                 // [splits]
+    __shared__ float red[kMergeThreads / kWave];
+    __shared__ float o_s[kMergeThreads];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int dim = p.dim;
+    const size_t stride = (size_t)dim + 2;
+    const float* part = p.partial + (size_t)h * splits * stride;
+    float m = -INFINITY;
+    for (int s2 = tid; s2 < splits; s2 += kMergeThreads) m = fmaxf(m, part[s2 * stride]);
+    m = block_reduce<float>(m, red, [](float a, float b) { return fmaxf(a, b); }, wave_max_f32);
+    float l = 0.0f;
+    for (int s2 = tid; s2 < splits; s2 += kMergeThreads) {
+        const float ms = part[s2 * stride];
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - m);
+        w_s[s2] = w;
+        l += part[s2 * stride + 1] * w;
+    }
+    l = block_reduce<float>(l, red, [](float a, float b) { return a + b; }, wave_sum_f32);
+    __syncthreads();   // every weight is in LDS
+    const int groups = dim <= kMergeThreads ? kMergeThreads / dim : 1;
+    const int g = tid / dim, d = tid % dim;
+    float v = 0.0f;
+    if (g < groups) {
+#pragma unroll 8
+        for (int s2 = g; s2 < splits; s2 += groups) v = fmaf(part[s2 * stride + 2 + d], w_s[s2], v);
+        o_s[tid] = v;
+    }
+    __syncthreads();
+    for (int e = tid; e < dim; e += kMergeThreads) {
+        float total = 0.0f;
+        for (int k = 0; k < groups; ++k) total += o_s[k * dim + e];
+        p.out[(size_t)h * dim + e] = l > 0.0f ? total / l : 0.0f;
+    }
 }
 
 // ----------------------------------------------------- small elementwise ---
@@ -1787,6 +1823,9 @@ void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
     const int jn = (c.w.cols / E + kWave - 1) / kWave;
     if (c.pair.mode == kPairRopeKv) return launch_fused_fp_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
     if (c.pair.mode == kPairGated) return launch_fused_fp_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    // tall int8 / int4 matrices: four rows per wave (the row read from LDS
+    // serves more weight bytes), when the grid still covers the CUs
+    if ((BITS == 8 || BITS == 4) && c.w.rows >= 4 * 4096) return launch_fused_fp_rpw<BITS, 4, kPairNone>(c, jn, stream);
     launch_fused_fp_rpw<BITS, 2, kPairNone>(c, jn, stream);
 }
 
@@ -1987,7 +2026,9 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
             w, nullptr, xq, xs, c.tokens, 1, c.y, c.epilogue, c.acc_out, c.unfused_group_sum && c.tokens > 1);
         return 2;
     }
-    if ((c.norm.kind >= 0 || c.pair.mode != kPairNone) && fp_fuses(c)) {
+    if (fp_fuses(c)) {
+        // every single-token FP GEMV it handles: all of a wave's weight chunks
+        // in flight at once, the input row read once per block
         switch (w.bits) {
         case 32: launch_fused_fp<32>(c, stream); break;
         case 16: launch_fused_fp<16>(c, stream); break;
@@ -2044,7 +2085,7 @@ bool launch_attention(const AttentionCall& call, hipStream_t stream) {
             // block: that needs device-scope release/acquire fences, which
             // write back and invalidate L2 on every block (measured ~5 us/layer).
             attention_decode_kernel<<<dim3(call.kv_heads, splits), kBlock, 0, stream>>>(call, per_split, nullptr);
-            attention_merge_spans_kernel<<<call.heads, kWave, 0, stream>>>(call, splits);
+            attention_merge_spans_kernel<<<call.heads, kMergeThreads, splits * sizeof(float), stream>>>(call, splits);
             return true;
         }
     }
