@@ -541,6 +541,9 @@ def _db_counters(db: Path) -> list:
 # The four W8A8 GEMMs of a TinyLlama prefill layer, in launch order, at 512
 # tokens: (name, rows, K).
 PREFILL_GEMMS = (("qkv", 2560, 2048), ("o", 2048, 2048), ("gate_up", 11264, 2048), ("down", 2048, 5632))
+# Template arguments of the only tile configuration the stacked gate|up
+# projection uses (128 rows x 256 tokens, 2 x 4 waves): the label of its dispatches.
+GATE_UP_TILE = "<2, 2, 3, 2, 4>"
 
 
 def derive_prefill_counters(base: Path) -> dict:
@@ -558,14 +561,14 @@ def derive_prefill_counters(base: Path) -> dict:
 
     def gemms(entries):
         # Label the prefill GEMM dispatches: q|k|v runs 320 blocks of 64 x 64
-        # tiles, gate|up 128 x 256 tiles; o and down both run 256 blocks and
+        # tiles, gate|up 128 x 256 tiles on eight waves; o and down both run 256 blocks and
         # follow q|k|v and gate|up respectively (the last layer, trimmed to
         # one row, runs only its q|k|v as a GEMM).
         out, previous = [], None
         for name, blocks, values in entries:
             if "gemm_w8a8_mfma_kernel" not in name:
                 continue
-            if "<2, 4, 3>" in name:
+            if GATE_UP_TILE in name:
                 label = "gate_up"
             elif blocks == 320:
                 label = "qkv"
@@ -633,7 +636,7 @@ def summarize_trace(db: Path, top: int = 25) -> str:
     for name, blocks, duration in rows:
         if "gemm_w8a8_mfma_kernel" not in name:
             continue
-        if "<2, 4, 3>" in name:
+        if GATE_UP_TILE in name:
             label = "gate_up"
         elif blocks == 320:
             label = "qkv"

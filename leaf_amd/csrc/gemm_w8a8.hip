@@ -7,7 +7,7 @@
 // K % 128 == 0.  The integer sums are exact and the epilogue is the CPU
 // path's expression, so every output is bit-identical to it.
 //
-// Tiling.  A block of four waves (2 x 2) owns 64 TM weight rows x 64 TN
+// Tiling.  A block of WR x WC waves owns 32 WR TM weight rows x 32 WC TN
 // tokens; each wave a TM x TN grid of v_mfma_i32_32x32x32_i8 tiles.  The
 // weight rows are the MFMA's A operand and the tokens its B operand, so a
 // lane of an output tile holds one token and, per group of four results,
@@ -77,18 +77,19 @@ __device__ __forceinline__ float dequant(int acc, float sx, float sw, float b) {
     return fmaf((float)acc * sx, sw, 0.0f) + b;
 }
 
-template <int TM, int TN, int NSTAGE>
-__global__ __launch_bounds__(256) void gemm_w8a8_mfma_kernel(
+template <int TM, int TN, int NSTAGE, int WR = 2, int WC = 2>
+__global__ __launch_bounds__(64 * WR * WC) void gemm_w8a8_mfma_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ w_scales, const float* __restrict__ bias,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, int M, int N, int K, float* __restrict__ y,
     int epilogue, int32_t* __restrict__ acc_out, int splits, int32_t* __restrict__ partial, bool vec) {
-    constexpr int BN = 64 * TM, BM = 64 * TN;                 // weight rows, tokens per block
+    constexpr int kWaves = WR * WC;                           // WR x WC waves (weight rows x tokens)
+    constexpr int BN = 32 * WR * TM, BM = 32 * WC * TN;       // weight rows, tokens per block
     constexpr int kChunksW = BN / 8;                          // 8 rows x 128 K bytes per chunk
     constexpr int kChunks = kChunksW + BM / 8;
-    constexpr int kLoads = kChunks / 4;                       // 16-byte loads per lane per stage
+    constexpr int kLoads = kChunks / kWaves;                  // 16-byte loads per lane per stage
     constexpr int kStageBytes = kChunks * kChunkBytes;
     constexpr int kSets = TM * TN >= 4 ? 1 : 2;               // accumulator sets (alternating k-steps)
-    static_assert(kChunks % 4 == 0, "chunks must divide among the waves");
+    static_assert(kChunks % kWaves == 0, "chunks must divide among the waves");
     static_assert((NSTAGE - 2) * kLoads < 64, "vmcnt holds at most 63");
     __shared__ __align__(1024) int8_t lds[NSTAGE * kStageBytes];
 
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void gemm_w8a8_mfma_kernel(
     int dst[kLoads];
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-        const int c = j * 4 + wave;
+        const int c = j * kWaves + wave;
         const bool is_w = c < kChunksW;
         const int cc = is_w ? c : c - kChunksW;
         const int row = cc * 8 + (lane >> 3);
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(256) void gemm_w8a8_mfma_kernel(
     }
 
     // ---- accumulators: wave sub-tile rows wn.., tokens wm..
-    const int wn = (wave >> 1) * 32 * TM, wm = (wave & 1) * 32 * TN;
+    const int wn = (wave / WC) * 32 * TM, wm = (wave % WC) * 32 * TN;
     v16i acc[kSets][TM][TN];
 #pragma unroll
     for (int q = 0; q < kSets; ++q)
@@ -253,15 +254,16 @@ __global__ __launch_bounds__(256) void gemm_w8a8_mfma_kernel(
     }
 }
 
-template <int TM, int TN, int NSTAGE>
+template <int TM, int TN, int NSTAGE, int WR = 2, int WC = 2>
 void launch_tiles(const int8_t* W, const float* w_scales, const float* bias, const int8_t* xq, const float* xs,
                   int M, int N, int K, float* y, int epilogue, int32_t* acc_out, int splits, int32_t* partial,
                   hipStream_t stream) {
     auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const bool vec = N % 4 == 0 && aligned(w_scales) && aligned(bias) && aligned(y) && aligned(acc_out) &&
                      aligned(partial);
-    const dim3 grid(((M + 64 * TN - 1) / (64 * TN)) * ((N + 64 * TM - 1) / (64 * TM)) * splits);
-    gemm_w8a8_mfma_kernel<TM, TN, NSTAGE><<<grid, 256, 0, stream>>>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue,
+    constexpr int BN = 32 * WR * TM, BM = 32 * WC * TN;
+    const dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN) * splits);
+    gemm_w8a8_mfma_kernel<TM, TN, NSTAGE, WR, WC><<<grid, 64 * WR * WC, 0, stream>>>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue,
                                                                      acc_out, splits, partial, vec);
 }
 
@@ -271,8 +273,11 @@ bool gemm_w8a8_mfma_supported(int K) { return K % kStageK == 0 && K > 0; }
 
 GemmTiles gemm_w8a8_tiles(int M, int N, int K, size_t split_capacity) {
     // Large outputs (the stacked gate|up projection of a 512-token prefill)
-    // take 128 weight rows x 256 tokens per block; everything else 64 x 64,
-    // which puts the most blocks on the CUs.  A grid still short of 128
+    // take 128 weight rows x 256 tokens per block, eight waves of 64 x 64
+    // (two waves per SIMD: one issues MFMAs while the other waits on a
+    // barrier or its operands; 25 against 29 us with four waves of 64 x 128
+    // for 512 x 11264 x 2048); everything else 64 x 64 with four waves (two
+    // blocks fit a CU), which puts the most blocks on the CUs.  A grid still short of 128
     // blocks (few tokens) splits K, each split at least four 128-byte stages,
     // when the workspace holds the int32 sums.
     GemmTiles g;
@@ -297,26 +302,10 @@ void launch_gemm_w8a8_mfma(const int8_t* W, const float* w_scales, const float* 
                            const float* xs, int M, int N, int K, float* y, int epilogue, int32_t* acc_out,
                            const GemmTiles& tiles, int32_t* partial, hipStream_t stream) {
     const int splits = partial ? tiles.splits : 1;
-    const int shape = tiles.rows * 1000 + tiles.tokens;
-    switch (shape) {
-    case 128256:
-        launch_tiles<2, 4, 3>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-        break;
-    case 256128:
-        launch_tiles<4, 2, 3>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-        break;
-    case 128128:
-        launch_tiles<2, 2, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-        break;
-    case 128064:
-        launch_tiles<2, 1, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-        break;
-    case 64128:
-        launch_tiles<1, 2, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-        break;
-    default:
+    if (tiles.rows == 128 && tiles.tokens == 256)   // eight waves (two per SIMD), each 64 rows x 64 tokens
+        launch_tiles<2, 2, 3, 2, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
+    else
         launch_tiles<1, 1, 4>(W, w_scales, bias, xq, xs, M, N, K, y, epilogue, acc_out, splits, partial, stream);
-    }
 }
 
 }  // namespace leafhip
