@@ -30,6 +30,28 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
 }
 
+// The eight two's-complement nibbles of `word` (nibble e = bits 4e..4e+3, the
+// low nibble first) as value / 16, exactly.  v_cvt_off_f32_i4 converts the
+// low four bits of its operand to value / 16; byte selects of `word` reach the
+// even nibbles and byte selects of `word >> 4` the odd ones, so a word costs
+// one shift and eight converts.  (The empty asm keeps the compiler from
+// folding the shift into bit-field extracts, which would drop the selects.)
+// A product with value / 16, and every sum of such products, is the one with
+// value scaled by exactly 2^-4 (outside the subnormal range), so a group
+// scale taken times 16 gives the same results as dequantizing to value.
+__device__ __forceinline__ void int4_sixteenths(uint32_t word, float (&f)[8]) {
+    uint32_t odd = word >> 4;
+    asm("" : "+v"(odd));
+    f[0] = __builtin_amdgcn_cvt_off_f32_i4(word);
+    f[2] = __builtin_amdgcn_cvt_off_f32_i4((word >> 8) & 0xFFu);
+    f[4] = __builtin_amdgcn_cvt_off_f32_i4((word >> 16) & 0xFFu);
+    f[6] = __builtin_amdgcn_cvt_off_f32_i4(word >> 24);
+    f[1] = __builtin_amdgcn_cvt_off_f32_i4(odd);
+    f[3] = __builtin_amdgcn_cvt_off_f32_i4((odd >> 8) & 0xFFu);
+    f[5] = __builtin_amdgcn_cvt_off_f32_i4((odd >> 16) & 0xFFu);
+    f[7] = __builtin_amdgcn_cvt_off_f32_i4(odd >> 24);
+}
+
 // Butterfly reductions across the 64 lanes of a wave; every lane gets the result.
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll

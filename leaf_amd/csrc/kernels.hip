@@ -704,20 +704,21 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
         for (int r = 0; r < RPW; ++r) {
             const int row = min(row_first + r, w.rows - 1);
             const uint4 wv = load_stream16((const uint4*)(base + (size_t)row * row_bytes) + c);
-            // int4: flipping each nibble's sign bit (xor 8) gives u = value + 8 in
-            // 0..15; the float with bits 0x4B000000 | u is 2^23 + u exactly, so
-            // subtracting 2^23 + 8 leaves the signed value, exactly
-            const uint32_t words[4] = {BITS == 4 ? wv.x ^ 0x88888888u : wv.x, BITS == 4 ? wv.y ^ 0x88888888u : wv.y,
-                                       BITS == 4 ? wv.z ^ 0x88888888u : wv.z, BITS == 4 ? wv.w ^ 0x88888888u : wv.w};
+            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+            // int4: value / 16 (the group scale is taken times 16 below)
             float wf[E];
+            if constexpr (BITS == 4) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                if constexpr (BITS == 32) wf[e] = __uint_as_float(words[e]);
-                else if constexpr (BITS == 16) wf[e] = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
-                else if constexpr (BITS == 8) wf[e] = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
-                else  // nibble e: bits 4 (e % 8) of word e / 8 (low nibble = even column)
-                    wf[e] = __uint_as_float(0x4B000000u | ((words[e / 8] >> (4 * (e & 7))) & 0xFu)) - 8388616.0f;
+                for (int q = 0; q < 4; ++q) int4_sixteenths(words[q], *(float(*)[8])(wf + 8 * q));
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    if constexpr (BITS == 32) wf[e] = __uint_as_float(words[e]);
+                    else if constexpr (BITS == 16) wf[e] = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
+                    else wf[e] = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
+                }
             }
+            constexpr float kScaleOf = BITS == 4 ? 16.0f : 1.0f;
             if constexpr (BITS == 32 || BITS == 16) {
 #pragma unroll
                 for (int t = 0; t < T; ++t)
@@ -725,7 +726,7 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
                     for (int e = 0; e < E; ++e) acc[r][t] = fmaf(wf[e], xv[t][e], acc[r][t]);
             } else if (piece == E) {
                 // one scale group covers the chunk: unrolled, the same sums
-                const float s = w.scales[(size_t)row * groups + (c * E) / w.group];
+                const float s = w.scales[(size_t)row * groups + (c * E) / w.group] * kScaleOf;
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
                     float part = 0.0f;
@@ -735,7 +736,7 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
                 }
             } else {
                 for (int p0 = 0; p0 < E; p0 += piece) {
-                    const float s = w.scales[(size_t)row * groups + (c * E + p0) / w.group];
+                    const float s = w.scales[(size_t)row * groups + (c * E + p0) / w.group] * kScaleOf;
 #pragma unroll
                     for (int t = 0; t < T; ++t) {
                         float part = 0.0f;
@@ -802,7 +803,9 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
         for (int j = 0; j < MAXJ; ++j) {
             const int c = min(lane + kWave * j, nch - 1);
             wv[r][j] = load_stream16(rp + c);
-            if constexpr (BITS == 8 || BITS == 4) ws[r][j] = w.scales[(size_t)row * groups + (c * E) / w.group];
+            // int4 sums run on value / 16: the scale is taken times 16
+            if constexpr (BITS == 8 || BITS == 4)
+                ws[r][j] = w.scales[(size_t)row * groups + (c * E) / w.group] * (BITS == 4 ? 16.0f : 1.0f);
         }
     }
     float4 v[V];
@@ -827,20 +830,24 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
                 const float4 q = *(const float4*)(lds_x + c * E + 4 * k);
                 xv[4 * k] = q.x; xv[4 * k + 1] = q.y; xv[4 * k + 2] = q.z; xv[4 * k + 3] = q.w;
             }
-            const uint32_t words[4] = {BITS == 4 ? wv[r][j].x ^ 0x88888888u : wv[r][j].x,
-                                       BITS == 4 ? wv[r][j].y ^ 0x88888888u : wv[r][j].y,
-                                       BITS == 4 ? wv[r][j].z ^ 0x88888888u : wv[r][j].z,
-                                       BITS == 4 ? wv[r][j].w ^ 0x88888888u : wv[r][j].w};
+            const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+            float wf[E];
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) int4_sixteenths(words[q], *(float(*)[8])(wf + 8 * q));
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    if constexpr (BITS == 32) wf[e] = __uint_as_float(words[e]);
+                    else if constexpr (BITS == 16) wf[e] = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
+                    else wf[e] = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
+                }
+            }
             float part = 0.0f;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                float wf;
-                if constexpr (BITS == 32) wf = __uint_as_float(words[e]);
-                else if constexpr (BITS == 16) wf = bf16_to_f32((words[e / 2] >> (16 * (e & 1))) & 0xFFFFu);
-                else if constexpr (BITS == 8) wf = (float)(int)(int8_t)((words[e / 4] >> (8 * (e & 3))) & 0xFFu);
-                else wf = __uint_as_float(0x4B000000u | ((words[e / 8] >> (4 * (e & 7))) & 0xFu)) - 8388616.0f;
-                if constexpr (BITS == 32 || BITS == 16) acc = fmaf(wf, xv[e], acc);
-                else part = fmaf(wf, xv[e], part);
+                if constexpr (BITS == 32 || BITS == 16) acc = fmaf(wf[e], xv[e], acc);
+                else part = fmaf(wf[e], xv[e], part);
             }
             if constexpr (BITS == 8 || BITS == 4) acc = fmaf(part, ws[r][j], acc);
         }
