@@ -766,13 +766,15 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_kernel(WeightView w, const flo
 // chunks of the wave's rows are requested before the norm starts.  Per row
 // the sums are gemv_fp_kernel's (lane-strided chunks, groups summed then
 // scaled), then one wave sum.  Paired epilogues fuse RoPE with the KV append
-// (q|k|v) or the gated activation (gate|up), as in the integer GEMV.
+// (q|k|v) or the gated activation (gate|up), as in the integer GEMV; a wave
+// takes RPW / 2 consecutive pairs.  Each chunk's activations are read from
+// LDS once and serve all of the wave's rows.
 // Quantized weights need scale groups of whole 16-byte chunks.
 template <int BITS, int RPW, int MAXJ, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, const float* __restrict__ x,
                                                               NormView norm, float* __restrict__ y, int epilogue,
                                                               PairEpilogue pe) {
-    static_assert(EPI == kPairNone || RPW == 2, "paired epilogues compute two rows per wave");
+    static_assert(EPI == kPairNone || RPW % 2 == 0, "paired epilogues compute whole pairs");
     constexpr int E = 128 / BITS;                    // weight values per 16-byte chunk
     constexpr int V = kFusedMaxV;                    // float4 of the row per thread
     __shared__ __align__(16) float lds_x[kFusedMaxK];
@@ -786,7 +788,10 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
 #pragma unroll
     for (int r = 0; r < RPW; ++r) rows_of[r] = row_first + r;
     if constexpr (EPI != kPairNone) {
-        if (row_first < w.rows) pair_rows(pe, wave_index, rows_of[0], rows_of[1]);
+        // pair q = wave_index * RPW / 2 + i exists while 2 q < rows
+#pragma unroll
+        for (int i = 0; i < RPW / 2; ++i)
+            if (row_first + 2 * i < w.rows) pair_rows(pe, wave_index * (RPW / 2) + i, rows_of[2 * i], rows_of[2 * i + 1]);
     }
     RowSlice<V> slice;
     slice.issue(x, K, norm);
@@ -816,20 +821,21 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
         if (in[i]) *(float4*)(lds_x + 4 * (threadIdx.x + kBlock * i)) = v[i];
     __syncthreads();
     if (row_first >= w.rows) return;
-    float vals[RPW];
+    float acc[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        float acc = 0.0f;
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + kWave * j;
-            if (c >= nch) continue;
-            float xv[E];
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + kWave * j;
+        if (c >= nch) continue;
+        float xv[E];
 #pragma unroll
-            for (int k = 0; k < E / 4; ++k) {
-                const float4 q = *(const float4*)(lds_x + c * E + 4 * k);
-                xv[4 * k] = q.x; xv[4 * k + 1] = q.y; xv[4 * k + 2] = q.z; xv[4 * k + 3] = q.w;
-            }
+        for (int k = 0; k < E / 4; ++k) {
+            const float4 q = *(const float4*)(lds_x + c * E + 4 * k);
+            xv[4 * k] = q.x; xv[4 * k + 1] = q.y; xv[4 * k + 2] = q.z; xv[4 * k + 3] = q.w;
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
             const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
             float wf[E];
             if constexpr (BITS == 4) {
@@ -846,13 +852,17 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
             float part = 0.0f;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                if constexpr (BITS == 32 || BITS == 16) acc = fmaf(wf[e], xv[e], acc);
+                if constexpr (BITS == 32 || BITS == 16) acc[r] = fmaf(wf[e], xv[e], acc[r]);
                 else part = fmaf(wf[e], xv[e], part);
             }
-            if constexpr (BITS == 8 || BITS == 4) acc = fmaf(part, ws[r][j], acc);
+            if constexpr (BITS == 8 || BITS == 4) acc[r] = fmaf(part, ws[r][j], acc[r]);
         }
+    }
+    float vals[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
         const int row = rows_of[r];
-        const float a = wave_sum_f32(acc);
+        const float a = wave_sum_f32(acc[r]);
         vals[r] = row < w.rows ? a + bias_at(w, row) : 0.0f;
         if constexpr (EPI == kPairNone) {
             if (lane == 0 && row < w.rows) {
@@ -862,7 +872,10 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
         }
     }
     if constexpr (EPI != kPairNone) {
-        if (lane == 0) pair_store(pe, rows_of[0], vals[0], rows_of[1], vals[1]);
+#pragma unroll
+        for (int i = 0; i < RPW / 2; ++i)
+            if (lane == 0 && row_first + 2 * i < w.rows)
+                pair_store(pe, rows_of[2 * i], vals[2 * i], rows_of[2 * i + 1], vals[2 * i + 1]);
     }
 }
 
@@ -1829,7 +1842,18 @@ void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
     constexpr int E = 128 / BITS;
     const int jn = (c.w.cols / E + kWave - 1) / kWave;
     if (c.pair.mode == kPairRopeKv) return launch_fused_fp_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
-    if (c.pair.mode == kPairGated) return launch_fused_fp_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    if (c.pair.mode == kPairGated) {
+        // Tall int8 / int4 gate|up stacks (rows of few bytes): several pairs
+        // per wave, so fewer blocks repeat the norm prologue, while the grid
+        // still covers the CUs (>= 256 blocks) and the wave's weight chunks
+        // fit its registers.  FP32 / BF16 rows keep one pair per wave: more
+        // blocks keep more of their bytes in flight.
+        if constexpr (BITS <= 8) {
+            if (jn <= 2 && c.w.rows >= 8 * 4 * 256) return launch_fused_fp_rpw<BITS, 8, kPairGated>(c, jn, stream);
+            if (jn <= 4 && c.w.rows >= 4 * 4 * 256) return launch_fused_fp_rpw<BITS, 4, kPairGated>(c, jn, stream);
+        }
+        return launch_fused_fp_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    }
     // tall int8 / int4 matrices: four rows per wave (the row read from LDS
     // serves more weight bytes), when the grid still covers the CUs
     if ((BITS == 8 || BITS == 4) && c.w.rows >= 4 * 4096) return launch_fused_fp_rpw<BITS, 4, kPairNone>(c, jn, stream);
