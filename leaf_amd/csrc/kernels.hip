@@ -1854,9 +1854,13 @@ void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
         }
         return launch_fused_fp_rpw<BITS, 2, kPairGated>(c, jn, stream);
     }
-    // tall int8 / int4 matrices: four rows per wave (the row read from LDS
-    // serves more weight bytes), when the grid still covers the CUs
-    if ((BITS == 8 || BITS == 4) && c.w.rows >= 4 * 4096) return launch_fused_fp_rpw<BITS, 4, kPairNone>(c, jn, stream);
+    // tall int8 / int4 matrices: four or eight rows per wave (the row staged
+    // in LDS by every block serves more weight bytes), when the grid still
+    // covers the CUs and the chunks fit the wave's registers
+    if constexpr (BITS == 8 || BITS == 4) {
+        if (jn <= 2 && c.w.rows >= 8 * 4 * 2048) return launch_fused_fp_rpw<BITS, 8, kPairNone>(c, jn, stream);
+        if (c.w.rows >= 4 * 4096) return launch_fused_fp_rpw<BITS, 4, kPairNone>(c, jn, stream);
+    }
     launch_fused_fp_rpw<BITS, 2, kPairNone>(c, jn, stream);
 }
 
