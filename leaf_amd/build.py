@@ -22,7 +22,7 @@ LIBRARY = PACKAGE / "libleafhip.so"
 EXECUTABLE = PACKAGE / "bin" / "leaf_decoder"
 ARCH = os.environ.get("LEAF_HIP_ARCH", "gfx950")
 
-SOURCES = ["kernels.hip", "gemm_w8a8.hip", "decode_step.hip", "reference_order.hip", "artifact_format.cpp", "runtime.cpp",
+SOURCES = ["kernels.hip", "gemm_w8a8.hip", "gemm_f32.hip", "decode_step.hip", "reference_order.hip", "artifact_format.cpp", "runtime.cpp",
            "session.cpp", "capi.cpp"]
 
 # -ffp-contract=off: every FMA in the kernels is explicit (fmaf), so the integer

@@ -120,6 +120,12 @@ void launch_gemm_w8a8_mfma(const int8_t* W, const float* w_scales, const float* 
 
 // Returns the path used (1 GEMV, 2 generic, 3 GEMM) or a negative value when
 // the call cannot run (missing scratch for the GEMM quantization).
+// FP32-math prefill GEMM on f32 MFMA with LDS-staged tiles (gemm_f32.hip):
+// K % 32 == 0, 16-byte aligned input and weights, quantized groups % 16 == 0.
+bool gemm_f32_lds_supported(const WeightView& w, const float* x);
+void launch_gemm_f32_lds(const WeightView& w, const float* x, int tokens, float* y, int epilogue,
+                         hipStream_t stream);
+
 int launch_linear(const LinearCall& call, hipStream_t stream);
 // True when launch_linear runs the single-token integer GEMV that normalizes,
 // quantizes and applies paired epilogues inside the kernel.

@@ -2087,6 +2087,10 @@ int launch_linear(const LinearCall& call, hipStream_t stream) {
         }
         return 1;
     }
+    if (path == 3 && !c.force_path && gemm_f32_lds_supported(w, c.x)) {
+        launch_gemm_f32_lds(w, c.x, c.tokens, c.y, c.epilogue, stream);
+        return 3;
+    }
     if (path == 3) {
         dim3 grid(ceil_div(w.rows, 64), ceil_div(c.tokens, 64));
         switch (w.bits) {
