@@ -210,12 +210,29 @@ void launch_tiles(const WeightView& w, const float* x, int tokens, float* y, int
 
 template <int BITS>
 void launch_bits(const WeightView& w, const float* x, int tokens, float* y, int epilogue, hipStream_t stream) {
-    // The largest tile that still gives 256 blocks: 128 tokens x 128 rows,
-    // then 128 x 64, then 64 x 64.
-    auto blocks = [&](int bm, int bn) { return ((tokens + bm - 1) / bm) * ((w.rows + bn - 1) / bn); };
-    if (blocks(128, 128) >= 256) launch_tiles<BITS, 4, 4>(w, x, tokens, y, epilogue, stream);
-    else if (blocks(128, 64) >= 256) launch_tiles<BITS, 4, 2>(w, x, tokens, y, epilogue, stream);
-    else launch_tiles<BITS, 2, 2>(w, x, tokens, y, epilogue, stream);
+    // Tile by the work of the busiest CU: ceil(blocks / 256 CUs) tiles of
+    // bm x bn, 64 x 64 tiles charged 10% for their lower MFMA density; ties
+    // go to the earlier tile.  (Measured at the Qwen / SmolLM2 prefill shapes:
+    // within 15% of the best of the four tiles, and 128 x 128 alone lost up
+    // to 1.8x where its grid covered the CUs 1.1 or 2.5 times.)
+    const int tiles[4][2] = {{128, 64}, {64, 128}, {128, 128}, {64, 64}};
+    int best = 0;
+    double best_cost = 0.0;
+    for (int i = 0; i < 4; ++i) {
+        const int bm = tiles[i][0], bn = tiles[i][1];
+        const long blocks = (long)((tokens + bm - 1) / bm) * ((w.rows + bn - 1) / bn);
+        const double cost = (double)((blocks + 255) / 256) * bm * bn * (i == 3 ? 1.1 : 1.0);
+        if (i == 0 || cost < best_cost) {
+            best = i;
+            best_cost = cost;
+        }
+    }
+    switch (best) {
+    case 0: launch_tiles<BITS, 4, 2>(w, x, tokens, y, epilogue, stream); break;
+    case 1: launch_tiles<BITS, 2, 4>(w, x, tokens, y, epilogue, stream); break;
+    case 2: launch_tiles<BITS, 4, 4>(w, x, tokens, y, epilogue, stream); break;
+    default: launch_tiles<BITS, 2, 2>(w, x, tokens, y, epilogue, stream); break;
+    }
 }
 
 }  // namespace
