@@ -52,6 +52,16 @@ __device__ __forceinline__ void int4_sixteenths(uint32_t word, float (&f)[8]) {
     f[7] = __builtin_amdgcn_cvt_off_f32_i4(odd >> 24);
 }
 
+// Barrier for LDS hand-offs between the waves of a block: waits for this
+// wave's LDS operations only (lgkmcnt(0)), so global loads into registers
+// stay in flight across it (__syncthreads also waits for those).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((7 << 4) | 15 | (3 << 14));   // lgkmcnt(0); vmcnt, expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Butterfly reductions across the 64 lanes of a wave; every lane gets the result.
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll

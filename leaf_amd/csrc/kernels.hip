@@ -1285,28 +1285,29 @@ constexpr int kPrefillLds = 2 * kPrefillKeys * kPrefillStride > (kPrefillSlices 
 
 // One thread's share of a 64 x 64 K (and V) tile: float4 i, i + kPrefillThreads, ...
 // Rows at or past `end` were never written (they may hold NaN, and a masked
-// key still multiplies its V row by 0): they are zeros.
+// key still multiplies its V row by 0): they load row 0 and are stored as
+// zeros.  (The loaded values are not touched until the store, so the loads
+// stay in flight while the current tile is used.)
 __device__ __forceinline__ void prefill_tile_load(const float* K, const float* V, int k0, int end,
                                                   v4f (&kr)[kPrefillLoads], v4f (&vr)[kPrefillLoads]) {
 #pragma unroll
     for (int j = 0; j < kPrefillLoads; ++j) {
         const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
         const int key = k0 + row;
-        const bool ok = key < end;
-        const size_t at = (size_t)(ok ? key : 0) * 64 + col;
-        const v4f kv = *(const v4f*)(K + at), vv = *(const v4f*)(V + at);
-        const v4f zero = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        kr[j] = ok ? kv : zero;
-        vr[j] = ok ? vv : zero;
+        const size_t at = (size_t)(key < end ? key : 0) * 64 + col;
+        kr[j] = *(const v4f*)(K + at);
+        vr[j] = *(const v4f*)(V + at);
     }
 }
 __device__ __forceinline__ void prefill_tile_store(float* ks, float* vs, const v4f (&kr)[kPrefillLoads],
-                                                   const v4f (&vr)[kPrefillLoads]) {
+                                                   const v4f (&vr)[kPrefillLoads], int k0, int end) {
 #pragma unroll
     for (int j = 0; j < kPrefillLoads; ++j) {
         const int f = threadIdx.x + kPrefillThreads * j, row = f / 16, col = 4 * (f % 16);
-        *(v4f*)(ks + row * kPrefillStride + col) = kr[j];
-        *(v4f*)(vs + row * kPrefillStride + col) = vr[j];
+        const bool ok = k0 + row < end;
+        const v4f zero = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        *(v4f*)(ks + row * kPrefillStride + col) = ok ? kr[j] : zero;
+        *(v4f*)(vs + row * kPrefillStride + col) = ok ? vr[j] : zero;
     }
 }
 
@@ -1346,17 +1347,28 @@ __device__ __forceinline__ void attention_prefill_item(const AttentionCall& p, i
     float m = -INFINITY, l = 0.0f;
     const float scale = p.scale;
     for (int k0 = first; k0 < end; k0 += kPrefillKeys) {
-        __syncthreads();   // the previous tile is no longer read
-        prefill_tile_store(ks, vs, kr, vr);
-        __syncthreads();
+        lds_barrier();     // the previous tile is no longer read (the next one's loads stay in flight)
+        prefill_tile_store(ks, vs, kr, vr, k0, end);
+        lds_barrier();
         if (k0 + kPrefillKeys < end) prefill_tile_load(K, V, k0 + kPrefillKeys, end, kr, vr);
         // the keys this wave can see in this tile
         const int wave_end = min(end, p.position + min(tw + 16, p.tokens));
         for (int sub = 16 * slice; sub < kPrefillKeys && k0 + sub < wave_end; sub += 16 * kPrefillSlices) {
             v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             const float* krow = ks + (sub + li) * kPrefillStride + lj;
+            float kv[16];   // all of the chain's K operands first: one LDS wait, not eight
 #pragma unroll
-            for (int c = 0; c < 16; ++c) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[4 * c], qv[c], sc, 0, 0, 0);
+            for (int c = 0; c < 16; ++c) kv[c] = krow[4 * c];
+            __builtin_amdgcn_sched_barrier(0);   // keep the reads batched ahead of the chain
+#pragma unroll
+            for (int c = 0; c < 16; ++c) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], sc, 0, 0, 0);
+            // the V operands of O^T += V^T P^T below, read while the softmax runs
+            float vv[4][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int dc = 0; dc < 4; ++dc) vv[r][dc] = vs[(sub + 4 * lj + r) * kPrefillStride + li + 16 * dc];
+            __builtin_amdgcn_sched_barrier(0);
             // lane: query q_tok, keys k0 + sub + 4 lj + r
             float e[4];
             float tile_max = -INFINITY;
@@ -1385,12 +1397,10 @@ __device__ __forceinline__ void attention_prefill_item(const AttentionCall& p, i
             for (int dc = 0; dc < 4; ++dc) o[dc] = o[dc] * alpha;
             // O^T += V^T P^T over keys {4 j + r}: lane supplies V[4 lj + r][16 dc + li]
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float* vrow = vs + (sub + 4 * lj + r) * kPrefillStride + li;
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
                 for (int dc = 0; dc < 4; ++dc)
-                    o[dc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * dc], e[r], o[dc], 0, 0, 0);
-            }
+                    o[dc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][dc], e[r], o[dc], 0, 0, 0);
         }
     }
     // merge the other slices' states into slice 0's wave of the same tokens
