@@ -58,8 +58,10 @@ void launch_scale_columns(const float* x, int rows, int width, const float* fact
 //    q_heads [heads, 1, dim] and k, v into the caches at `position`
 //    (rotary() and KVCache::append, decoder.cpp:1259-1281, 1332-1343);
 //  kPairGated: rows are a stacked [gate | up] projection; act[j] =
-//    up[j] * activate(gate[j]) (decoder.cpp:1396-1414).
-enum PairMode : int { kPairNone = 0, kPairRopeKv = 1, kPairGated = 2 };
+//    up[j] * activate(gate[j]) (decoder.cpp:1396-1414);
+//  kPairActivation (single-token FP linears only): not a pair, each row's
+//    output is stored as activate(value) (an ungated MLP's up projection).
+enum PairMode : int { kPairNone = 0, kPairRopeKv = 1, kPairGated = 2, kPairActivation = 3 };
 struct PairEpilogue {
     int mode = kPairNone;
     int heads = 0, kv_heads = 0, dim = 0, rotary = 0, position = 0, capacity = 0;

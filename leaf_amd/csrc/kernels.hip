@@ -774,7 +774,8 @@ template <int BITS, int RPW, int MAXJ, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, const float* __restrict__ x,
                                                               NormView norm, float* __restrict__ y, int epilogue,
                                                               PairEpilogue pe) {
-    static_assert(EPI == kPairNone || RPW % 2 == 0, "paired epilogues compute whole pairs");
+    constexpr bool kPaired = EPI == kPairRopeKv || EPI == kPairGated;
+    static_assert(!kPaired || RPW % 2 == 0, "paired epilogues compute whole pairs");
     constexpr int E = 128 / BITS;                    // weight values per 16-byte chunk
     constexpr int V = kFusedMaxV;                    // float4 of the row per thread
     __shared__ __align__(16) float lds_x[kFusedMaxK];
@@ -787,7 +788,7 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
     int rows_of[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) rows_of[r] = row_first + r;
-    if constexpr (EPI != kPairNone) {
+    if constexpr (kPaired) {
         // pair q = wave_index * RPW / 2 + i exists while 2 q < rows
 #pragma unroll
         for (int i = 0; i < RPW / 2; ++i)
@@ -869,9 +870,11 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
                 const float prev = epilogue == kAccumulate ? y[row] : 0.0f;
                 y[row] = epilogue == kAccumulate ? prev + vals[r] : vals[r];
             }
+        } else if constexpr (EPI == kPairActivation) {
+            if (lane == 0 && row < w.rows) y[row] = activate_value(pe.activation, vals[r]);
         }
     }
-    if constexpr (EPI != kPairNone) {
+    if constexpr (kPaired) {
 #pragma unroll
         for (int i = 0; i < RPW / 2; ++i)
             if (lane == 0 && row_first + 2 * i < w.rows)
@@ -1519,7 +1522,7 @@ __device__ __forceinline__ void merge_head_spans(const float* part, int splits, 
 // block writes (max, sum, out[dim]) per head; with `counters` the last span
 // of a KV head merges in place, otherwise attention_merge_kernel does.
 __global__ __launch_bounds__(kBlock) void attention_decode_kernel(AttentionCall p, int keys_per_split,
-                                                                 unsigned* counters) {
+                                                                 unsigned* counters, bool direct) {
     __shared__ __align__(16) float k_s[kDecodeKeys * (256 + 4)];
     __shared__ __align__(16) float v_s[kTileFloats];
     __shared__ __align__(16) float q_s[16 * 256];
@@ -1599,6 +1602,17 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(AttentionCall 
                 const float v = v_s[k * dim + d];
                 o0 = fmaf(e0[k], v, o0);
                 o1 = fmaf(e1[k], v, o1);
+            }
+            if (direct) {
+                // a single span: the merge would weigh it by exp(0) = 1, so
+                // its output is o / l, written here
+                const float l0 = l_s[g];
+                p.out[(size_t)(kvh * group + g) * dim + d] = l0 > 0.0f ? o0 / l0 : 0.0f;
+                if (two) {
+                    const float l1 = l_s[g2];
+                    p.out[(size_t)(kvh * group + g2) * dim + d] = l1 > 0.0f ? o1 / l1 : 0.0f;
+                }
+                continue;
             }
             float* part = p.partial + ((size_t)(kvh * group + g) * splits + split) * stride;
             part[2 + d] = o0;
@@ -1852,6 +1866,7 @@ void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
     constexpr int E = 128 / BITS;
     const int jn = (c.w.cols / E + kWave - 1) / kWave;
     if (c.pair.mode == kPairRopeKv) return launch_fused_fp_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
+    if (c.pair.mode == kPairActivation) return launch_fused_fp_rpw<BITS, 2, kPairActivation>(c, jn, stream);
     if (c.pair.mode == kPairGated) {
         // Tall int8 / int4 gate|up stacks (rows of few bytes): several pairs
         // per wave, so fewer blocks repeat the norm prologue, while the grid
@@ -1976,14 +1991,15 @@ bool fp_fuses(const LinearCall& c) {
     const bool quantized = w.bits == 8 || w.bits == 4;
     return w.cols % E == 0 && w.cols <= kFusedMaxK && w.cols / E <= 8 * kWave && (!quantized || w.group % E == 0) &&
            (c.force_path == 0 || c.force_path == 1) && (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 &&
-           (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 && (c.pair.mode == kPairNone || w.rows % 2 == 0);
+           (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 &&
+           (c.pair.mode == kPairNone || c.pair.mode == kPairActivation || w.rows % 2 == 0);
 }
 
 bool linear_fuses(const LinearCall& c) {
     const WeightView& w = c.w;
     const int E8 = w.bits == 8 ? 16 : 32;
     if (!c.integer_activations) return fp_fuses(c);
-    return (w.bits == 8 || w.bits == 4) && c.tokens == 1 && c.x && !c.xq &&
+    return (w.bits == 8 || w.bits == 4) && c.tokens == 1 && c.x && !c.xq && c.pair.mode != kPairActivation &&
            w.group == w.cols && w.cols % E8 == 0 && w.cols <= kFusedMaxK &&
            (c.force_path == 0 || c.force_path == 1) && (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 && (c.pair.mode == kPairNone || w.rows % 2 == 0);
@@ -2133,8 +2149,13 @@ bool launch_attention(const AttentionCall& call, hipStream_t stream) {
             // A separate merge launch is cheaper here than merging in the last
             // block: that needs device-scope release/acquire fences, which
             // write back and invalidate L2 on every block (measured ~5 us/layer).
-            attention_decode_kernel<<<dim3(call.kv_heads, splits), kBlock, 0, stream>>>(call, per_split, nullptr);
-            attention_merge_spans_kernel<<<call.heads, kMergeThreads, splits * sizeof(float), stream>>>(call, splits);
+            // One span (a short context) writes the output itself.
+            const bool direct = splits == 1;
+            attention_decode_kernel<<<dim3(call.kv_heads, splits), kBlock, 0, stream>>>(call, per_split, nullptr,
+                                                                                   direct);
+            if (!direct)
+                attention_merge_spans_kernel<<<call.heads, kMergeThreads, splits * sizeof(float), stream>>>(call,
+                                                                                                        splits);
             return true;
         }
     }

@@ -819,16 +819,22 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             if (!fuse_act && !prequantizes(L.down, rows))
                 timed(Profiler::Other, 0, 0, [&] { activation(gate_up, rows, f, 1, act); });
         } else {
-            // ungated MLP: a single-token FP up projection normalizes its input itself
+            // ungated MLP: a single-token FP up projection normalizes its input
+            // itself and stores activate(value) straight into act
+            PairEpilogue activated;
+            activated.mode = kPairActivation;
+            activated.activation = int(c.activation);
             const bool fuse_up = rows == 1 && !reference_ && !model.integer_linear(L.up) &&
-                                 linear_fuses(make_call(L.up, hid, rows, gate_up, kStore, &L.post_norm));
+                                 linear_fuses([&] { LinearCall t = make_call(L.up, hid, rows, act, kStore,
+                                                                             &L.post_norm);
+                                                    t.pair = activated; return t; }());
             if (fuse_up) {
-                run_linear(L.up, hid, rows, gate_up, kStore, &L.post_norm);
+                run_linear(L.up, hid, rows, act, kStore, &L.post_norm, &activated);
             } else {
                 norm(hid, rows, h, L.post_norm, normed);
                 run_linear(L.up, normed, rows, gate_up, kStore, nullptr);
+                activation(gate_up, rows, f, 0, act);
             }
-            activation(gate_up, rows, f, 0, act);
         }
         const bool down_q = c.gated && prequantizes(L.down, rows) &&
                             !(rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up);
