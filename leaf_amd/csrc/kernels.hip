@@ -1382,8 +1382,8 @@ __device__ __forceinline__ void attention_prefill_item(const AttentionCall& p, i
                 e[r] = ok ? sc[r] * scale * scale : -INFINITY;
                 tile_max = fmaxf(tile_max, e[r]);
             }
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
+            tile_max = max_xor16(tile_max);
+            tile_max = max_xor32(tile_max);
             const float m_new = fmaxf(m, tile_max);
             const float alpha = m_new == -INFINITY ? 1.0f : expf(m - m_new);
             float tile_sum = 0.0f;
@@ -1392,8 +1392,8 @@ __device__ __forceinline__ void attention_prefill_item(const AttentionCall& p, i
                 e[r] = m_new == -INFINITY ? 0.0f : expf(e[r] - m_new);
                 tile_sum += e[r];
             }
-            tile_sum += __shfl_xor(tile_sum, 16, kWave);
-            tile_sum += __shfl_xor(tile_sum, 32, kWave);
+            tile_sum = add_xor16(tile_sum);
+            tile_sum = add_xor32(tile_sum);
             l = l * alpha + tile_sum;
             m = m_new;
 #pragma unroll
