@@ -23,6 +23,9 @@
 // instruction fills 8 rows x 128 bytes, lane l fetching row l / 8, segment
 // (l % 8) ^ (l / 8)).  BF16 / int8 / int4 weights are loaded into registers
 // one stage ahead, widened or dequantized, and written to their slots.
+#include <cstdlib>
+#include <cstring>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -208,6 +211,17 @@ void launch_tiles(const WeightView& w, const float* x, int tokens, float* y, int
     gemm_f32_lds_kernel<BITS, WTM, WTN><<<grid, kThreads, 0, stream>>>(w, x, tokens, y, epilogue);
 }
 
+// LEAF_F32_GEMM_TILE=128x64|64x128|128x128|64x64 (tokens x rows) forces a
+// tile (tests compare them); any other value, or none, lets the cost decide.
+int forced_tile() {
+    const char* v = getenv("LEAF_F32_GEMM_TILE");
+    if (!v) return -1;
+    const char* names[4] = {"128x64", "64x128", "128x128", "64x64"};
+    for (int i = 0; i < 4; ++i)
+        if (strcmp(v, names[i]) == 0) return i;
+    return -1;
+}
+
 template <int BITS>
 void launch_bits(const WeightView& w, const float* x, int tokens, float* y, int epilogue, hipStream_t stream) {
     // Tile by the work of the busiest CU: ceil(blocks / 256 CUs) tiles of
@@ -227,6 +241,8 @@ void launch_bits(const WeightView& w, const float* x, int tokens, float* y, int 
             best_cost = cost;
         }
     }
+    const int forced = forced_tile();
+    if (forced >= 0) best = forced;
     switch (best) {
     case 0: launch_tiles<BITS, 4, 2>(w, x, tokens, y, epilogue, stream); break;
     case 1: launch_tiles<BITS, 2, 4>(w, x, tokens, y, epilogue, stream); break;

@@ -227,6 +227,34 @@ def test_fp_linear_within_tolerance(rt, oracle, bits, M):
     assert np.all(np.abs(y - ref) <= 4e-5 * (1 + np.abs(ref)))
 
 
+@pytest.mark.parametrize("bits", [32, 16, 8, 4])
+def test_f32_gemm_tiles_agree_bit_exactly(rt, oracle, monkeypatch, bits):
+    # The LDS-staged f32 GEMM runs the same MFMA sequence per output in every
+    # tile shape, so all four tiles must give the same bits, on ragged token
+    # and row counts (partial tiles at both edges), and stay within the FP
+    # linear tolerance of the oracle.
+    rng = np.random.default_rng(700 + bits)
+    M, K, N = 300, 896, 200
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    data, scales, group = fp_case(bits, w, K)
+    b = rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    dw = rt.DeviceWeight(data, bits, K, scales, group, b)
+    dx = rt.DeviceArray.of(x)
+    outs = {}
+    for tile in ("128x64", "64x128", "128x128", "64x64"):
+        monkeypatch.setenv("LEAF_F32_GEMM_TILE", tile)
+        dy = rt.DeviceArray((M, N), np.float32)
+        rt.linear(dw, dx, M, 32, dy)
+        outs[tile] = dy.numpy()
+    monkeypatch.delenv("LEAF_F32_GEMM_TILE")
+    first = outs["128x64"]
+    for tile, y in outs.items():
+        assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), tile
+    ref = oracle.linear_fp(bits, N, K, group, data, scales, b, x)
+    assert np.all(np.abs(first - ref) <= 4e-5 * (1 + np.abs(ref)))
+
+
 def test_norms_within_tolerance(rt, oracle):
     from leaf_amd.runtime import check, library
     rng = np.random.default_rng(9)
