@@ -659,6 +659,64 @@ def summarize_trace(db: Path, top: int = 25) -> str:
     return "\n".join(lines)
 
 
+def summarize_config_trace(db: Path) -> str:
+    """Markdown tables from a rocprofv3 --kernel-trace run of the configuration
+    benchmarks (graph replays traced as plain launches): for one decode step in
+    the middle of each configuration's greedy run, every kernel's time per
+    token, and the decode attention's read rate over the K and V rows of the
+    visible keys.  A step is the kernels after one step's argmax launches up to
+    and including the next step's; its configuration is told by the weight
+    format of its fused GEMV."""
+    import re
+    import sqlite3
+    from leaf_amd.models import PRESETS
+    con = sqlite3.connect(str(db))
+    rows = con.execute("select name, duration from kernels order by start").fetchall()
+    con.close()
+    clean = lambda n: re.sub(r"leafhip::|\(anonymous namespace\)::|void ", "", n).split("(")[0]   # noqa: E731
+    meta, _ = golden()
+    by_bits = {"<32,": "gpt2", "<4,": "qwen", "<16,": "smollm2"}
+    # a step ends with its argmax launches (one, or the chunks and their combine)
+    argmax = [i for i, r in enumerate(rows)
+              if "argmax" in r[0] and (i + 1 == len(rows) or "argmax" not in rows[i + 1][0])]
+    steps: dict = {}
+    for a, b in zip(argmax, argmax[1:]):
+        names = [clean(rows[i][0]) for i in range(a + 1, b + 1)]
+        if any("gemm" in n for n in names) or len(names) < 8:
+            continue                                 # a prefill, or not a decode step
+        fused = next((n for n in names if n.startswith("gemv_fp_fused_kernel")), "")
+        family = next((f for k, f in by_bits.items() if fused.startswith("gemv_fp_fused_kernel" + k)), None)
+        if family:
+            steps.setdefault(family, []).append((a, b))
+    out = []
+    for family in ("gpt2", "qwen", "smollm2"):
+        if family not in steps:
+            continue
+        spec, m = PRESETS[family](), meta[family]
+        idx = len(steps[family]) // 2
+        a, b = steps[family][idx]
+        ctx = m["prompt_tokens"] + idx + 1
+        per: dict = {}
+        for i in range(a + 1, b + 1):
+            t = per.setdefault(clean(rows[i][0]), [0, 0.0])
+            t[0] += 1
+            t[1] += rows[i][1] / 1e3
+        total = sum(t[1] for t in per.values())
+        kv_bytes = 2 * spec.kv_heads * spec.head_dim * 4 * ctx   # one layer's K and V rows
+        out += [f"**{family}** (decode step {idx + 1} of {len(steps[family])} traced, {ctx} keys): "
+                f"{total:.1f} us of kernel time per token", "",
+                "| Kernel | Calls per token | us per token | us per call |", "|---|---:|---:|---:|"]
+        for name, (calls, us) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+            out.append(f"| `{name}` | {calls} | {us:.1f} | {us / calls:.2f} |")
+        att = per.get("attention_decode_kernel")
+        if att:
+            gbps = kv_bytes * att[0] / (att[1] * 1e3)
+            out += ["", f"Decode attention: {kv_bytes / 1e6:.2f} MB of K and V per layer, "
+                    f"{att[1] / att[0]:.2f} us per call: {gbps:.0f} GB/s ({gbps / HBM_PEAK_GBS:.3f} of 8 TB/s)."]
+        out.append("")
+    return "\n".join(out)
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -673,9 +731,13 @@ def main() -> int:
     parser.add_argument("--derive-traffic", type=Path, default=None)
     parser.add_argument("--derive-prefill-counters", type=Path, default=None)
     parser.add_argument("--summarize-trace", type=Path, default=None)
+    parser.add_argument("--summarize-config-trace", type=Path, default=None)
     args = parser.parse_args()
     if args.summarize_trace is not None:
         print(summarize_trace(args.summarize_trace))
+        return 0
+    if args.summarize_config_trace is not None:
+        print(summarize_config_trace(args.summarize_config_trace))
         return 0
     if args.derive_prefill_counters is not None:
         print(json.dumps(derive_prefill_counters(args.derive_prefill_counters), indent=1))

@@ -180,9 +180,14 @@ void launch_residual(float* hidden, const float* a, const float* b, int count, h
 // index of the first maximum of each row (std::max_element, main_decoder.cpp:102)
 void launch_argmax(const float* logits, int rows, int width, uint32_t* out, hipStream_t stream);
 // Greedy step on the device: argmax of one row into next_id[0] and host_out[0]
-// (mapped host memory, may be null), then position[0] += 1.
+// (mapped host memory, may be null), then position[0] += 1.  Many blocks take
+// a part of the row each, a second launch combines their results; scratch
+// holds argmax_scratch_floats() floats.
 void launch_argmax_advance(const float* logits, int width, uint32_t* next_id, uint32_t* host_out, int* position,
-                           hipStream_t stream);
+                           float* scratch, hipStream_t stream);
+// The same for one row without the greedy step.
+void launch_argmax_row(const float* logits, int width, uint32_t* out, float* scratch, hipStream_t stream);
+int argmax_scratch_floats();
 // Number of key spans the decode attention uses for `keys` visible keys.
 int attention_decode_spans(int keys, int dim);
 // Whether single-token attention runs the span kernels (graph-capturable).

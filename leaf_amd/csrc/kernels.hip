@@ -1774,6 +1774,7 @@ __global__ void residual_kernel(float* hidden, const float* a, const float* b, i
 }
 
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxMaxBlocks = 256;
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* logits, int width, uint32_t* out,
                                                                 uint32_t* host_out, int* position) {
     __shared__ float bv[kArgmaxThreads / kWave];
@@ -1813,6 +1814,52 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
         if (host_out) host_out[blockIdx.x] = (uint32_t)index;
         if (position) *position += 1;
     }
+}
+
+// One row's argmax over many blocks: block b takes columns [b chunk,
+// (b + 1) chunk) with argmax_kernel's rule (greater, or equal at a lower
+// index) and stores its (value, index) in scratch[2 b], then one wave of
+// argmax_combine_kernel combines the blocks' results in block order with the
+// same rule, so the index is the first maximum as with one block.  (Two
+// launches: a last-block combine needs agent-scope fences, which cost more.)
+constexpr int kArgmaxChunkThreads = 256;
+struct ArgmaxBest {
+    float best = -INFINITY;
+    int index;
+    __device__ explicit ArgmaxBest(int width) : index(width) {}
+    __device__ __forceinline__ void take(float v, int c, int width) {
+        if (c != width && (index == width || v > best || (v == best && c < index))) { best = v; index = c; }
+    }
+};
+__global__ __launch_bounds__(kArgmaxChunkThreads) void argmax_chunks_kernel(const float* logits, int width, int chunk,
+                                                                           float* scratch) {
+    __shared__ float bv[kArgmaxChunkThreads / kWave];
+    __shared__ int bi[kArgmaxChunkThreads / kWave];
+    const int c0 = blockIdx.x * chunk, c1 = min(width, c0 + chunk);
+    ArgmaxBest r(width);
+    for (int c = c0 + threadIdx.x; c < c1; c += kArgmaxChunkThreads) r.take(logits[c], c, width);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) r.take(__shfl_xor(r.best, o, kWave), __shfl_xor(r.index, o, kWave), width);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { bv[wave] = r.best; bi[wave] = r.index; }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w2 = 1; w2 < kArgmaxChunkThreads / kWave; ++w2) r.take(bv[w2], bi[w2], width);
+    scratch[2 * blockIdx.x] = r.best;
+    scratch[2 * blockIdx.x + 1] = __int_as_float(r.index);
+}
+__global__ __launch_bounds__(kWave) void argmax_combine_kernel(const float* scratch, int blocks, int width,
+                                                             uint32_t* out, uint32_t* host_out, int* position) {
+    // lane l takes blocks l, l + 64, ... in order, then the lanes combine in
+    // lane order: every candidate meets the rule in block order
+    ArgmaxBest r(width);
+    for (int b = threadIdx.x; b < blocks; b += kWave) r.take(scratch[2 * b], __float_as_int(scratch[2 * b + 1]), width);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) r.take(__shfl_xor(r.best, o, kWave), __shfl_xor(r.index, o, kWave), width);
+    if (threadIdx.x != 0) return;
+    out[0] = (uint32_t)r.index;
+    if (host_out) host_out[0] = (uint32_t)r.index;
+    if (position) *position += 1;
 }
 
 int ceil_div(size_t a, size_t b) { return (int)((a + b - 1) / b); }
@@ -2192,9 +2239,24 @@ void launch_residual(float* hidden, const float* a, const float* b, int count, h
     residual_kernel<<<std::min(ceil_div(count, kBlock), 8192), kBlock, 0, stream>>>(hidden, a, b, count);
 }
 
+int argmax_scratch_floats() { return 2 * kArgmaxMaxBlocks; }
+
+// Blocks of at least 1024 columns, at most kArgmaxMaxBlocks of them.
+static void launch_argmax_chunks(const float* logits, int width, uint32_t* out, uint32_t* host_out, int* position,
+                                 float* scratch, hipStream_t stream) {
+    const int blocks = std::max(1, std::min(kArgmaxMaxBlocks, ceil_div(width, 1024)));
+    const int chunk = ceil_div(width, blocks);
+    argmax_chunks_kernel<<<blocks, kArgmaxChunkThreads, 0, stream>>>(logits, width, chunk, scratch);
+    argmax_combine_kernel<<<1, kWave, 0, stream>>>(scratch, blocks, width, out, host_out, position);
+}
+
 void launch_argmax_advance(const float* logits, int width, uint32_t* next_id, uint32_t* host_out, int* position,
-                           hipStream_t stream) {
-    argmax_kernel<<<1, kArgmaxThreads, 0, stream>>>(logits, width, next_id, host_out, position);
+                           float* scratch, hipStream_t stream) {
+    launch_argmax_chunks(logits, width, next_id, host_out, position, scratch, stream);
+}
+
+void launch_argmax_row(const float* logits, int width, uint32_t* out, float* scratch, hipStream_t stream) {
+    launch_argmax_chunks(logits, width, out, nullptr, nullptr, scratch, stream);
 }
 
 bool attention_decode_supported(int heads, int kv_heads, int dim) {

@@ -240,7 +240,7 @@ private:
     hipStream_t stream() const { return model.context.stream; }
     DeviceBuffer kv_, rope_cos_, rope_sin_;
     DeviceBuffer hidden_, normed_, qkv_, q_heads_, attn_, attn_proj_, gate_up_, act_, proj_, logits_, xq_, xs_;
-    DeviceBuffer ids_, argmax_, partial_, scaled_, counters_, split_;
+    DeviceBuffer ids_, argmax_, argmax_scratch_, partial_, scaled_, counters_, split_;
     uint32_t logits_rows_ = 0;
     uint32_t* host_ids_ = nullptr;   // pinned staging for token ids
     uint32_t* host_argmax_ = nullptr;

@@ -131,6 +131,8 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t 
     counters_.allocate(size_t(c.kv_heads) * sizeof(unsigned));
     hip_check(hipMemset(counters_.ptr, 0, counters_.bytes), "hipMemset");
     grow<uint32_t>(argmax_, 1);
+    argmax_scratch_.allocate(size_t(argmax_scratch_floats()) * sizeof(float));
+    hip_check(hipMemset(argmax_scratch_.ptr, 0, argmax_scratch_.bytes), "hipMemset");
     hip_check(hipHostMalloc((void**)&host_argmax_, sizeof(uint32_t), hipHostMallocMapped), "hipHostMalloc");
     hip_check(hipHostGetDevicePointer((void**)&mapped_argmax_, host_argmax_, 0), "hipHostGetDevicePointer");
     hip_check(hipHostMalloc((void**)&host_position_, sizeof(int)), "hipHostMalloc");
@@ -313,8 +315,8 @@ void Session::forward(const uint32_t* ids, size_t count, bool all_logits, float*
     launch(int(count), length, all_logits, nullptr, 0);
     const int head_rows = all_logits ? int(count) : 1;
     float* logits = logits_.as<float>();
-    launch_argmax(logits + size_t(head_rows - 1) * model.config.vocab, 1, int(model.config.vocab),
-                  argmax_.as<uint32_t>(), s);
+    launch_argmax_row(logits + size_t(head_rows - 1) * model.config.vocab, int(model.config.vocab),
+                      argmax_.as<uint32_t>(), argmax_scratch_.as<float>(), s);
     hip_check(hipMemcpyAsync(host_argmax_, argmax_.ptr, sizeof(uint32_t), hipMemcpyDeviceToHost, s), "argmax copy");
     if (host_logits)
         hip_check(hipMemcpyAsync(host_logits, logits, size_t(head_rows) * model.config.vocab * sizeof(float),
@@ -362,7 +364,7 @@ void Session::decode_graphed(uint32_t id, bool upload_id, float* host_logits, ui
         try {
             launch(1, length, false, position_.as<int>(), bucket);
             launch_argmax_advance(logits_.as<float>(), int(c.vocab), ids_.as<uint32_t>(), mapped_argmax_,
-                                  position_.as<int>(), s);
+                                  position_.as<int>(), argmax_scratch_.as<float>(), s);
         } catch (...) {
             (void)hipStreamEndCapture(s, &graph);
             throw;
