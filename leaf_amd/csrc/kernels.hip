@@ -1904,7 +1904,10 @@ void launch_fused_fp_rpw(const LinearCall& c, int jn, hipStream_t stream) {
     if (jn <= 1) LEAF_FUSED_FP(1);
     else if (jn <= 2) LEAF_FUSED_FP(2);
     else if (jn <= 4) LEAF_FUSED_FP(4);
-    else LEAF_FUSED_FP(8);
+    else if (jn <= 8) LEAF_FUSED_FP(8);
+    else {
+        if constexpr (RPW == 1) LEAF_FUSED_FP(16);   // long rows: one row per wave (launch_fused_fp)
+    }
 #undef LEAF_FUSED_FP
 }
 
@@ -1912,6 +1915,8 @@ template <int BITS>
 void launch_fused_fp(const LinearCall& c, hipStream_t stream) {
     constexpr int E = 128 / BITS;
     const int jn = (c.w.cols / E + kWave - 1) / kWave;
+    // rows of 9-16 chunks per lane (fp_fuses: no pair epilogue): one per wave
+    if (jn > 8) return launch_fused_fp_rpw<BITS, 1, kPairNone>(c, jn, stream);
     if (c.pair.mode == kPairRopeKv) return launch_fused_fp_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
     if (c.pair.mode == kPairActivation) return launch_fused_fp_rpw<BITS, 2, kPairActivation>(c, jn, stream);
     if (c.pair.mode == kPairGated) {
@@ -2029,14 +2034,16 @@ void launch_scale_columns(const float* x, int rows, int width, const float* fact
 }
 
 // The single-token FP GEMV with the norm (and a paired epilogue) fused in:
-// whole 16-byte chunks, at most 8 per lane, scale groups of whole chunks.
+// whole 16-byte chunks, at most 8 per lane (16 without a pair epilogue),
+// scale groups of whole chunks.
 bool fp_fuses(const LinearCall& c) {
     const WeightView& w = c.w;
     if (c.integer_activations || c.tokens != 1 || !c.x || c.xq) return false;
     if (w.bits != 32 && w.bits != 16 && w.bits != 8 && w.bits != 4) return false;
     const int E = 128 / w.bits;
     const bool quantized = w.bits == 8 || w.bits == 4;
-    return w.cols % E == 0 && w.cols <= kFusedMaxK && w.cols / E <= 8 * kWave && (!quantized || w.group % E == 0) &&
+    const int max_chunks = (c.pair.mode == kPairNone ? 16 : 8) * kWave;
+    return w.cols % E == 0 && w.cols <= kFusedMaxK && w.cols / E <= max_chunks && (!quantized || w.group % E == 0) &&
            (c.force_path == 0 || c.force_path == 1) && (reinterpret_cast<uintptr_t>(c.x) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(w.data) & 15) == 0 &&
            (c.pair.mode == kPairNone || c.pair.mode == kPairActivation || w.rows % 2 == 0);

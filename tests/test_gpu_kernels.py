@@ -227,6 +227,26 @@ def test_fp_linear_within_tolerance(rt, oracle, bits, M):
     assert np.all(np.abs(y - ref) <= 4e-5 * (1 + np.abs(ref)))
 
 
+@pytest.mark.parametrize("bits,K", [(32, 3072), (16, 5632), (32, 1028)])
+def test_fp_single_token_long_rows_within_tolerance(rt, oracle, bits, K):
+    # One token over rows of 9-16 chunks per lane (GPT-2's 3072-wide MLP
+    # output projection, BF16 at 5632) and a width with a partial last chunk
+    # pass: the fused GEMV's one-row-per-wave variant, against the oracle.
+    rng = np.random.default_rng(bits + K)
+    N = 300
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    data, scales, group = fp_case(bits, w, K)
+    b = rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    dw = rt.DeviceWeight(data, bits, K, scales, group, b)
+    dx = rt.DeviceArray.of(x)
+    dy = rt.DeviceArray((1, N), np.float32)
+    rt.linear(dw, dx, 1, 32, dy)
+    ref = oracle.linear_fp(bits, N, K, group, data, scales, b, x)
+    y = dy.numpy()
+    assert np.all(np.abs(y - ref) <= 4e-5 * (1 + np.abs(ref)))
+
+
 @pytest.mark.parametrize("bits", [32, 16, 8, 4])
 def test_f32_gemm_tiles_agree_bit_exactly(rt, oracle, monkeypatch, bits):
     # The LDS-staged f32 GEMM runs the same MFMA sequence per output in every
