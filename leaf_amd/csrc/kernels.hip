@@ -777,7 +777,10 @@ __global__ __launch_bounds__(kBlock) void gemv_fp_fused_kernel(WeightView w, con
     constexpr bool kPaired = EPI == kPairRopeKv || EPI == kPairGated;
     static_assert(!kPaired || RPW % 2 == 0, "paired epilogues compute whole pairs");
     constexpr int E = 128 / BITS;                    // weight values per 16-byte chunk
-    constexpr int V = kFusedMaxV;                    // float4 of the row per thread
+    // float4 of the row per thread: enough for the widest row this MAXJ takes
+    // (64 MAXJ chunks of E values), so short rows do not hold registers for
+    // the longest
+    constexpr int V = (MAXJ * E + 15) / 16 < kFusedMaxV ? (MAXJ * E + 15) / 16 : kFusedMaxV;
     __shared__ __align__(16) float lds_x[kFusedMaxK];
     __shared__ float red[16];
     __shared__ double dred[16];
