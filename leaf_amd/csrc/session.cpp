@@ -345,7 +345,9 @@ void Session::decode_graphed(uint32_t id, bool upload_id, float* host_logits, ui
     hipStream_t s = stream();
     const int needed = attention_decode_spans(int(length) + 1, int(c.head_dim));
     const int most = attention_decode_spans(int(capacity), int(c.head_dim));
-    int bucket = 4;
+    // Span buckets of 1, 2, 4, 8, ... spans, one captured graph each: a context
+    // of one span runs its attention without the merge launch.
+    int bucket = 1;
     while (bucket < needed) bucket *= 2;
     bucket = std::min(bucket, most);
     if (!device_position_valid_) {

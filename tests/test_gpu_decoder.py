@@ -123,12 +123,14 @@ def test_rejects_corrupt_artifacts(runtime, tmp_path, artifacts):
 
 
 @pytest.mark.parametrize("family,prompt_tokens", [("gpt2", 150), ("tinyllama", 230), ("qwen", 230),
-                                                  ("smollm2", 230)])
+                                                  ("smollm2", 230), ("gpt2", 20), ("qwen", 20)])
 def test_graph_replayed_decode_is_bit_identical_to_eager(runtime, artifacts, monkeypatch, family, prompt_tokens):
     """Single-token steps replay a captured graph per attention-span bucket
     (device-resident position, device argmax feeding the next id); the result
     must not differ by a bit from launching the same kernels one by one,
-    across bucket boundaries and after a reset."""
+    across bucket boundaries and after a reset.  20-token prompts start in
+    the one-span bucket (attention without a merge launch) and cross into
+    two spans at 64 keys."""
     from leaf_amd import models
     bits, math = models.RUN_POLICY[family]
     rng = np.random.default_rng(5)
