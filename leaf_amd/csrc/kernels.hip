@@ -525,7 +525,7 @@ template <int BITS, int RPW, int MAXJ, int EPI, bool SEQ = false>
 __global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, const float* __restrict__ x, NormView norm,
                                                                float* __restrict__ y, int epilogue,
                                                                int32_t* __restrict__ acc_out, PairEpilogue pe) {
-    static_assert(EPI == kPairNone || RPW == 2, "paired epilogues compute two rows per wave");
+    static_assert(EPI == kPairNone || RPW % 2 == 0, "paired epilogues compute pairs of rows");
     constexpr int E = BITS == 8 ? 16 : 32;          // weight values per 16-byte chunk
     __shared__ __align__(16) int8_t lds_q[kFusedMaxK];
     // the row's terms for sequential sums (K <= MAXJ * 64 * E columns)
@@ -540,7 +540,11 @@ __global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, co
 #pragma unroll
     for (int r = 0; r < RPW; ++r) rows_of[r] = row_first + r;
     if constexpr (EPI != kPairNone) {
-        if (row_first < w.rows) pair_rows(pe, wave_index, rows_of[0], rows_of[1]);
+        // RPW / 2 pairs per wave; pair i's rows go to rows_of[2i], rows_of[2i + 1]
+        // (a pair past the last one keeps rows past w.rows: nothing is stored)
+#pragma unroll
+        for (int i = 0; i < RPW / 2; ++i)
+            if (row_first + 2 * i < w.rows) pair_rows(pe, wave_index * (RPW / 2) + i, rows_of[2 * i], rows_of[2 * i + 1]);
     }
 
     // Small L2-resident operands first (row slice, norm parameters, this
@@ -604,7 +608,10 @@ __global__ __launch_bounds__(kBlock) void gemv_int_fused_kernel(WeightView w, co
         }
     }
     if constexpr (EPI != kPairNone) {
-        if (lane == 0) pair_store(pe, rows_of[0], vals[0] + bw[0], rows_of[1], vals[1] + bw[1]);
+#pragma unroll
+        for (int i = 0; i < RPW / 2; ++i)
+            if (lane == 0 && row_first + 2 * i < w.rows)
+                pair_store(pe, rows_of[2 * i], vals[2 * i] + bw[2 * i], rows_of[2 * i + 1], vals[2 * i + 1] + bw[2 * i + 1]);
     }
 }
 
@@ -1891,7 +1898,14 @@ void launch_fused_int(const LinearCall& c, hipStream_t stream) {
     const int nch = c.w.cols / E;
     const int jn = (nch + kWave - 1) / kWave;
     if (c.pair.mode == kPairRopeKv) return launch_fused_int_rpw<BITS, 2, kPairRopeKv>(c, jn, stream);
-    if (c.pair.mode == kPairGated) return launch_fused_int_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    if (c.pair.mode == kPairGated) {
+        // A column-order norm sum is a long chain in every block: two pairs
+        // per wave halve the blocks, so that a tall gate|up matrix runs in
+        // one round of resident blocks.
+        if (c.norm.kind >= 0 && c.norm.sequential && c.w.rows >= 8192 && jn <= 2)
+            return launch_fused_int_seq<BITS, 4, kPairGated, true>(c, jn, stream);
+        return launch_fused_int_rpw<BITS, 2, kPairGated>(c, jn, stream);
+    }
     // Enough blocks to cover the CUs, and more rows per wave for tall matrices
     // so the per-block prologue is amortized.
     if (c.w.rows >= 8192 && jn <= 2) launch_fused_int_rpw<BITS, 4, kPairNone>(c, jn, stream);

@@ -161,10 +161,11 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 //   * Scores: thread k takes keys k, k + 256, ...; the next key's row loads
 //     into registers while the current one is summed (q . k in column order,
 //     q read from LDS).
+//   * Exponentials: four independent keys per thread at a time.
 //   * Output: output[d] = (...(p_0 v_0[d]) + p_1 v_1[d]) + ...) in key order.
 //     The products are independent of the running sum.  The V rows of up to
 //     kRoRound keys are loaded into registers (all threads, coalesced) while
-//     the exponentials and the denominator are formed; then, chunk by chunk,
+//     the denominator is formed; then, chunk by chunk,
 //     all threads write p_k * v_k[d] into an LDS buffer and wave 0 adds a
 //     chunk's products in key order (lane d, output element d) while the
 //     other threads fill the second buffer.
@@ -251,10 +252,24 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
                             : v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
-    load_round(0);   // lands while the exponentials and the denominator are formed
-    // every thread exponentiates the scores it formed
-    for (int k = tid; k < n; k += kRoBlock) sc[k] = libm_expf(sc[k] - maximum);
+    // exponentials, four keys per thread at a time (their table reads overlap)
+    for (int k0 = 0; k0 < n; k0 += 4 * kRoBlock) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = sc[min(k0 + tid + kRoBlock * i, n - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = libm_expf(e[i] - maximum);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = k0 + tid + kRoBlock * i;
+            if (k < n) sc[k] = e[i];
+        }
+    }
     __syncthreads();   // every e is written
+    // The first round of V lands while the denominator is summed.  (Issued
+    // before the exponentials, it would make each table read wait for it:
+    // loads complete in order.)
+    load_round(0);
     // masked keys add exp(-inf) = 0, which leaves the sum unchanged
     if (tid == 0) den_shared = sequential_sum(sc, n);
     __syncthreads();

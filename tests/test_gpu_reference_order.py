@@ -77,7 +77,8 @@ def test_norms_bit_exact(rt, oracle, width):
 
 
 @pytest.mark.parametrize("tokens,position,window,heads,kv", [
-    (1, 640, 0, 32, 4), (1, 4351, 0, 14, 2), (1, 700, 64, 14, 2), (37, 0, 0, 14, 2), (13, 21, 0, 15, 5),
+    (1, 640, 0, 32, 4), (1, 4351, 0, 14, 2), (1, 700, 64, 14, 2), (1, 0, 0, 14, 2), (1, 300, 0, 32, 4),
+    (1, 9000, 0, 8, 1), (37, 0, 0, 14, 2), (13, 21, 0, 15, 5),
     (16, 5, 7, 14, 2), (512, 0, 0, 32, 4), (200, 300, 0, 32, 4), (130, 100, 64, 14, 2)])
 def test_attention_bit_exact(rt, oracle, tokens, position, window, heads, kv):
     from leaf_amd.runtime import check, library
