@@ -295,22 +295,31 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
                 r[1] = pk * v[1];
                 r[2] = pk * v[2];
                 r[3] = pk * v[3];
-                *reinterpret_cast<v4f*>(dst + 4 * f) = r;
+                // Four 4-byte stores (16-byte LDS accesses of 64 lanes ran
+                // several times slower per byte here).  Element d of key kl
+                // sits at kl * D + (d ^ (kl % 4)): the 64 lanes of a store
+                // (keys 4 j .. 4 j + 3, one e) meet 64 different banks.
+                const int swz = (f / (D / 4)) & 3;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    asm volatile("" ::: "memory");
+                    dst[4 * f + (e ^ swz)] = r[e];
+                }
             }
             __syncthreads();   // the chunk's products are written
             if (tid < D) {
-                // output[d] += p * v[d] in key order (16 products at a time into registers)
-                const float* pr = dst + tid;
+                // output[d] += p * v[d] in key order (16 products at a time
+                // into registers); key kl's element d at kl * D + (d ^ (kl % 4))
                 const int rows = min(kRoChunk, n - k0);
                 int k = 0;
                 for (; k + 16 <= rows; k += 16) {
                     float t[16];
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) t[j] = pr[(k + j) * D];
+                    for (int j = 0; j < 16; ++j) t[j] = dst[(k + j) * D + (tid ^ (j & 3))];
 #pragma unroll
                     for (int j = 0; j < 16; ++j) acc += t[j];
                 }
-                for (; k < rows; ++k) acc += pr[k * D];
+                for (; k < rows; ++k) acc += dst[k * D + (tid ^ (k & 3))];
             }
         }
     }
