@@ -285,10 +285,18 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
             if (k0 >= n) break;
             __syncthreads();   // wave 0 is done with this buffer (and, first time, every p is written)
             float* dst = prod + (c & 1) * kRoChunk * D;
+            // every p of this thread's keys first: a read between the stores
+            // below would wait out its latency once per key
+            float pks[kRoChunkF4];
 #pragma unroll
             for (int i = 0; i < kRoChunkF4; ++i) {
-                const int f = tid + kRoBlock * i, key = k0 + f / (D / 4);
-                const float pk = key < n ? sc[key] : 0.0f;
+                const int key = k0 + (tid + kRoBlock * i) / (D / 4);
+                pks[i] = key < n ? sc[key] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < kRoChunkF4; ++i) {
+                const int f = tid + kRoBlock * i;
+                const float pk = pks[i];
                 const v4f v = vv[kRoChunkF4 * c + i];
                 v4f r;
                 r[0] = pk * v[0];
