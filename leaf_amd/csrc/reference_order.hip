@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 
 // Single-token attention at head dim 64 (decode): the same arithmetic as
 // ro_attention_kernel, arranged so that no dependent sum waits on memory.
-//   * Scores: thread k takes keys k, k + 256, ...; the next key's row loads
+//   * Scores: thread k takes keys k, k + 512, ...; the next key's row loads
 //     into registers while the current one is summed (q . k in column order,
 //     q read from LDS).
 //   * Exponentials: four independent keys per thread at a time.
@@ -171,17 +171,18 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 //     other threads fill the second buffer.
 constexpr int kRoChunk = 128;                                          // keys per product buffer
 constexpr int kRoDecodeDim = 64;
-constexpr int kRoChunkF4 = kRoChunk * kRoDecodeDim / 4 / kRoBlock;    // float4 per thread per chunk (8)
+constexpr int kRoDecodeBlock = 512;                                  // threads of the decode kernel
+constexpr int kRoChunkF4 = kRoChunk * kRoDecodeDim / 4 / kRoDecodeBlock;    // float4 per thread per chunk (4)
 constexpr int kRoRoundChunks = 5;
 constexpr int kRoRound = kRoChunk * kRoRoundChunks;                    // keys whose V rows sit in registers
 
-__global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(AttentionCall p) {
+__global__ __launch_bounds__(kRoDecodeBlock) void ro_attention_decode_kernel(AttentionCall p) {
     constexpr int D = kRoDecodeDim;
     extern __shared__ float lds[];
     float* qs = lds;                          // [D]
     float* prod = lds + D;                    // [2][kRoChunk][D] products p_k * v_k[d]
     float* sc = prod + 2 * kRoChunk * D;      // [visible keys]: scores, then e, then p
-    __shared__ float red[kRoBlock / kWave];
+    __shared__ float red[kRoDecodeBlock / kWave];
     __shared__ float den_shared;
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
@@ -207,8 +208,8 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
             for (int j = 0; j < D / 4; ++j) dst[j] = src[j];
         };
         if (tid < n) load_row(cur, tid);
-        for (int k = tid; k < n; k += kRoBlock) {
-            if (k + kRoBlock < n) load_row(nxt, k + kRoBlock);
+        for (int k = tid; k < n; k += kRoDecodeBlock) {
+            if (k + kRoDecodeBlock < n) load_row(nxt, k + kRoDecodeBlock);
             float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < D / 4; ++j) {
@@ -233,35 +234,35 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     float maximum = red[0];
-    for (int w = 1; w < kRoBlock / kWave; ++w) maximum = maximum < red[w] ? red[w] : maximum;
+    for (int w = 1; w < kRoDecodeBlock / kWave; ++w) maximum = maximum < red[w] ? red[w] : maximum;
     if (!isfinite(maximum)) {
         // fully masked (or infinite) row: the CPU leaves the zero-filled output
         if (tid < D) o[tid] = 0.0f;
         return;
     }
 
-    // ---- V rows of a round: thread t holds float4 f = t + kRoBlock i (key
+    // ---- V rows of a round: thread t holds float4 f = t + kRoDecodeBlock i (key
     // r0 + f / 16, columns 4 (f % 16) ..); chunk c of the round is
     // vv[kRoChunkF4 c .. kRoChunkF4 (c + 1))
     v4f vv[kRoRoundChunks * kRoChunkF4];
     auto load_round = [&](int r0) {
 #pragma unroll
         for (int i = 0; i < kRoRoundChunks * kRoChunkF4; ++i) {
-            const int f = tid + kRoBlock * i, key = r0 + f / (D / 4);
+            const int f = tid + kRoDecodeBlock * i, key = r0 + f / (D / 4);
             vv[i] = key < n ? *reinterpret_cast<const v4f*>(V + (size_t)key * D + 4 * (f % (D / 4)))
                             : v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
     // exponentials, four keys per thread at a time (their table reads overlap)
-    for (int k0 = 0; k0 < n; k0 += 4 * kRoBlock) {
+    for (int k0 = 0; k0 < n; k0 += 4 * kRoDecodeBlock) {
         float e[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = sc[min(k0 + tid + kRoBlock * i, n - 1)];
+        for (int i = 0; i < 4; ++i) e[i] = sc[min(k0 + tid + kRoDecodeBlock * i, n - 1)];
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = libm_expf(e[i] - maximum);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int k = k0 + tid + kRoBlock * i;
+            const int k = k0 + tid + kRoDecodeBlock * i;
             if (k < n) sc[k] = e[i];
         }
     }
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
     if (tid == 0) den_shared = sequential_sum(sc, n);
     __syncthreads();
     const float den = den_shared;
-    for (int k = tid; k < n; k += kRoBlock) sc[k] = sc[k] / den;
+    for (int k = tid; k < n; k += kRoDecodeBlock) sc[k] = sc[k] / den;
 
     float acc = 0.0f;
     for (int r0 = 0; r0 < n; r0 += kRoRound) {
@@ -290,12 +291,12 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_decode_kernel(Attention
             float pks[kRoChunkF4];
 #pragma unroll
             for (int i = 0; i < kRoChunkF4; ++i) {
-                const int key = k0 + (tid + kRoBlock * i) / (D / 4);
+                const int key = k0 + (tid + kRoDecodeBlock * i) / (D / 4);
                 pks[i] = key < n ? sc[key] : 0.0f;
             }
 #pragma unroll
             for (int i = 0; i < kRoChunkF4; ++i) {
-                const int f = tid + kRoBlock * i;
+                const int f = tid + kRoDecodeBlock * i;
                 const float pk = pks[i];
                 const v4f v = vv[kRoChunkF4 * c + i];
                 v4f r;
@@ -539,7 +540,7 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
     if (p.tokens == 1 && p.dim == kRoDecodeDim) {
         const size_t lds = ((size_t)kRoDecodeDim + 2 * kRoChunk * kRoDecodeDim + max_keys) * sizeof(float);
         if (!allow_lds(ro_attention_decode_kernel, lds, g_attention_decode_lds)) return false;
-        ro_attention_decode_kernel<<<p.heads, kRoBlock, lds, stream>>>(p);
+        ro_attention_decode_kernel<<<p.heads, kRoDecodeBlock, lds, stream>>>(p);
         return true;
     }
     const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
