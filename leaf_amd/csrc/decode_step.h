@@ -49,6 +49,11 @@ struct StepParams {
     int layers = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, rotary = 0, vocab = 0;
     int window = 0, capacity = 0, activation = 0;
     int item_heads = 1;                 // least query heads per exchange wave in an attention item (1, 2, 4 or 8)
+    // Nonzero: every floating-point step in the CPU reference's order and rounding (sequential norm and
+    // softmax sums, key-order p.v, glibc expf in the softmax and SiLU, dot_avx order in the FP32 head),
+    // so logits equal the reference's bit for bit.  Needs SiLU or ReLU and a hidden width that is a
+    // multiple of 32 (decode_step_fits_reference).
+    int reference = 0;
     float epsilon = 0, embedding_scale = 1, attention_scale = 1;
     const StepLayer* layer = nullptr;   // device array [layers]
     WeightView embedding;               // int8 per row or f32
@@ -87,6 +92,8 @@ struct StepParams {
 
 // Whether a decoder of this geometry runs on the persistent step kernel.
 bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int vocab, int blocks);
+// ... and, in addition, in reference order (StepParams::reference).
+bool decode_step_fits_reference(int hidden, int activation);
 // Attention spans for `keys` visible keys.
 int decode_step_spans(int keys);
 // Blocks the step runs on (one per CU), or 0 when one block per CU cannot be resident.

@@ -34,7 +34,10 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "device_common.h"
+#include "libm_expf.h"
 
 namespace leafhip {
 namespace {
@@ -102,6 +105,13 @@ struct __align__(16) Shared {
     int received[kA];               // last phase whose input vector each exchange wave has read
     int published;                  // phase outputs this block's weight waves published (kB per phase)
     int abort;
+};
+
+// Reference order adds each chain wave's softmax terms of one query head
+// (scores, then exp(score - max), then the probabilities), kept in key order.
+constexpr int kRefMaxKeys = kStepMaxSpans * kStepSpanKeys;
+struct __align__(16) SharedRef : Shared {
+    float pe[kA][kRefMaxKeys];
 };
 
 // Wave reductions on DPP lane moves instead of LDS-crossbar shuffles: xor 1
@@ -464,18 +474,40 @@ __device__ __forceinline__ void post(Shared& s, int phase) {
     if ((threadIdx.x & 63) == 0) lds_store(&s.ready[threadIdx.x >> 6], phase);
 }
 
-// RMSNorm of the n values held as runs (decoder.cpp:706-727).
-template <int N>
+// RMSNorm of the n values held as runs (decoder.cpp:706-727).  In reference
+// order the squares are summed in column order, as norm() sums them: every
+// lane stores its runs' squares in column order (s.xf is free until the
+// head), exchange wave 0 adds them one by one and trades the sum to wave 1;
+// the normalized value is (x - 0) * scale * gamma + 0, norm()'s expression
+// with mean 0 and no beta.
+template <bool REF, int N>
 __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
                                               Shared& s, int& round) {
     const int live = n / kRun - a;
     float sq = 0.0f;
+    if constexpr (REF) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) sq += (i / kRun) * kAT < live ? x[i] * x[i] : 0.0f;
-    if (!a_sum(sq, s, round)) return false;
-    const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+        for (int g = 0; g < N / kRun; ++g)
+            if (g * kAT < live) {
+                const float x0 = x[kRun * g] - 0.0f, x1 = x[kRun * g + 1] - 0.0f;
+                *reinterpret_cast<v2f*>(s.xf + kRun * run_of(g, a)) = v2f{x0 * x0, x1 * x1};
+            }
+        if (!a_sync(s, round)) return false;   // both waves' squares are in place
+        if (a < kWave) sq = sequential_sum(s.xf, n);
+        float other;
+        if (!a_trade(sq, other, s, round)) return false;
+        if (a >= kWave) sq = other;
+        const float scale = 1.0f / sqrtf(sq / (float)n + eps);
 #pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
+        for (int i = 0; i < N; ++i) x[i] = (x[i] - 0.0f) * scale * gamma[i] + 0.0f;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) sq += (i / kRun) * kAT < live ? x[i] * x[i] : 0.0f;
+        if (!a_sum(sq, s, round)) return false;
+        const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
+    }
     return true;
 }
 
@@ -672,6 +704,13 @@ __device__ __forceinline__ float activate(int activation, float x) {
     return x < 0.0f ? 0.0f : x;
 }
 
+// Decoder::Impl::activate in reference order: SiLU with glibc's expf, ReLU
+// as std::max(x, 0.0f).  (The step runs reference order only for these two.)
+__device__ __forceinline__ float ref_activate(int activation, float x) {
+    if (activation == 0) return x / (1.0f + libm_expf(-x));
+    return x < 0.0f ? 0.0f : x;
+}
+
 __device__ __forceinline__ float embed_value(const WeightView& w, uint32_t id, int c) {
     const size_t index = (size_t)id * w.cols + c;
     if (w.bits == 32) return ldg(static_cast<const float*>(w.data) + index);
@@ -824,6 +863,106 @@ __device__ __forceinline__ void attention_item(const StepParams& P, Shared& s, i
     }
 }
 
+// Reference order (attention_impl, transformer.cpp:112-143): an item only
+// scores its span's keys for the wave's query heads, (q . k) * scale * scale
+// with the dot summed over the dims in order and separate roundings
+// (scalar_dot, :69-73), and publishes the raw scores in the span-partial
+// layout: word 2 + key of each head's slot (lanes past the span's keys
+// publish -inf), words 0 and 1 only the epoch.  The head's chain wave takes
+// the maximum, the exponentials, the sequential denominator and the key-order
+// output.  Rows of s.k past the span hold finite values that no score uses.
+template <int HPW>
+__device__ __forceinline__ void ref_score_item(const StepParams& P, Shared& s, int lane, int aw, int h0, int h_end,
+                                               int keys, u64* parts, unsigned epoch, bool local) {
+    auto put = [&](u64* p, float v) {
+        if (local) __hip_atomic_store((LEAF_GLOBAL u64*)p, tagged(epoch, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+        else publish(p, epoch, v);
+    };
+    constexpr int dim = kStepDim;
+    float sum[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) sum[h] = 0.0f;
+#pragma unroll(8 / HPW)
+    for (int d4 = 0; d4 < dim / 4; ++d4) {
+        const v4f kv = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
+        v4f qv[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+            qv[h] = *reinterpret_cast<const v4f*>(s.q + min(h0 + aw + kA * h, h_end - 1) * dim + 4 * d4);
+        all_loaded(kv, qv);
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum[h] = sum[h] + qv[h][j] * kv[j];
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        const int gh = h0 + aw + kA * h;
+        if (gh < h_end) {
+            u64* part = parts + (size_t)gh * (dim + 2);
+            put(part + 2 + lane, lane < keys ? sum[h] * P.attention_scale * P.attention_scale : -INFINITY);
+            if (lane == 0) {
+                put(part, 0.0f);
+                put(part + 1, 0.0f);
+            }
+        }
+    }
+}
+
+// Reference order, the rest of one query head's attention in one wave
+// (attention_impl, transformer.cpp:122-143): the scores of its n visible keys
+// (pe, key order) -> the maximum (NaN scores never become it, as with
+// std::max) -> exp(s - max) with glibc's expf -> the denominator summed in key
+// order -> p = e / denominator -> output[d] += p * v[d] in key order, lane d.
+// Cached keys' V rows come from the cache (this XCD's items loaded them a
+// moment ago); the new key's from the exchange words of q|k|v.  A fully
+// masked or infinite row leaves the zero output, like the CPU.  Returns
+// false (abort raised) when a wait failed; o is this lane's output element.
+__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, int n, float m, const float* V,
+                                          const u64* vnew_word, unsigned vnew_epoch, int lane, float& o) {
+    constexpr int dim = kStepDim;
+    o = 0.0f;
+    const float maximum = dpp_max_f32(m);
+    if (!isfinite(maximum)) return true;
+    lds_done();
+    for (int k = lane; k < n; k += kWave) pe[k] = libm_expf(pe[k] - maximum);
+    lds_done();
+    const float den = sequential_sum(pe, n);   // every lane: broadcast reads
+    for (int k = lane; k < n; k += kWave) pe[k] = pe[k] / den;
+    lds_done();
+    float vnew;
+    if (!await_one(vnew_word, true, vnew_epoch, vnew, P)) return false;
+    const int cached = n - 1;   // the new key is the last visible one
+    constexpr int B = 16;
+    auto load = [&](float (&d)[B], int k0) {
+#pragma unroll
+        for (int j = 0; j < B; ++j) d[j] = ldg(V + (size_t)(k0 + j) * dim);
+    };
+    auto add = [&](const float (&d)[B], int k0) {
+        float p[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) p[j] = pe[k0 + j];
+#pragma unroll
+        for (int j = 0; j < B; ++j) o = o + p[j] * d[j];
+    };
+    // two batches in flight: the next batch's V rows load while one is added
+    int k = 0;
+    float va[B], vb[B];
+    if (cached >= B) load(va, 0);
+    while (k + B <= cached) {
+        if (k + 2 * B <= cached) load(vb, k + B);
+        add(va, k);
+        k += B;
+        if (k + B > cached) break;
+        if (k + 2 * B <= cached) load(va, k + B);
+        add(vb, k);
+        k += B;
+    }
+    for (; k < cached; ++k) o = o + pe[k] * ldg(V + (size_t)k * dim);
+    o = o + pe[cached] * vnew;
+    return true;
+}
+
 // How a step lays out its attention (both roles compute the same plan).
 // Items are (KV head, span of keys, slice of the group's query heads);
 // slices are as narrow as the grid allows (hpw heads per exchange wave).
@@ -906,7 +1045,7 @@ __device__ __forceinline__ void capture_acc(const StepParams& P, int L, int phas
 }
 
 // Returns false when the kernel is abandoned (abort).
-template <bool CAP>
+template <bool CAP, bool REF>
 __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     int a = threadIdx.x;                     // 0 .. kAT - 1
     const int G = gridDim.x, b = blockIdx.x;
@@ -995,7 +1134,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
         }
         store_runs(s.h_in, x, a);
-        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
         capture_input<CAP>(P, s, x, H, 0, L, 0, a);
         post(s, 4 * L + 0);
         stamp(P.trace, b, 64 * L + 2);
@@ -1024,44 +1163,57 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             if (!a_check(ok_q, s, P)) return false;
             stamp(P.trace, b, 64 * L + 3);
             if (a < kA * dim / 2) *reinterpret_cast<v2f*>(s.q + item_h0 * dim + 2 * a) = v2f{got2[0], got2[1]};
-            if (!a_sync(s, round)) return false;
-            stamp(P.trace, b, 64 * L + 56);
-            float keep[3];
-            attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys - (new_key ? 1 : 0), nullptr, epoch(L, 2),
-                              true, keep);
-            float m = keep[0], l = keep[1], o = keep[2];
-            if (new_key) {
+            if constexpr (REF) {
+                // the new key's k joins the staged rows before the scores
                 float kv_got;
-                if (!a_check(await_one(P.x_qkv + kv_word, a < 2 * dim, epoch(L, 1), kv_got, P), s, P)) return false;
-                if (!a_sync(s, round)) return false;   // both waves are done with the cached rows
-                const int nl = pos - k0;
-                if (a < dim) s.k[nl * kKStride + a] = kv_got;
-                else s.v[nl * dim + (a - dim)] = kv_got;
+                if (!a_check(await_one(P.x_qkv + kv_word, new_key && a < dim, epoch(L, 1), kv_got, P), s, P))
+                    return false;
+                if (new_key && a < dim) s.k[(pos - k0) * kKStride + a] = kv_got;
                 if (!a_sync(s, round)) return false;
-                // fold key nl in: rescale the cached keys' partials to the new max
-                const int gh = min(item_h0 + aw, item_h1 - 1);
-                const float qd = s.q[gh * dim + lane], kd = s.k[nl * kKStride + lane], vd = s.v[nl * dim + lane];
-                const float sn = dpp_sum_f32(qd * kd) * P.attention_scale * P.attention_scale;
-                const float mn = fmaxf(m, sn);
-                const float alpha = expf(m - mn), beta = expf(sn - mn);
-                l = l * alpha + beta;
-                o = fmaf(o, alpha, beta * vd);
-                m = mn;
-            }
-            const int gh = item_h0 + aw;
-            if (gh < item_h1) {
-                u64* part = part_base + ((size_t)(item_g * spans + item_s) * group + gh) * (dim + 2);
-                const unsigned e2 = epoch(L, 2);
-                __hip_atomic_store((LEAF_GLOBAL u64*)(part + 2 + lane), tagged(e2, o), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WAVEFRONT);
-                if (lane == 0) {
-                    __hip_atomic_store((LEAF_GLOBAL u64*)part, tagged(e2, m), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
-                    __hip_atomic_store((LEAF_GLOBAL u64*)(part + 1), tagged(e2, l), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+                stamp(P.trace, b, 64 * L + 56);
+                u64* parts = part_base + (size_t)(item_g * spans + item_s) * group * (dim + 2);
+                ref_score_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), true);
+                stamp(P.trace, b, 64 * L + 57);
+            } else {
+                if (!a_sync(s, round)) return false;
+                stamp(P.trace, b, 64 * L + 56);
+                float keep[3];
+                attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys - (new_key ? 1 : 0), nullptr, epoch(L, 2),
+                                  true, keep);
+                float m = keep[0], l = keep[1], o = keep[2];
+                if (new_key) {
+                    float kv_got;
+                    if (!a_check(await_one(P.x_qkv + kv_word, a < 2 * dim, epoch(L, 1), kv_got, P), s, P)) return false;
+                    if (!a_sync(s, round)) return false;   // both waves are done with the cached rows
+                    const int nl = pos - k0;
+                    if (a < dim) s.k[nl * kKStride + a] = kv_got;
+                    else s.v[nl * dim + (a - dim)] = kv_got;
+                    if (!a_sync(s, round)) return false;
+                    // fold key nl in: rescale the cached keys' partials to the new max
+                    const int gh = min(item_h0 + aw, item_h1 - 1);
+                    const float qd = s.q[gh * dim + lane], kd = s.k[nl * kKStride + lane], vd = s.v[nl * dim + lane];
+                    const float sn = dpp_sum_f32(qd * kd) * P.attention_scale * P.attention_scale;
+                    const float mn = fmaxf(m, sn);
+                    const float alpha = expf(m - mn), beta = expf(sn - mn);
+                    l = l * alpha + beta;
+                    o = fmaf(o, alpha, beta * vd);
+                    m = mn;
                 }
+                const int gh = item_h0 + aw;
+                if (gh < item_h1) {
+                    u64* part = part_base + ((size_t)(item_g * spans + item_s) * group + gh) * (dim + 2);
+                    const unsigned e2 = epoch(L, 2);
+                    __hip_atomic_store((LEAF_GLOBAL u64*)(part + 2 + lane), tagged(e2, o), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+                    if (lane == 0) {
+                        __hip_atomic_store((LEAF_GLOBAL u64*)part, tagged(e2, m), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WAVEFRONT);
+                        __hip_atomic_store((LEAF_GLOBAL u64*)(part + 1), tagged(e2, l), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WAVEFRONT);
+                    }
+                }
+                stamp(P.trace, b, 64 * L + 57);
             }
-            stamp(P.trace, b, 64 * L + 57);
         } else if (has_item) {
             // q of the group's heads, and the new key's k (lanes < dim) or v
             // (the q|k|v buffer is padded so a lane's runs stay inside it)
@@ -1083,13 +1235,53 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             if (!a_sync(s, round)) return false;
             stamp(P.trace, b, 64 * L + 56);
             u64* parts = part_base + (size_t)(item_g * spans + item_s) * group * (dim + 2);
-            if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), local);
-            else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
-            else if (hpw == 4) attention_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
-            else attention_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+            if constexpr (REF) {
+                if (hpw == 1) ref_score_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), local);
+                else if (hpw == 2) ref_score_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+                else if (hpw == 4) ref_score_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+                else ref_score_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+            } else {
+                if (hpw == 1) attention_item<1>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), local);
+                else if (hpw == 2) attention_item<2>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+                else if (hpw == 4) attention_item<4>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+                else attention_item<kHeadsA>(P, s, lane, aw, item_h0, item_h1, keys, parts, epoch(L, 2), false);
+            }
             stamp(P.trace, b, 64 * L + 57);
         }
-        if (merge_block) {
+        if (merge_block && REF) {
+            // reference order: this wave's query head mh, all of it (ref_chain)
+            bool ok = true;
+            const int mh = local ? merge_sigma / slices * group + merge_sigma % slices * kA + aw : (G - 1 - b) * kA + aw;
+            const bool mine = local ? merge_sigma % slices * kA + aw < group : mh < P.heads;
+            if (mine) {
+                const int g = mh / group, gh = mh % group;
+                const size_t stride = (size_t)group * (dim + 2);
+                const u64* base = part_base + ((size_t)g * spans * group + gh) * (dim + 2);
+                float* pe = static_cast<SharedRef&>(s).pe[aw];
+                const int n = end - begin;
+                float m = -INFINITY;
+                v2f ml;
+                float os[kMergeBatch];
+                for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
+                    ok = await_partials(base, (int)stride, spans, s0, lane, epoch(L, 2), ml, os, P);
+#pragma unroll
+                    for (int j = 0; j < kMergeBatch; ++j) {
+                        const int k = (s0 + j) * kStepSpanKeys + lane;
+                        if (ok && k < n) {
+                            pe[k] = os[j];
+                            m = m < os[j] ? os[j] : m;
+                        }
+                    }
+                }
+                float o = 0.0f;
+                if (ok)
+                    ok = ref_chain(P, pe, n, m, Vc + ((size_t)g * P.capacity + begin) * dim + lane,
+                                   P.x_qkv + qw + kvw + g * dim + lane, epoch(L, 1), lane, o);
+                if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), o);
+            }
+            if (!a_check(ok, s, P)) return false;
+            stamp(P.trace, b, 64 * L + 60);
+        } else if (merge_block) {
             // this wave's query head mh: combine its spans (lane s holds span
             // s's max and sum; lane d accumulates output element d)
             bool ok = true;
@@ -1150,7 +1342,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 6);
         stamp(P.trace, b, 64 * L + 59, kWave);
         store_runs(s.h_mid, x, a);
-        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
+        if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
         capture_input<CAP>(P, s, x, H, 0, L, 2, a);
         post(s, 4 * L + 2);
         // ---- SiLU-gated activation -> int8 for down_proj
@@ -1184,7 +1376,7 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             return false;
         note_received(s, 4 * P.layers);
         stamp(P.trace, b, 64 * P.layers + 1);
-        if (!rms_normalize(x, H, gamma, P.epsilon, a, s, round)) return false;
+        if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round)) return false;
         store_runs(s.xf, x, a);
         post(s, 4 * P.layers);
     }
@@ -1202,7 +1394,7 @@ struct LayerRows {
     RowScale gs;   // per lane: the gate|up row whose total this lane's 8-lane group holds
 };
 
-template <bool CAP>
+template <bool CAP, bool REF>
 __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     const int t = threadIdx.x, lane = t & 63;
     const int bw = __builtin_amdgcn_readfirstlane((t >> 6) - kA);   // 0 .. kB - 1, wave-uniform
@@ -1398,7 +1590,8 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
             const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
                                                                              __float_as_uint(mine), false, false)[1]);
             if (lane < 32 && (lane & 7) == 0 && g_live)
-                publish(P.x_act + g_pair, epoch(L, 5), up * activate(P.activation, mine));
+                publish(P.x_act + g_pair, epoch(L, 5), up * (REF ? ref_activate(P.activation, mine)
+                                                                  : activate(P.activation, mine)));
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
@@ -1432,9 +1625,9 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     return wait_ready(s, 4 * P.layers);
 }
 
-template <bool CAP>
+template <bool CAP, bool REF>
 __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
-    __shared__ Shared s;
+    __shared__ typename std::conditional<REF, SharedRef, Shared>::type s;
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int G = gridDim.x, b = blockIdx.x;
@@ -1459,7 +1652,7 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     const bool forced = P.x_part_local && P.xcd_check_flip && b == G - 1;
     if (P.x_part_local && t == 0 && (forced || xcc_id() != (b & 7))) raise_abort(P, kAbortXcdMapping);
     if (forced) return;
-    const bool ok = wave < kA ? exchange_role<CAP>(P, s) : weight_role<CAP>(P, s);
+    const bool ok = wave < kA ? exchange_role<CAP, REF>(P, s) : weight_role<CAP, REF>(P, s);
     if (__syncthreads_or(!ok)) return;          // every wave leaves when one gave up (abort flags raised)
 
     // ---------------- FP32 LM head and greedy argmax (all waves)
@@ -1470,7 +1663,71 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
     int best_i = V;
     const float* head = static_cast<const float*>(P.head.data);
     constexpr int kPerLane = kStepMaxHidden / 4 / kWave;       // float4 per lane of a row
-    for (int r = v_first + wave; r < v_end; r += 2 * kWaves) {
+    if constexpr (REF) {
+        // dot_avx order (decoder.cpp:355-391; one token, one scale group):
+        // chains a, b, c, d of 8 lanes run over the row's 32-column blocks,
+        // lane l of chain c summing fmaf(w, x) over columns 32 j + 8 c + l;
+        // then (a + b) + (c + d) per lane, the horizontal sum
+        // ((l0 + l4) + (l2 + l6)) + ((l1 + l5) + (l3 + l7)), fmaf(sum, 1, 0)
+        // for the group scale, and the bias.  Eight rows per wave: lane
+        // 8 r + 2 c + h holds lanes 4 h .. 4 h + 3 of chain c of row r, so each
+        // load is one 16-byte piece of a 32-column block.  Every lane of a
+        // row's eight ends with the same total (IEEE addition commutes).
+        const int r8 = lane >> 3, col = 8 * ((lane >> 1) & 3) + 4 * (lane & 1);
+        constexpr int kBatch = 8;                              // 32-column blocks per batch of loads
+        const int blocks32 = H / 32;
+        for (int r0 = v_first + 8 * wave; r0 < v_end; r0 += 8 * kWaves) {
+            const int r = min(r0 + r8, v_end - 1);
+            const LEAF_GLOBAL v4f* wr = (const LEAF_GLOBAL v4f*)(head + (size_t)r * H + col);
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f wa[kBatch], wb[kBatch];
+            auto load = [&](v4f (&w)[kBatch], int j0) {
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) w[j] = __builtin_nontemporal_load(wr + 8 * min(j0 + j, blocks32 - 1));
+            };
+            auto fold = [&](const v4f (&w)[kBatch], int j0) {
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j)
+                    if (j0 + j < blocks32) {
+                        const v4f xv = *reinterpret_cast<const v4f*>(s.xf + 32 * (j0 + j) + col);
+                        acc[0] = fmaf(w[j].x, xv.x, acc[0]);
+                        acc[1] = fmaf(w[j].y, xv.y, acc[1]);
+                        acc[2] = fmaf(w[j].z, xv.z, acc[2]);
+                        acc[3] = fmaf(w[j].w, xv.w, acc[3]);
+                    }
+            };
+            load(wa, 0);
+            for (int j0 = 0; j0 < blocks32; j0 += 2 * kBatch) {
+                if (j0 + kBatch < blocks32) load(wb, j0 + kBatch);
+                fold(wa, j0);
+                if (j0 + kBatch >= blocks32) break;
+                if (j0 + 2 * kBatch < blocks32) load(wa, j0 + 2 * kBatch);
+                fold(wb, j0 + kBatch);
+            }
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float t2 = acc[i] + __shfl_xor(acc[i], 2, kWave);   // a + b, c + d
+                v[i] = t2 + __shfl_xor(t2, 4, kWave);                     // (a + b) + (c + d)
+            }
+            float h4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h4[i] = v[i] + __shfl_xor(v[i], 1, kWave);   // l + (l + 4)
+            const float total = (h4[0] + h4[2]) + (h4[1] + h4[3]);
+            const float logit = fmaf(total, 1.0f, 0.0f) + ldg(P.head.bias + r);
+            if (r0 + r8 < v_end) {
+                if ((lane & 7) == 0) stg(P.logits + r, logit);
+                if (better(logit, r, best, best_i)) { best = logit; best_i = r; }
+            }
+        }
+#pragma unroll
+        for (int o = 8; o < kWave; o <<= 1) {
+            const float ov = __shfl_xor(best, o, kWave);
+            const int oi = __shfl_xor(best_i, o, kWave);
+            if (better(ov, oi, best, best_i)) { best = ov; best_i = oi; }
+        }
+    }
+    for (int r = v_first + wave; !REF && r < v_end; r += 2 * kWaves) {
         const int r2 = r + kWaves;
         const bool two = r2 < v_end;
         v4f wa[kPerLane], wb[kPerLane];
@@ -1555,8 +1812,10 @@ int decode_step_spans(int keys) { return (keys + kStepSpanKeys - 1) / kStepSpanK
 int decode_step_blocks(int device) {
     int cus = 0, resident = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    for (const void* kernel : {reinterpret_cast<const void*>(decode_step_kernel<false>),
-                               reinterpret_cast<const void*>(decode_step_kernel<true>)}) {
+    for (const void* kernel : {reinterpret_cast<const void*>(decode_step_kernel<false, false>),
+                               reinterpret_cast<const void*>(decode_step_kernel<true, false>),
+                               reinterpret_cast<const void*>(decode_step_kernel<false, true>),
+                               reinterpret_cast<const void*>(decode_step_kernel<true, true>)}) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kernel, kT, 0) != hipSuccess || resident < 1)
             return 0;
     }
@@ -1573,11 +1832,19 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
            (ffn + blocks - 1) / blocks <= kGP * kB;
 }
 
+bool decode_step_fits_reference(int hidden, int activation) {
+    // the head's dot_avx chains cover the row in whole 32-column blocks;
+    // GELU needs glibc's erff / tanhf, which the device does not restate
+    return hidden % 32 == 0 && (activation == 0 || activation == 3);
+}
+
 hipError_t launch_decode_step(const StepParams& params, int blocks, hipStream_t stream, bool cooperative) {
     StepParams p = params;
     void* args[] = {&p};
-    const void* kernel = p.capture.x ? reinterpret_cast<const void*>(decode_step_kernel<true>)
-                                     : reinterpret_cast<const void*>(decode_step_kernel<false>);
+    const void* kernel = p.reference ? (p.capture.x ? reinterpret_cast<const void*>(decode_step_kernel<true, true>)
+                                                    : reinterpret_cast<const void*>(decode_step_kernel<false, true>))
+                                     : (p.capture.x ? reinterpret_cast<const void*>(decode_step_kernel<true, false>)
+                                                    : reinterpret_cast<const void*>(decode_step_kernel<false, false>));
     if (cooperative) return hipLaunchCooperativeKernel(kernel, dim3(blocks), dim3(kT), args, 0, stream);
     // A plain launch of the same grid: one block per CU fits (decode_step_blocks
     // checked the occupancy), so on an otherwise idle device every block is

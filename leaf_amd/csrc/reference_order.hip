@@ -167,8 +167,9 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 //     kRoRound keys are loaded into registers (all threads, coalesced) while
 //     the denominator is formed; then, chunk by chunk,
 //     all threads write p_k * v_k[d] into an LDS buffer and wave 0 adds a
-//     chunk's products in key order (lane d, output element d) while the
-//     other threads fill the second buffer.
+//     chunk's products in key order (lane d, output element d); the next
+//     chunk's products are written once wave 0 is done with the buffer (the
+//     barrier at the top of each chunk), so one buffer serves every chunk.
 constexpr int kRoChunk = 128;                                          // keys per product buffer
 constexpr int kRoDecodeDim = 64;
 constexpr int kRoDecodeBlock = 512;                                  // threads of the decode kernel
@@ -180,8 +181,8 @@ __global__ __launch_bounds__(kRoDecodeBlock) void ro_attention_decode_kernel(Att
     constexpr int D = kRoDecodeDim;
     extern __shared__ float lds[];
     float* qs = lds;                          // [D]
-    float* prod = lds + D;                    // [2][kRoChunk][D] products p_k * v_k[d]
-    float* sc = prod + 2 * kRoChunk * D;      // [visible keys]: scores, then e, then p
+    float* prod = lds + D;                    // [kRoChunk][D] products p_k * v_k[d]
+    float* sc = prod + kRoChunk * D;          // [visible keys]: scores, then e, then p
     __shared__ float red[kRoDecodeBlock / kWave];
     __shared__ float den_shared;
     const int h = blockIdx.x;
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(kRoDecodeBlock) void ro_attention_decode_kernel(Att
             const int k0 = r0 + c * kRoChunk;
             if (k0 >= n) break;
             __syncthreads();   // wave 0 is done with this buffer (and, first time, every p is written)
-            float* dst = prod + (c & 1) * kRoChunk * D;
+            float* dst = prod;
             // every p of this thread's keys first: a read between the stores
             // below would wait out its latency once per key
             float pks[kRoChunkF4];
@@ -531,14 +532,14 @@ bool launch_norm_reference_order(const float* x, int rows, int width, const Norm
     return true;
 }
 
-// LDS of the decode kernel (the larger one): q, two product buffers, the
+// LDS of the decode kernel (the larger one): q, the product buffer, the
 // scores; 1 KiB stays for the static arrays.
-int reference_order_attention_keys() { return (160 * 1024 - 1024) / 4 - kRoDecodeDim - 2 * kRoChunk * kRoDecodeDim; }
+int reference_order_attention_keys() { return (160 * 1024 - 1024) / 4 - kRoDecodeDim - kRoChunk * kRoDecodeDim; }
 
 bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipStream_t stream) {
     if (max_keys > reference_order_attention_keys() || p.dim > 256) return false;
     if (p.tokens == 1 && p.dim == kRoDecodeDim) {
-        const size_t lds = ((size_t)kRoDecodeDim + 2 * kRoChunk * kRoDecodeDim + max_keys) * sizeof(float);
+        const size_t lds = ((size_t)kRoDecodeDim + kRoChunk * kRoDecodeDim + max_keys) * sizeof(float);
         if (!allow_lds(ro_attention_decode_kernel, lds, g_attention_decode_lds)) return false;
         ro_attention_decode_kernel<<<p.heads, kRoDecodeBlock, lds, stream>>>(p);
         return true;

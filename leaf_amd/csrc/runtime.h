@@ -31,14 +31,18 @@ void hip_check(hipError_t status, const char* what);
 
 // A numerics mode (LH_NUMERICS_*) resolved: whether the kernels follow the CPU
 // path's order, and whether grouped INT8 sums take quant_vnni_tile's form.
-// DEFAULT reads LEAF_GPU_NUMERICS; REFERENCE asks this host what the CPU path
-// would (AVX2, FMA and AVX-VNNI present, LEAF_DISABLE_VNNI unset or empty:
-// decoder.cpp:773, 780-782).  Throws on an unknown mode.
+// DEFAULT reads LEAF_GPU_NUMERICS ("fast", "reference", "reference-avx2",
+// "reference-vnni"); unset, it is REFERENCE for a decoder with int8
+// activations (a one-ulp change upstream of an int8 quantization moves the
+// whole bin, so only the CPU's order reproduces its tokens) and FAST
+// otherwise.  REFERENCE asks this host what the CPU path would (AVX2, FMA and
+// AVX-VNNI present, LEAF_DISABLE_VNNI unset or empty: decoder.cpp:773,
+// 780-782).  Throws on an unknown mode.
 struct NumericsMode {
     bool reference = false;
     bool vnni = false;
 };
-NumericsMode resolve_numerics(uint32_t numerics);
+NumericsMode resolve_numerics(uint32_t numerics, bool integer_activations = false);
 
 struct DeviceBuffer {
     void* ptr = nullptr;

@@ -62,13 +62,15 @@ Profiler::~Profiler() {
     for (auto e : events_) (void)hipEventDestroy(e);
 }
 
-NumericsMode resolve_numerics(uint32_t numerics) {
+NumericsMode resolve_numerics(uint32_t numerics, bool integer_activations) {
     if (numerics == LH_NUMERICS_DEFAULT) {
         const char* env = std::getenv("LEAF_GPU_NUMERICS");
         const std::string name = env ? env : "";
         numerics = name == "reference" ? LH_NUMERICS_REFERENCE
                  : name == "reference-avx2" ? LH_NUMERICS_REFERENCE_AVX2
-                 : name == "reference-vnni" ? LH_NUMERICS_REFERENCE_VNNI : LH_NUMERICS_FAST;
+                 : name == "reference-vnni" ? LH_NUMERICS_REFERENCE_VNNI
+                 : name == "fast" ? LH_NUMERICS_FAST
+                 : integer_activations ? LH_NUMERICS_REFERENCE : LH_NUMERICS_FAST;
     }
     NumericsMode mode;
     switch (numerics) {
@@ -94,7 +96,7 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t 
     const Config& c = m.config;
     capacity = max_context ? std::min(max_context, c.max_positions) : c.max_positions;
     check(capacity > 0, "session capacity must be positive", LH_ERROR_INVALID_ARGUMENT);
-    const NumericsMode mode = resolve_numerics(numerics);
+    const NumericsMode mode = resolve_numerics(numerics, m.activation_bits == 8);
     reference_ = mode.reference;
     reference_vnni_ = mode.vnni && m.activation_bits == 8;
     if (reference_) {
@@ -103,7 +105,19 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t 
         check(!m.accurate, "reference-order numerics do not support accurate FP32 math", LH_ERROR_UNSUPPORTED);
         check(c.hidden <= uint32_t(kReferenceOrderMaxWidth) && c.head_dim <= 256,
               "reference-order numerics: hidden or head width too large", LH_ERROR_UNSUPPORTED);
+        // One query's keys sit in LDS in the reference-order attention.  A
+        // session asked for more visible keys is refused here, not at the
+        // token that would pass the limit; without a requested size the
+        // capacity stops at the limit.
         reference_keys_ = reference_order_attention_keys();
+        const uint32_t limit = uint32_t(reference_keys_);
+        if (std::min(capacity, c.sliding_window ? c.sliding_window : capacity) > limit) {
+            check(max_context == 0,
+                  "reference-order numerics hold at most " + std::to_string(limit) +
+                      " visible keys per query; ask for a smaller context",
+                  LH_ERROR_UNSUPPORTED);
+            capacity = limit;
+        }
     }
     // KV cache for the whole context, [layers][k|v][kv_heads][capacity][dim].
     kv_.allocate(size_t(c.layers) * 2 * c.kv_heads * capacity * c.head_dim * sizeof(float));
@@ -143,14 +157,11 @@ Session::Session(Model& m, uint32_t max_context, uint32_t max_prefill, uint32_t 
     const char* fuse = std::getenv("LEAF_PREFILL_FUSE");
     fuse_quantize_ = !(fuse && std::string(fuse) == "0");
     const char* step = std::getenv("LEAF_DECODE_STEP");
-    step_enabled_ = !(step && std::string(step) == "0") && !reference_;
+    step_enabled_ = !(step && std::string(step) == "0");
     // LEAF_DECODE_STEP_COOPERATIVE=0: launch the step as a plain grid (for
     // profilers that fail at process exit after cooperative launches).
     const char* coop = std::getenv("LEAF_DECODE_STEP_COOPERATIVE");
     step_cooperative_ = !(coop && std::string(coop) == "0");
-    // Graph-replayed decode sizes the reference-order attention for the whole cache.
-    if (reference_ && int(std::min<uint32_t>(capacity, c.sliding_window ? c.sliding_window : capacity)) > reference_keys_)
-        graphs_enabled_ = false;
     if (step_enabled_) step_prepare();
 }
 
@@ -400,6 +411,7 @@ void Session::step_prepare() {
         c.layers > uint32_t(kStepMaxLayers))
         return;
     if (m.final_norm.beta || m.head.view.bits != 32 || m.head.input_scale) return;
+    if (reference_ && !decode_step_fits_reference(int(c.hidden), int(c.activation))) return;
     if (!(m.embedding.bits == 32 || (m.embedding.bits == 8 && m.embedding.group == m.embedding.cols))) return;
     auto per_row_int8 = [](const Linear& l) {
         return l.present && l.view.bits == 8 && l.view.group == l.view.cols && !l.input_scale && l.view.bias;
@@ -480,6 +492,7 @@ void Session::step_prepare() {
     p.window = int(c.sliding_window);
     p.capacity = int(capacity);
     p.activation = int(c.activation);
+    p.reference = reference_ ? 1 : 0;
     p.epsilon = c.epsilon;
     p.embedding_scale = c.embedding_scale;
     p.attention_scale = 1.0f / std::sqrt(std::sqrt(static_cast<float>(c.head_dim)));

@@ -10,7 +10,8 @@ the same greedy loop.
 * TinyLlama-1.1B W8A8, 512-token prompt, 128 greedy tokens; Qwen2.5-0.5B INT4
   (W4A32), 4096-token prompt, 256 tokens: with reference-order numerics the
   prefill and last logits equal the reference's bit for bit and all tokens
-  are identical.
+  are identical; TinyLlama's 127 decode tokens each run as one launch of the
+  persistent decode step.
 * GPT-2 small FP32, 16 + 32; Qwen INT4 4096 + 256; SmolLM2-360M BF16 with the
   accurate FP32 policy, 2048 + 256: with the fast kernels, logits within 1e-3
   of the largest |logit| and identical tokens.
@@ -84,23 +85,27 @@ def artifact(full_artifacts, family, meta):
     return path
 
 
-def greedy(dec, prompt, limit):
-    """generate_continuation on the GPU: (tokens, prefill logits, last logits)."""
+def greedy(dec, prompt, limit, profile=False):
+    """generate_continuation on the GPU: (tokens, prefill logits, last logits,
+    decode launches per profiler class when `profile`; profiling keeps graph
+    replays off, so the graph-replayed paths run unprofiled)."""
     logits = dec.forward(prompt)
     first = logits
     tokens = []
+    dec.set_profiling(profile)
     for i in range(limit):
         tokens.append(int(np.argmax(logits)))   # the first maximum, as std::max_element
         if i + 1 < limit:
             logits = dec.forward([tokens[-1]])
-    return tokens, first, logits
+    launches = {k: v["launches"] for k, v in dec.profile().items()}
+    return tokens, first, logits, launches
 
 
-def run(rt, path, meta, prompt, numerics):
+def run(rt, path, meta, prompt, numerics, profile=False):
     dec = rt.Decoder(path, meta["activation_bits"], meta["fp32_math"], numerics=numerics,
                      max_context=len(prompt) + meta["generate"] + 8, max_prefill=len(prompt))
     try:
-        return greedy(dec, prompt, meta["generate"])
+        return greedy(dec, prompt, meta["generate"], profile)
     finally:
         dec.close()
 
@@ -110,14 +115,21 @@ def test_reference_numerics_equal_the_reference_at_the_configured_size(rt, golde
     arrays, meta = golden
     m = meta[family]
     prompt = prompt_of(family, m)
-    tokens, first, last = run(rt, artifact(full_artifacts, family, m), m, prompt, "reference")
+    tokens, first, last, launches = run(rt, artifact(full_artifacts, family, m), m, prompt, "reference",
+                                        profile=family == "tinyllama")
     want = arrays[f"{family}_tokens"].tolist()
     diverged = next((i for i, (a, b) in enumerate(zip(tokens, want)) if a != b), None)
     print(f"{family} {len(prompt)}+{m['generate']} reference numerics: prefill logits bit-equal "
-          f"{bits_equal(first, arrays[f'{family}_prefill_logits'])}, first token difference at {diverged}")
+          f"{bits_equal(first, arrays[f'{family}_prefill_logits'])}, first token difference at {diverged}, "
+          f"decode launches {launches}")
     assert bits_equal(first, arrays[f"{family}_prefill_logits"]), "prefill logits differ from the reference"
     assert tokens == want, f"greedy tokens differ from step {diverged}"
     assert bits_equal(last, arrays[f"{family}_last_logits"]), "last-step logits differ from the reference"
+    if family == "tinyllama":
+        # every decode token ran on the persistent step (a step whose XCD
+        # placement check failed runs once more on the memory path)
+        steps = m["generate"] - 1
+        assert steps <= launches.get("decode_step", 0) <= steps + 4, launches
 
 
 @pytest.mark.parametrize("family", ["gpt2", "qwen", "smollm2"])
@@ -125,7 +137,7 @@ def test_fast_numerics_match_the_reference_at_the_configured_size(rt, golden, fu
     arrays, meta = golden
     m = meta[family]
     prompt = prompt_of(family, m)
-    tokens, first, last = run(rt, artifact(full_artifacts, family, m), m, prompt, "fast")
+    tokens, first, last, _ = run(rt, artifact(full_artifacts, family, m), m, prompt, "fast")
     e_first = rel_error(first, arrays[f"{family}_prefill_logits"])
     e_last = rel_error(last, arrays[f"{family}_last_logits"])
     want = arrays[f"{family}_tokens"].tolist()
@@ -140,7 +152,7 @@ def test_tinyllama_fast_numerics_stay_within_the_w8a8_band(rt, golden, full_arti
     arrays, meta = golden
     m = meta["tinyllama"]
     prompt = prompt_of("tinyllama", m)
-    tokens, first, _ = run(rt, artifact(full_artifacts, "tinyllama", m), m, prompt, "fast")
+    tokens, first, _, _ = run(rt, artifact(full_artifacts, "tinyllama", m), m, prompt, "fast")
     ref = arrays["tinyllama_prefill_logits"]
     want = arrays["tinyllama_tokens"].tolist()
     same = next((i for i, (a, b) in enumerate(zip(tokens, want)) if a != b), len(want))

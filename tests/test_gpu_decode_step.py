@@ -1,5 +1,7 @@
-"""The persistent single-token decode step against the oracle and the multi-launch path.
+"""The persistent single-token decode step in fast numerics against the oracle and the multi-launch path.
 
+(The same step in reference-order numerics, the default for W8A8 decoders,
+is bit-exact against the oracle: tests/test_gpu_decode_step_reference.py.)
 Single-token W8A8 forwards of TinyLlama-shape decoders (RMSNorm, RoPE, gated
 SiLU MLP, head dim 64, per-row INT8 matrices, FP32 head) run as one
 cooperative launch.  The runs are teacher-forced: the oracle's greedy token is
@@ -81,7 +83,7 @@ def decisive(reference, tolerance=2e-2):
 
 
 def run_steps(rt, oracle, path, prompt_tokens, steps, seed, **decoder_args):
-    dec = rt.Decoder(path, 8, **decoder_args)
+    dec = rt.Decoder(path, 8, numerics="fast", **decoder_args)
     od = oracle.decoder(path, 8, False)
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, dec.vocabulary_size, prompt_tokens).astype(np.uint32)
@@ -155,7 +157,7 @@ def test_step_and_graph_paths_agree(rt, small, monkeypatch):
     runs = []
     for flag in ("1", "0"):
         monkeypatch.setenv("LEAF_DECODE_STEP", flag)
-        dec = rt.Decoder(small, 8)
+        dec = rt.Decoder(small, 8, numerics="fast")
         dec.set_profiling(True)
         dec.forward(np.arange(1, 41, dtype=np.uint32) * 7)
         rows = [dec.forward([int(tok)]) for tok in feed]
@@ -183,7 +185,7 @@ def test_xcd_local_attention_matches_the_memory_path(rt, wide, oracle, monkeypat
         monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_MERGE", merge)
         monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_Q", q)
         monkeypatch.setenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH", force)
-        dec = rt.Decoder(wide, 8)
+        dec = rt.Decoder(wide, 8, numerics="fast")
         dec.set_profiling(True)
         dec.forward(prompt)
         rows = [dec.forward([int(tok)]) for tok in feed]
@@ -202,7 +204,7 @@ def test_xcd_local_attention_matches_the_memory_path(rt, wide, oracle, monkeypat
 
 
 def test_step_is_deterministic_across_reset(rt, small):
-    dec = rt.Decoder(small, 8)
+    dec = rt.Decoder(small, 8, numerics="fast")
     prompt = np.arange(3, 53, dtype=np.uint32)
     outs = []
     for _ in range(2):

@@ -42,13 +42,15 @@ def read_capture(path):
     return x, q, sx, acc, at
 
 
-def test_decode_step_quantization_and_int32_dots_equal_the_oracle(full_artifacts, oracle, tmp_path, monkeypatch):
+@pytest.mark.parametrize("numerics", ["fast", "reference"])
+def test_decode_step_quantization_and_int32_dots_equal_the_oracle(full_artifacts, oracle, tmp_path, monkeypatch,
+                                                                   numerics):
     from leaf_amd import models, runtime
     from leaf_amd.artifact import load_tensor
     path = full_artifacts("tinyllama")
     capture = tmp_path / "step.cap"
     monkeypatch.setenv("LEAF_DECODE_STEP_CAPTURE", str(capture))
-    dec = runtime.Decoder(path, 8)
+    dec = runtime.Decoder(path, 8, numerics=numerics)
     prompt = np.random.default_rng(17).integers(0, dec.vocabulary_size, 40).astype(np.uint32)
     token = dec.forward_into(prompt, None)
     dec.set_profiling(True)
