@@ -197,6 +197,15 @@ lh_status lh_set_kernel_numerics(uint32_t numerics);
  * FMA (the exp of the CPU path's softmax and SiLU, transformer.cpp:134,
  * decoder.cpp:983), for every float input. */
 lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream);
+/* sums[i] = (...((0 + x[i][0]) + x[i][1]) + ...) + x[i][n - 1] in float, the
+ * order in which norm() sums its squares and attention_impl its softmax
+ * denominator (decoder.cpp:716-718, transformer.cpp:127-130), for count rows
+ * of n <= 8192 values; values must be >= 0 for method 0, which forms that sum
+ * in parallel (the reference-order decode step's way; bit-identical), while
+ * method 1 adds one by one.  cycles (may be NULL): the GPU clock cycles each
+ * row's sum took.  No reference counterpart: a diagnostic of this build. */
+lh_status lh_sequential_sum(const float* x, size_t n, size_t count, float* sums, int64_t* cycles,
+                            uint32_t method, lh_stream stream);
 
 /* One weight matrix as stored in a LEAFDC artifact (Weight, decoder.cpp:236-251):
  * bits 32 = f32, 16 = BF16 bits, 8 = int8, 4 = signed nibbles (low = even column);

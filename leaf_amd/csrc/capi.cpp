@@ -549,6 +549,18 @@ lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream) {
     });
 }
 
+lh_status lh_sequential_sum(const float* x, size_t n, size_t count, float* sums, int64_t* cycles, uint32_t method,
+                            lh_stream stream) {
+    return guarded([&] {
+        require_arg(x && sums && n >= 1 && n <= size_t(leafhip::kSequentialSumMax) && count >= 1 &&
+                        count <= 0x7fffffff && method <= 1,
+                    "invalid sequential sum call");
+        leafhip::launch_sequential_sum(x, int(n), int(count), sums, reinterpret_cast<long long*>(cycles),
+                                       int(method), as_stream(stream));
+        leafhip::hip_check(hipGetLastError(), "sequential sum launch");
+    });
+}
+
 lh_status lh_quantize_rows_i8(const float* x, size_t rows, size_t cols, int8_t* q, float* scales, lh_stream stream) {
     return guarded([&] {
         require_arg(x && q && scales && rows && cols && rows <= 0x7fffffff && cols <= 0x7fffffff, "invalid quantization call");

@@ -94,6 +94,8 @@ struct StepParams {
 bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int vocab, int blocks);
 // ... and, in addition, in reference order (StepParams::reference).
 bool decode_step_fits_reference(int hidden, int activation);
+// Most visible keys a step takes in reference order (longer contexts decode on the graph path).
+int decode_step_reference_keys();
 // Attention spans for `keys` visible keys.
 int decode_step_spans(int keys);
 // Blocks the step runs on (one per CU), or 0 when one block per CU cannot be resident.

@@ -38,6 +38,7 @@
 
 #include "device_common.h"
 #include "libm_expf.h"
+#include "sequential_sum.h"
 
 namespace leafhip {
 namespace {
@@ -108,11 +109,22 @@ struct __align__(16) Shared {
 };
 
 // Reference order adds each chain wave's softmax terms of one query head
-// (scores, then exp(score - max), then the probabilities), kept in key order.
-constexpr int kRefMaxKeys = kStepMaxSpans * kStepSpanKeys;
+// (scores, then exp(score - max), then the probabilities) in the transposed
+// layout of wave_sequential_sum, and per exchange wave the scratch of that
+// sum, which the p.v chain then uses to stage its V rows.
+constexpr int kRefMaxKeys = 2048;   // visible keys of the reference-order step (kSeqSumMaxPerLane per lane)
+static_assert(kRefMaxKeys == kWave * kSeqSumMaxPerLane, "the denominator's terms fit one register chunk per lane");
+static_assert(kA * kRefMaxKeys <= kStepSpanKeys * kStepDim, "s.v holds each chain wave's probabilities in key order");
 struct __align__(16) SharedRef : Shared {
     float pe[kA][kRefMaxKeys];
+    float4 area[kA][kSeqSumArea];
+    // pe and area, both free then, stage the gated activation while its
+    // maximum is traded (quantize_into)
+    __device__ float* stage() { return &pe[0][0]; }
 };
+static_assert(sizeof(float) * kA * kRefMaxKeys + sizeof(float4) * kA * kSeqSumArea >= sizeof(float) * kNF * kAT,
+              "pe and area hold an ffn-wide vector's runs");
+static_assert(sizeof(SharedRef) <= 160 * 1024, "one block per CU holds the reference-order LDS");
 
 // Wave reductions on DPP lane moves instead of LDS-crossbar shuffles: xor 1
 // and xor 2 (quad permutes), then the half-row and row mirrors (once lanes of
@@ -476,27 +488,27 @@ __device__ __forceinline__ void post(Shared& s, int phase) {
 
 // RMSNorm of the n values held as runs (decoder.cpp:706-727).  In reference
 // order the squares are summed in column order, as norm() sums them: every
-// lane stores its runs' squares in column order (s.xf is free until the
-// head), exchange wave 0 adds them one by one and trades the sum to wave 1;
-// the normalized value is (x - 0) * scale * gamma + 0, norm()'s expression
-// with mean 0 and no beta.
+// lane stores its runs' squares (s.xf is free until the head) in the layout
+// of wave_sequential_sum, and each exchange wave forms the column-order sum
+// itself (no second trade); the normalized value is (x - 0) * scale * gamma
+// + 0, norm()'s expression with mean 0 and no beta.
 template <bool REF, int N>
 __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
                                               Shared& s, int& round) {
     const int live = n / kRun - a;
     float sq = 0.0f;
     if constexpr (REF) {
+        const SeqLayout lay(n);
 #pragma unroll
         for (int g = 0; g < N / kRun; ++g)
             if (g * kAT < live) {
+                const int e = kRun * run_of(g, a);
                 const float x0 = x[kRun * g] - 0.0f, x1 = x[kRun * g + 1] - 0.0f;
-                *reinterpret_cast<v2f*>(s.xf + kRun * run_of(g, a)) = v2f{x0 * x0, x1 * x1};
+                s.xf[lay.at(e)] = x0 * x0;
+                s.xf[lay.at(e + 1)] = x1 * x1;
             }
         if (!a_sync(s, round)) return false;   // both waves' squares are in place
-        if (a < kWave) sq = sequential_sum(s.xf, n);
-        float other;
-        if (!a_trade(sq, other, s, round)) return false;
-        if (a >= kWave) sq = other;
+        sq = wave_sequential_sum(s.xf, n, static_cast<SharedRef&>(s).area[a >> 6]);
         const float scale = 1.0f / sqrtf(sq / (float)n + eps);
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = (x[i] - 0.0f) * scale * gamma[i] + 0.0f;
@@ -508,28 +520,6 @@ __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float 
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
     }
-    return true;
-}
-
-// Per-token symmetric int8 quantization into s.xq[buf] (decoder.cpp:1028-1043).
-// Runs past n land in the buffer's tail, which no reader uses.
-template <int N>
-__device__ __forceinline__ bool quantize_into(const float (&x)[N], int n, int buf, int a, Shared& s, int& round) {
-    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
-    const int live = n / kRun - a;
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / kRun) * kAT < live ? fabsf(x[i]) : 0.0f);
-    if (!a_max(amax, s, round)) return false;
-    const float sx = fmaxf(amax / 127.0f, 1e-12f);
-    const float multiplier = 1.0f / sx;
-#pragma unroll
-    for (int g = 0; g < N / kRun; ++g) {
-        const float* v = x + kRun * g;
-        *reinterpret_cast<uint16_t*>(s.xq[buf] + kRun * run_of(g, a)) =
-            (uint16_t)((quantize_one(v[0], multiplier) & 255) | ((quantize_one(v[1], multiplier) & 255) << 8));
-    }
-    if (a == 0) s.sx[buf] = sx;
     return true;
 }
 
@@ -552,6 +542,69 @@ __device__ __forceinline__ void load_runs(float (&x)[N], const float* src, int a
         x[kRun * g] = v[0];
         x[kRun * g + 1] = v[1];
     }
+}
+
+// Per-token symmetric int8 quantization into s.xq[buf] (decoder.cpp:1028-1043).
+// Runs past n land in the buffer's tail, which no reader uses.  With `stage`
+// the values wait in LDS (this lane's runs) while the maximum is traded, so
+// they hold no registers across the wait.
+template <int N>
+__device__ __forceinline__ bool quantize_into(float (&x)[N], int n, int buf, int a, Shared& s, int& round,
+                                              float* stage = nullptr) {
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
+    const int live = n / kRun - a;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax = fmaxf(amax, (i / kRun) * kAT < live ? fabsf(x[i]) : 0.0f);
+    if (stage) store_runs(stage, x, a);
+    if (!a_max(amax, s, round)) return false;
+    if (stage) load_runs(x, stage, a);
+    const float sx = fmaxf(amax / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g) {
+        const float* v = x + kRun * g;
+        *reinterpret_cast<uint16_t*>(s.xq[buf] + kRun * run_of(g, a)) =
+            (uint16_t)((quantize_one(v[0], multiplier) & 255) | ((quantize_one(v[1], multiplier) & 255) << 8));
+    }
+    if (a == 0) s.sx[buf] = sx;
+    return true;
+}
+
+// Reference order streams the gated activation through LDS instead (its 48
+// values per lane and the 64-bit words they arrive in would not fit the
+// exchange waves' registers beside the rest): runs G0 .. G0 + N/kRun - 1 of
+// the vector, once they carry `epoch`, go to `stage` (natural element order)
+// and into the running maximum of |x|.
+template <int N, int G0>
+__device__ __forceinline__ bool await_staged(const u64* src, int n, unsigned epoch, float* stage, float& amax, int a,
+                                             const StepParams& P) {
+    float x[N];
+    if (!await_runs<N, G0, false>(src, n, epoch, x, a, P)) return false;
+    const int live = n / kRun - a - kAT * G0;
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g) {
+        if (g * kAT < live) amax = fmaxf(amax, fmaxf(fabsf(x[kRun * g]), fabsf(x[kRun * g + 1])));
+        *reinterpret_cast<v2f*>(stage + kRun * run_of(G0 + g, a)) = v2f{x[kRun * g], x[kRun * g + 1]};
+    }
+    return true;
+}
+// quantize_into for a vector staged by await_staged (amax: this lane's part).
+template <int N>
+__device__ __forceinline__ bool quantize_staged(const float* stage, int n, int buf, float amax, int a, Shared& s,
+                                                int& round) {
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
+    if (!a_max(amax, s, round)) return false;
+    const float sx = fmaxf(amax / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g) {
+        const v2f v = *reinterpret_cast<const v2f*>(stage + kRun * run_of(g, a));
+        *reinterpret_cast<uint16_t*>(s.xq[buf] + kRun * run_of(g, a)) =
+            (uint16_t)((quantize_one(v[0], multiplier) & 255) | ((quantize_one(v[1], multiplier) & 255) << 8));
+    }
+    if (a == 0) s.sx[buf] = sx;
+    return true;
 }
 
 // gamma for this lane's runs; runs past n read the last one (their x are 0).
@@ -911,55 +964,123 @@ __device__ __forceinline__ void ref_score_item(const StepParams& P, Shared& s, i
 
 // Reference order, the rest of one query head's attention in one wave
 // (attention_impl, transformer.cpp:122-143): the scores of its n visible keys
-// (pe, key order) -> the maximum (NaN scores never become it, as with
-// std::max) -> exp(s - max) with glibc's expf -> the denominator summed in key
-// order -> p = e / denominator -> output[d] += p * v[d] in key order, lane d.
-// Cached keys' V rows come from the cache (this XCD's items loaded them a
-// moment ago); the new key's from the exchange words of q|k|v.  A fully
-// masked or infinite row leaves the zero output, like the CPU.  Returns
-// false (abort raised) when a wait failed; o is this lane's output element.
-__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, int n, float m, const float* V,
-                                          const u64* vnew_word, unsigned vnew_epoch, int lane, float& o) {
+// (pe, in wave_sequential_sum's layout) -> the maximum (NaN scores never
+// become it, as with std::max) -> exp(s - max) with glibc's expf -> the
+// denominator summed in key order (wave_sequential_sum) -> p = e / denominator
+// -> output[d] += p * v[d] in key order, lane d.  V rows of the cached keys
+// come from the cache (this XCD's items loaded them a moment ago) as 16-byte
+// loads, kChainDepth chunks of kChainKeys keys in flight, each chunk staged
+// in `stage` (row-major) so that lane d reads its column; the new key's row
+// comes from the exchange words of q|k|v.  A fully masked or infinite row
+// leaves the zero output, like the CPU.  Returns false (abort raised) when a
+// wait failed; o is this lane's output element.
+constexpr int kChainKeys = 16;                                      // keys per V chunk
+constexpr int kChainDepth = 4;                                      // chunks in flight
+constexpr int kChainF4 = kChainKeys * kStepDim / 4 / kWave;         // float4 per lane per chunk
+static_assert(kChainKeys * kStepDim <= 4 * kSeqSumArea, "a V chunk fits the wave's staging area");
+__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float* pnat, float4* area, int n, float m,
+                                          const float* V, const u64* vnew_word, unsigned vnew_epoch, int lane,
+                                          float& o) {
     constexpr int dim = kStepDim;
     o = 0.0f;
     const float maximum = dpp_max_f32(m);
     if (!isfinite(maximum)) return true;
+    const int E = seq_per_lane(n);
+    const int valid = min(max(n - lane * E, 0), E);
+    const int cached = n - 1;   // the new key is the last visible one
+    const int chunks = (cached + kChainKeys - 1) / kChainKeys;
+    // V rows through a bounds-checked buffer view of the cached rows: rows
+    // past them read as 0, so the loads need no clamping.  Lane l's float4 i
+    // of a chunk: key 4 i + l / 16, columns 4 (l % 16) ..
+    const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(V), (short)0, cached * dim * (int)sizeof(float), kRawBufferWord3);
+    const int voff = (lane >> 4) * dim * (int)sizeof(float) + (lane & 15) * 16;
+    constexpr int kChunkBytes = kChainKeys * kStepDim * (int)sizeof(float);
+    v4u ring[kChainDepth][kChainF4];
+    auto load = [&](v4u (&r)[kChainF4], int c) {
+        const int at = voff + c * kChunkBytes;
+#pragma unroll
+        for (int i = 0; i < kChainF4; ++i)
+            r[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, at + i * 4 * dim * (int)sizeof(float), 0, 0);
+    };
     lds_done();
-    for (int k = lane; k < n; k += kWave) pe[k] = libm_expf(pe[k] - maximum);
+    // exp(s - max) of this lane's keys (lane * E + i, at row i of column lane),
+    // four at a time (a wider unroll interleaves so many expf evaluations that
+    // their registers spill)
+    for (int i0 = 0; i0 < E; i0 += 4) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = pe[min(i0 + i, E - 1) * kWave + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = i0 + i < valid ? libm_expf(e[i] - maximum) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i0 + i < E) pe[(i0 + i) * kWave + lane] = e[i];
+    }
     lds_done();
-    const float den = sequential_sum(pe, n);   // every lane: broadcast reads
-    for (int k = lane; k < n; k += kWave) pe[k] = pe[k] / den;
+    // the first chunks' V rows load while the denominator is formed
+#pragma unroll
+    for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
+    const float den = wave_sequential_sum(pe, n, area);
+    // p = e / den in key order (pnat), read four keys at a time below
+    for (int i0 = 0; i0 < E; i0 += 8) {
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = pe[min(i0 + i, E - 1) * kWave + lane];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i0 + i < valid) pnat[lane * E + i0 + i] = e[i] / den;
+    }
+    lds_done();
+    float* stage = reinterpret_cast<float*>(area);
+    // Software-pipelined: chunk c + 1 is staged (the wave's LDS accesses
+    // complete in order, so one staging buffer serves every chunk) and read
+    // into registers while chunk c is added; its loads are replaced by those
+    // of chunk c + 1 + kChainDepth right after staging, unconditionally, so
+    // the wait before staging a chunk counts exactly the loads issued after it.
+    float vv[2][kChainKeys];
+    v4f pp[2][kChainKeys / 4];
+    auto stage_read = [&](const v4u (&r)[kChainF4], int c, float (&v)[kChainKeys], v4f (&p)[kChainKeys / 4]) {
+#pragma unroll
+        for (int i = 0; i < kChainF4; ++i)
+            *reinterpret_cast<v4u*>(stage + (4 * i + (lane >> 4)) * dim + 4 * (lane & 15)) = r[i];
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < kChainKeys; ++j) v[j] = stage[j * dim + lane];
+#pragma unroll
+        for (int j = 0; j < kChainKeys / 4; ++j)
+            p[j] = *reinterpret_cast<const v4f*>(pnat + min(c * kChainKeys, kRefMaxKeys - kChainKeys) + 4 * j);
+    };
+    // Keys past a chunk's count add (+0) * v = +-0, which leaves the sum
+    // unchanged (it starts at +0 and is never -0); full chunks skip the select.
+    auto add = [&](const float (&v)[kChainKeys], const v4f (&p)[kChainKeys / 4], int c) {
+        const int keys = cached - c * kChainKeys;
+        if (keys >= kChainKeys) {
+#pragma unroll
+            for (int j = 0; j < kChainKeys; ++j) o = o + p[j / 4][j % 4] * v[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < kChainKeys; ++j) o = o + (j < keys ? p[j / 4][j % 4] : 0.0f) * v[j];
+        }
+    };
+    if (chunks > 0) {
+        stage_read(ring[0], 0, vv[0], pp[0]);
+        load(ring[0], kChainDepth);
+    }
+    for (int c0 = 0; c0 < chunks; c0 += kChainDepth) {
+#pragma unroll
+        for (int u = 0; u < kChainDepth; ++u) {
+            const int c = c0 + u;
+            if (c >= chunks) break;
+            stage_read(ring[(u + 1) % kChainDepth], c + 1, vv[(u + 1) & 1], pp[(u + 1) & 1]);
+            load(ring[(u + 1) % kChainDepth], c + 1 + kChainDepth);
+            add(vv[u & 1], pp[u & 1], c);
+        }
+    }
     lds_done();
     float vnew;
     if (!await_one(vnew_word, true, vnew_epoch, vnew, P)) return false;
-    const int cached = n - 1;   // the new key is the last visible one
-    constexpr int B = 16;
-    auto load = [&](float (&d)[B], int k0) {
-#pragma unroll
-        for (int j = 0; j < B; ++j) d[j] = ldg(V + (size_t)(k0 + j) * dim);
-    };
-    auto add = [&](const float (&d)[B], int k0) {
-        float p[B];
-#pragma unroll
-        for (int j = 0; j < B; ++j) p[j] = pe[k0 + j];
-#pragma unroll
-        for (int j = 0; j < B; ++j) o = o + p[j] * d[j];
-    };
-    // two batches in flight: the next batch's V rows load while one is added
-    int k = 0;
-    float va[B], vb[B];
-    if (cached >= B) load(va, 0);
-    while (k + B <= cached) {
-        if (k + 2 * B <= cached) load(vb, k + B);
-        add(va, k);
-        k += B;
-        if (k + B > cached) break;
-        if (k + 2 * B <= cached) load(va, k + B);
-        add(vb, k);
-        k += B;
-    }
-    for (; k < cached; ++k) o = o + pe[k] * ldg(V + (size_t)k * dim);
-    o = o + pe[cached] * vnew;
+    o = o + pnat[cached] * vnew;
     return true;
 }
 
@@ -1262,20 +1383,22 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
                 float m = -INFINITY;
                 v2f ml;
                 float os[kMergeBatch];
+                const SeqLayout lay(n);
                 for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
                     ok = await_partials(base, (int)stride, spans, s0, lane, epoch(L, 2), ml, os, P);
 #pragma unroll
                     for (int j = 0; j < kMergeBatch; ++j) {
                         const int k = (s0 + j) * kStepSpanKeys + lane;
                         if (ok && k < n) {
-                            pe[k] = os[j];
+                            pe[lay.at(k)] = os[j];
                             m = m < os[j] ? os[j] : m;
                         }
                     }
                 }
                 float o = 0.0f;
                 if (ok)
-                    ok = ref_chain(P, pe, n, m, Vc + ((size_t)g * P.capacity + begin) * dim + lane,
+                    ok = ref_chain(P, pe, s.v + aw * kRefMaxKeys, static_cast<SharedRef&>(s).area[aw], n, m,
+                                   Vc + ((size_t)g * P.capacity + begin) * dim,
                                    P.x_qkv + qw + kvw + g * dim + lane, epoch(L, 1), lane, o);
                 if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), o);
             }
@@ -1347,15 +1470,34 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         post(s, 4 * L + 2);
         // ---- SiLU-gated activation -> int8 for down_proj
         {
-            float xd[kNF];
             bool ok = wait_published(s, 4 * L + 3);
-            ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
-            stamp(P.trace, b, 64 * L + 63, kWave);
-            if (!a_check(ok, s, P)) return false;
-            note_received(s, 4 * L + 3);
-            stamp(P.trace, b, 64 * L + 7);
-            if (!quantize_into(xd, F, 1, a, s, round)) return false;
-            capture_input<CAP>(P, s, xd, F, 1, L, 3, a);
+            if constexpr (REF) {
+                float* st = static_cast<SharedRef&>(s).stage();
+                float amax = 0.0f;
+                ok = ok && await_staged<kNF / 4, 0>(P.x_act, F, epoch(L, 5), st, amax, a, P);
+                ok = ok && await_staged<kNF / 4, kNF / 4 / kRun>(P.x_act, F, epoch(L, 5), st, amax, a, P);
+                ok = ok && await_staged<kNF / 4, kNF / 2 / kRun>(P.x_act, F, epoch(L, 5), st, amax, a, P);
+                ok = ok && await_staged<kNF / 4, 3 * kNF / 4 / kRun>(P.x_act, F, epoch(L, 5), st, amax, a, P);
+                stamp(P.trace, b, 64 * L + 63, kWave);
+                if (!a_check(ok, s, P)) return false;
+                note_received(s, 4 * L + 3);
+                stamp(P.trace, b, 64 * L + 7);
+                if (!quantize_staged<kNF>(st, F, 1, amax, a, s, round)) return false;
+                if constexpr (CAP) {
+                    float xd[kNF];
+                    load_runs(xd, st, a);
+                    capture_input<CAP>(P, s, xd, F, 1, L, 3, a);
+                }
+            } else {
+                float xd[kNF];
+                ok = ok && await_runs<kNF, 0, false>(P.x_act, F, epoch(L, 5), xd, a, P);
+                stamp(P.trace, b, 64 * L + 63, kWave);
+                if (!a_check(ok, s, P)) return false;
+                note_received(s, 4 * L + 3);
+                stamp(P.trace, b, 64 * L + 7);
+                if (!quantize_into(xd, F, 1, a, s, round)) return false;
+                capture_input<CAP>(P, s, xd, F, 1, L, 3, a);
+            }
             post(s, 4 * L + 3);
         }
         // ---- the next layer's input (the last layer's feeds the head below)
@@ -1377,6 +1519,8 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         note_received(s, 4 * P.layers);
         stamp(P.trace, b, 64 * P.layers + 1);
         if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round)) return false;
+        // (reference order: the other wave may still be reading its squares from s.xf)
+        if (REF && !a_sync(s, round)) return false;
         store_runs(s.xf, x, a);
         post(s, 4 * P.layers);
     }
@@ -1831,6 +1975,8 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
     return (pairs + blocks - 1) / blocks <= kQP * kB && (hidden + blocks - 1) / blocks <= kOR * kB &&
            (ffn + blocks - 1) / blocks <= kGP * kB;
 }
+
+int decode_step_reference_keys() { return kRefMaxKeys; }
 
 bool decode_step_fits_reference(int hidden, int activation) {
     // the head's dot_avx chains cover the row in whole 32-column blocks;

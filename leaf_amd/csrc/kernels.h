@@ -209,6 +209,14 @@ void launch_activation_reference_order(const float* gate_up, int tokens, int wid
                                        float* act, hipStream_t stream);
 // y[i] = expf(x[i]) as glibc computes it.
 void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream);
+// sums[i] = the column-order f32 sum of row i of x [count, n] (norm()'s and
+// the softmax denominator's order), by wave_sequential_sum (method 0) or by
+// one lane's plain chain (method 1); cycles[i] (may be null) = the clock
+// cycles the sum took.  False when n or method is out of range.
+constexpr int kSequentialSumMax = 8192;
+inline int seq_per_lane_host(int n) { return (n + 63) / 64; }
+bool launch_sequential_sum(const float* x, int n, int count, float* sums, long long* cycles, int method,
+                           hipStream_t stream);
 // dot_avx / dot_source_bf16_avx order for FP32, BF16, INT8 and INT4 weights with
 // FP32 activations, tokens in groups of four; y = result + bias (kStore) or
 // y += result + bias (kAccumulate).  False for other storage.

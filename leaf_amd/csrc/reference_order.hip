@@ -33,6 +33,7 @@
 #include "device_common.h"
 #include "kernels.h"
 #include "libm_expf.h"
+#include "sequential_sum.h"
 
 #include <math.h>
 
@@ -358,6 +359,27 @@ __global__ void ro_activation_kernel(const float* gate_up, int tokens, int width
     }
 }
 
+// One wave per vector: the vector staged in LDS in wave_sequential_sum's
+// layout, then its column-order sum by that function (method 0) or by the
+// plain chain (method 1), with the clock cycles the sum took.
+__global__ __launch_bounds__(kWave) void ro_sequential_sum_kernel(const float* x, int n, float* sums,
+                                                                  long long* cycles, int method) {
+    extern __shared__ float lds[];
+    float4* area = reinterpret_cast<float4*>(lds);
+    float* v = lds + 4 * kSeqSumArea;
+    const float* row = x + (size_t)blockIdx.x * n;
+    const SeqLayout lay(n);
+    for (int j = threadIdx.x; j < n; j += kWave) v[lay.at(j)] = row[j];
+    __syncthreads();
+    const long long t0 = clock64();
+    const float s = method == 0 ? wave_sequential_sum(v, n, area) : seq_chain(v, n, lay.E);
+    const long long t1 = clock64();
+    if (threadIdx.x == 0) {
+        sums[blockIdx.x] = s;
+        if (cycles) cycles[blockIdx.x] = t1 - t0;
+    }
+}
+
 __global__ void ro_expf_kernel(const float* x, size_t count, float* y) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
         y[i] = libm_expf(x[i]);
@@ -556,6 +578,14 @@ void launch_activation_reference_order(const float* gate_up, int tokens, int wid
     const size_t count = (size_t)tokens * width;
     const int grid = (int)std::min<size_t>((count + kRoBlock - 1) / kRoBlock, 4096);
     ro_activation_kernel<<<grid, kRoBlock, 0, stream>>>(gate_up, tokens, width, gated, activation, act);
+}
+
+bool launch_sequential_sum(const float* x, int n, int count, float* sums, long long* cycles, int method,
+                           hipStream_t stream) {
+    if (n < 1 || n > kSequentialSumMax || count < 1 || (method != 0 && method != 1)) return false;
+    const size_t lds = (size_t)kSeqSumArea * sizeof(float4) + (size_t)seq_per_lane_host(n) * kWave * sizeof(float);
+    ro_sequential_sum_kernel<<<count, kWave, lds, stream>>>(x, n, sums, cycles, method);
+    return true;
 }
 
 void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream) {

@@ -1,0 +1,242 @@
+// The sum  float s = 0; for (j = 0; j < n; ++j) s += v[j];  of n non-negative
+// floats, bit for bit, by one wave in a fraction of the time of the 2048-step
+// dependent chain (decoder.cpp:716-718 sums a norm's squares this way,
+// transformer.cpp:127-130 a softmax denominator).
+//
+// Why it can be split.  While the running sum s and the exact sum s + a of a
+// step lie in one binade [2^e, 2^(e+1)), s is a multiple of the binade's unit
+// g = 2^(e-23) and the step rounds to nearest on that grid, so
+//     fl(s + a) = s + g * rint(a / g)
+// whenever a / g is not a tie: the step's increment does not depend on s.  The
+// increments of such "safe" steps are multiples of g that stay below 2^(e+1),
+// so any order of adding them is exact.  Only the other steps need the true s:
+// those where the sum enters the next binade (about log2(n) of them), those
+// whose binade is not certain, and ties, which round to the even neighbour.
+//
+// How.  Lane l takes elements [l E, (l + 1) E), E = ceil(n / 64).
+//   1. An approximate exclusive prefix P of every element (lane totals in
+//      f32, a scan over the lanes, running sums in the lane).
+//   2. The true running sum s_j differs from P_j by less than
+//      (j + 2E + 8) 2^-24 P_j (each of the j earlier steps rounds by at most
+//      2^-24 of the sum so far; P has at most 2E + 8 roundings on its path);
+//      with d a little wider than that, a step is safe when P_j (1 - d) and
+//      (P_j + a_j) (1 + d) lie in one binade, a_j / g is not a tie and g is
+//      at least 2^-27 of the total (so the increments' f64 prefix sums are
+//      exact).  Safe increments are added in f64 per lane and scanned over the
+//      lanes: I_j, the exact sum of the safe increments before element j.
+//   3. Every other step (at most kSeqSumCap per lane) is recorded with its
+//      I_j and a_j, compacted in element order, and walked: between two such
+//      steps the sum grows by exactly I_q - I_p (a multiple of that run's g,
+//      so exact in f32 too); at each one, s = fl(s + a) is the real step.
+// Lane 0's chunk, where the binade changes at almost every doubling, is summed
+// one by one instead (its in-order total).  A lane with more than
+// kSeqSumCap unsafe steps, negative, infinite, NaN or subnormal terms, or a
+// total of 2^126 or more, falls back to the plain chain.
+//
+// The values sit in LDS in the transposed layout of SeqLayout: element j of
+// lane l's chunk at row j - l E, column l, so the lanes' reads of their chunks
+// meet different banks.  Every lane returns the sum.
+#pragma once
+
+#include "device_common.h"
+
+namespace leafhip {
+
+constexpr int kSeqSumCap = 12;                    // unsafe steps one lane records
+constexpr int kSeqSumArea = kWave * (kSeqSumCap + 1);   // float4 of LDS scratch per wave (one spare per lane)
+
+// Where element j of an n-element vector lives (E = seq_per_lane(n)):
+// (j mod E) * 64 + j / E.  The quotient comes from a float reciprocal and one
+// correction (exact for j < 2^24), not a 32-bit integer division.
+struct SeqLayout {
+    int E;
+    float inv;
+    __device__ explicit SeqLayout(int n) : E((n + kWave - 1) / kWave), inv(1.0f / (float)E) {}
+    __device__ __forceinline__ int at(int j) const {
+        int q = (int)((float)j * inv);
+        int r = j - q * E;
+        if (r >= E) { ++q; r -= E; }
+        if (r < 0) { --q; r += E; }
+        return r * kWave + q;
+    }
+};
+__device__ __forceinline__ int seq_per_lane(int n) { return (n + kWave - 1) / kWave; }
+
+// Elements [0, m) in order (lane by lane, a lane's chunk top to bottom), 32
+// LDS reads in flight at a time.
+__device__ __forceinline__ float seq_chain(const float* v, int m, int E) {
+    float s = 0.0f;
+    for (int l = 0; l * E < m; ++l) {
+        const int end = min(E, m - l * E);
+        for (int i0 = 0; i0 < end; i0 += 32) {
+            float e[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) e[i] = v[min(i0 + i, end - 1) * kWave + l];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) s = s + (i0 + i < end ? e[i] : 0.0f);   // + 0 leaves s unchanged
+        }
+    }
+    return s;
+}
+
+// Inclusive prefix sums over the wave's lanes on DPP lane moves: shifts by
+// 1, 2, 4 and 8 inside each 16-lane row, then the row totals broadcast to the
+// rows above (row_bcast:15 to rows 1 and 3, row_bcast:31 to rows 2 and 3).
+// Lanes a move does not reach add 0.  Exact for integers and for floating
+// values whose partial sums are all representable.
+constexpr int kDppRowShr = 0x110;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+constexpr int kDppWaveShr1 = 0x138;      // lane i reads lane i - 1 (lane 0: 0)
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ unsigned dpp_move(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, RowMask, 0xF, false);
+}
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ double dpp_move(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = dpp_move<Ctrl, RowMask>((unsigned)b), hi = dpp_move<Ctrl, RowMask>((unsigned)(b >> 32));
+    return __longlong_as_double((long long)((unsigned long long)lo | ((unsigned long long)hi << 32)));
+}
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __uint_as_float(dpp_move<Ctrl, RowMask>(__float_as_uint(v)));
+}
+template <int Ctrl, int RowMask = 0xF>
+__device__ __forceinline__ int dpp_move(int v) {
+    return (int)dpp_move<Ctrl, RowMask>((unsigned)v);
+}
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_sum(T x) {
+    x = x + dpp_move<kDppRowShr + 1>(x);
+    x = x + dpp_move<kDppRowShr + 2>(x);
+    x = x + dpp_move<kDppRowShr + 4>(x);
+    x = x + dpp_move<kDppRowShr + 8>(x);
+    x = x + dpp_move<kDppRowBcast15, 0xA>(x);
+    x = x + dpp_move<kDppRowBcast31, 0xC>(x);
+    return x;
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double lane_value(double v, int l) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __longlong_as_double((long long)((unsigned long long)lo | ((unsigned long long)hi << 32)));
+}
+
+// v: n >= 1 non-negative floats in the transposed layout; area: this wave's
+// kSeqSumArea float4 of LDS scratch.  Each lane holds its chunk in registers
+// (up to kSeqSumMaxPerLane values: n <= 2048; longer vectors take the chain).
+// Branch-free: loads and stores are unconditional (clamped indices, a
+// per-lane spare slot for the stores that record nothing), so every LDS
+// access of a phase is in flight at once.
+constexpr int kSeqSumMaxPerLane = 32;
+__device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
+    // A fresh lane index per call: callers inside long loops would otherwise
+    // have the lane-dependent constants below hoisted and held in registers.
+    int lane = threadIdx.x & (kWave - 1);
+    asm volatile("" : "+v"(lane));
+    const int E = seq_per_lane(n);
+    if (E > kSeqSumMaxPerLane) return seq_chain(v, n, E);
+    const int j0 = lane * E;
+    const int valid = min(max(n - j0, 0), E);      // this lane's elements; the rest read as +0
+    const int spare = kWave * kSeqSumCap + lane;
+    // 1. this lane's chunk, its in-order total, and the inputs' check: the
+    // largest bit pattern (negative, infinite or NaN terms reach 0x7f800000)
+    // and the smallest nonzero one (subnormal terms are below 0x00800000)
+    float x[kSeqSumMaxPerLane];
+#pragma unroll
+    for (int i = 0; i < kSeqSumMaxPerLane; ++i) x[i] = v[min(i, E - 1) * kWave + lane];
+    float T = 0.0f;
+    unsigned umax = 0u, umin = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < kSeqSumMaxPerLane; ++i) {
+        x[i] = i < valid ? x[i] : 0.0f;
+        T = T + x[i];   // padding adds +0, which leaves a sum of non-negative terms unchanged
+        const unsigned u = __float_as_uint(x[i]);
+        umax = max(umax, u);
+        umin = min(umin, u - 1u);   // 0 wraps to the top
+    }
+    const float incl = wave_inclusive_sum(T);
+    const float S = lane_value(incl, kWave - 1);
+    float P = dpp_move<kDppWaveShr1>(incl);   // the exclusive prefix (lane 0: 0)
+    if (__any(umax >= 0x7f800000u || umin < 0x007fffffu) || !(S < 0x1p126f)) return seq_chain(v, n, E);
+    if (S == 0.0f) return 0.0f;                     // all terms zero: the chain stays +0
+    // the head: lane 0's chunk, whose in-order total is its T
+    const float head = lane_value(T, 0);
+    // 2. safe increments, f64 per lane; unsafe steps recorded.  Padding terms
+    // (+0) change nothing: safe, they add 0; recorded, the walk adds 0.
+    const unsigned ebS = __float_as_uint(S) >> 23;
+    const unsigned ebmin = ebS > 51u ? ebS - 27u : 24u;
+    const float d = (float)(j0 + 3 * E + 16) * 0x1.1p-24f;
+    const float clo = 1.0f - d, chi = 1.0f + d;
+    const bool body = lane >= 1;
+    double J = 0.0;
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kSeqSumMaxPerLane; ++i) {
+        if (i < E) {   // wave-uniform
+            const float a = x[i];
+            const float Pn = P + a;
+            const unsigned blo = __float_as_uint(P * clo), bhi = __float_as_uint(Pn * chi);
+            const unsigned eb = bhi >> 23;
+            const float q = a * __uint_as_float((277u - eb) << 23);   // a / g, exact
+            const float inc = rintf(q) * __uint_as_float((eb - 23u) << 23);   // g rint(a / g)
+            const bool safe = (blo >> 23) == eb && eb - ebmin < 255u - ebmin && q - floorf(q) != 0.5f;
+            const bool rec = body && !safe;
+            const unsigned long long bits = (unsigned long long)__double_as_longlong(J);
+            area[rec && cnt < kSeqSumCap ? lane * kSeqSumCap + cnt : spare] =
+                make_float4(__uint_as_float((unsigned)bits), __uint_as_float((unsigned)(bits >> 32)), a, 0.0f);
+            cnt += rec ? 1 : 0;
+            J += body && safe ? (double)inc : 0.0;
+            P = Pn;
+        }
+    }
+    if (__any(cnt > kSeqSumCap)) return seq_chain(v, n, E);
+    // 3. scans: the lanes' safe totals (exact in f64) and unsafe counts
+    const double Jincl = wave_inclusive_sum(J);
+    const int cincl = wave_inclusive_sum(cnt);
+    const double Itot = lane_value(Jincl, kWave - 1);
+    const double Ibase = Jincl - J;                  // exact: every partial sum is
+    const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
+    const int off = cincl - cnt;
+    // compact the recorded steps in element order, with I = Ibase + J
+    float4 mine[kSeqSumCap];
+#pragma unroll
+    for (int k = 0; k < kSeqSumCap; ++k) mine[k] = area[lane * kSeqSumCap + k];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < kSeqSumCap; ++k) {
+        const unsigned long long jb = (unsigned long long)__float_as_uint(mine[k].x) |
+                                      ((unsigned long long)__float_as_uint(mine[k].y) << 32);
+        const double I = Ibase + __longlong_as_double((long long)jb);
+        const unsigned long long ib = (unsigned long long)__double_as_longlong(I);
+        area[k < cnt ? off + k : spare] =
+            make_float4(__uint_as_float((unsigned)ib), __uint_as_float((unsigned)(ib >> 32)), mine[k].z, 0.0f);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // 4. the walk, lane i taking recorded step i: the running sum moves one
+    // lane up per step (wave_shr:1), lane i adds its exact jump R_i to the
+    // step and then the step's term, fl(fl(s + R_i) + a_i).  Lane 0 of a batch
+    // starts from the sum so far (folded into its jump, exactly).
+    float s = head;
+    double prev = 0.0;
+    for (int b = 0; b < K; b += kWave) {
+        const float4 e = area[min(b + lane, K - 1)];
+        const double I = __longlong_as_double((long long)((unsigned long long)__float_as_uint(e.x) |
+                                                          ((unsigned long long)__float_as_uint(e.y) << 32)));
+        const double up = dpp_move<kDppWaveShr1>(I);
+        float R = (float)(I - (lane == 0 ? prev : up));   // exact jump to this step
+        if (lane == 0) R = s + R;                         // exact: the sum just before step b
+        const int m = min(kWave, K - b);
+        float t = 0.0f;
+        for (int i = 0; i < m; ++i) t = (dpp_move<kDppWaveShr1>(t) + R) + e.z;
+        s = lane_value(t, m - 1);
+        prev = lane_value(I, m - 1);
+    }
+    return s + (float)(Itot - prev);
+}
+
+}  // namespace leafhip

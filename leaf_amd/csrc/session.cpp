@@ -546,6 +546,7 @@ bool Session::step_usable() const {
     const size_t end = length + 1;
     const size_t begin = (c.sliding_window && end > c.sliding_window) ? end - c.sliding_window : 0;
     const int spans = decode_step_spans(int(end - begin));
+    if (reference_ && end - begin > size_t(decode_step_reference_keys())) return false;
     return spans <= kStepMaxSpans && size_t(spans) * c.kv_heads <= size_t(step_blocks_);
 }
 

@@ -130,6 +130,7 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_argmax": ([vp, sz, sz, vp, vp], i32),
         "lh_set_kernel_numerics": ([u32], i32),
         "lh_expf": ([vp, sz, vp, vp], i32),
+        "lh_sequential_sum": ([vp, sz, sz, vp, vp, u32, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -356,6 +357,13 @@ def set_kernel_numerics(numerics: str) -> None:
 
 def expf(x: DeviceArray, y: DeviceArray, stream=None) -> None:
     check(library().lh_expf(x.ptr, int(np.prod(x.shape)), y.ptr, stream))
+
+
+def sequential_sum(x: DeviceArray, n: int, count: int, sums: DeviceArray, cycles: DeviceArray | None = None,
+                   method: int = 0, stream=None) -> None:
+    """sums[i] = the float32 sum of row i in column order (lh_sequential_sum)."""
+    check(library().lh_sequential_sum(x.ptr, n, count, sums.ptr, cycles.ptr if cycles is not None else None,
+                                      method, stream))
 
 
 def quantize_rows(x: DeviceArray, rows: int, cols: int, q: DeviceArray, scales: DeviceArray, stream=None) -> None:
