@@ -160,6 +160,16 @@ typedef struct lh_profile_entry {
 lh_status lh_session_set_profiling(lh_session* session, int enable);
 /* Copies the accumulated entries and clears them. */
 lh_status lh_session_profile(lh_session* session, lh_profile_entry* out, size_t capacity, size_t* count);
+/* The session's numerics and the persistent decode step's record since the
+ * session began (no counterpart in the reference; for benchmarks and
+ * monitoring): whether the kernels follow the CPU engine's float order
+ * (LH_NUMERICS_DEFAULT resolved); tokens the persistent step produced; how
+ * many of those steps ran a second time on the memory exchange path because a
+ * block found itself off the XCD its index names; and whether the XCD-local
+ * exchange is still on (it is switched off for the session after four such
+ * steps in a row, or when the session never had it). */
+lh_status lh_session_status(const lh_session* session, int* reference_order, uint64_t* step_tokens,
+                            uint64_t* step_memory_reruns, int* xcd_local);
 /* Device pointer of the last forward's logits (valid until the next call). */
 lh_status lh_session_logits_device(const lh_session* session, const float** logits, size_t* count);
 

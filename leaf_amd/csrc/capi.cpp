@@ -433,6 +433,18 @@ lh_status lh_session_profile(lh_session* session, lh_profile_entry* out, size_t 
     });
 }
 
+lh_status lh_session_status(const lh_session* session, int* reference_order, uint64_t* step_tokens,
+                            uint64_t* step_memory_reruns, int* xcd_local) {
+    return guarded([&] {
+        require_arg(session && reference_order && step_tokens && step_memory_reruns && xcd_local,
+                    "session and outputs are required");
+        *reference_order = session->impl->reference_order() ? 1 : 0;
+        *step_tokens = session->impl->step_tokens();
+        *step_memory_reruns = session->impl->step_reruns();
+        *xcd_local = session->impl->step_xcd_local() ? 1 : 0;
+    });
+}
+
 lh_status lh_session_logits_device(const lh_session* session, const float** logits, size_t* count) {
     return guarded([&] {
         require_arg(session && logits && count, "session and outputs are required");

@@ -178,6 +178,12 @@ public:
         step_token_valid_ = false;
     }
     size_t cache_tokens() const { return length; }
+    // Tokens produced by the persistent decode step since the session began;
+    // of those, steps run a second time on the memory exchange path after a
+    // block ran off its XCD; whether the XCD-local exchange is still on.
+    uint64_t step_tokens() const { return step_tokens_; }
+    uint64_t step_reruns() const { return step_reruns_; }
+    bool step_xcd_local() const { return step_.x_part_local != nullptr; }
     // Decoder::forward_into (decoder.cpp:1282-1444)
     void forward(const uint32_t* ids, size_t count, bool all_logits, float* host_logits, size_t capacity,
                  uint32_t* argmax);
@@ -205,6 +211,8 @@ private:
     uint32_t step_token_ = 0;
     unsigned step_launch_ = 0;
     int step_xcd_misses_ = 0;        // consecutive steps re-run after an XCD mapping mismatch
+    uint64_t step_tokens_ = 0;       // tokens the persistent step produced
+    uint64_t step_reruns_ = 0;       // of those, steps run again on the memory exchange path
     double step_bytes_ = 0;          // algorithmic bytes of one step, without KV
     double step_kv_bytes_ = 0;       // KV bytes per visible key
     StepParams step_;

@@ -601,6 +601,7 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
             step_.x_part_local = nullptr;
             step_.x_q_local = nullptr;
             const bool retry_local = ++step_xcd_misses_ < 4;
+            ++step_reruns_;
             decode_step(id, host_logits, argmax);
             if (retry_local) {
                 step_.x_part_local = static_cast<decltype(step_.x_part_local)>(part_local);
@@ -629,6 +630,7 @@ void Session::decode_step(uint32_t id, float* host_logits, uint32_t* argmax) {
         }
     }
     if (p.x_part_local) step_xcd_misses_ = 0;
+    ++step_tokens_;
     const uint32_t next = *host_argmax_;
     if (argmax) *argmax = next;
     step_token_ = next;

@@ -101,6 +101,8 @@ def library(path: Path | None = None) -> C.CDLL:
         "lh_session_logits_device": ([vp, C.POINTER(vp), C.POINTER(sz)], i32),
         "lh_session_set_profiling": ([vp, i32], i32),
         "lh_session_profile": ([vp, vp, sz, C.POINTER(sz)], i32),
+        "lh_session_status": ([vp, C.POINTER(C.c_int), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                               C.POINTER(C.c_int)], i32),
         "lh_device_alloc": ([sz, C.POINTER(vp)], i32), "lh_device_free": ([vp], i32),
         "lh_copy_to_device": ([vp, vp, sz], i32), "lh_copy_to_host": ([vp, vp, sz], i32),
         "lh_memset_device": ([vp, i32, sz], i32), "lh_synchronize": ([], i32),
@@ -303,6 +305,16 @@ class Decoder:
         check(library().lh_session_profile(self._session, C.cast(entries, C.c_void_p), 16, C.byref(n)))
         return {e.name.decode(): {"launches": e.launches, "ms": e.milliseconds, "bytes": e.bytes,
                                   "ops": e.operations} for e in entries[:n.value]}
+
+    def status(self) -> dict:
+        """The session's numerics and the persistent decode step's record since the
+        session began: tokens it produced, steps re-run on the memory exchange path
+        after an XCD mismatch, and whether the XCD-local exchange is still on."""
+        ref, tokens, reruns, local = C.c_int(), C.c_uint64(), C.c_uint64(), C.c_int()
+        check(library().lh_session_status(self._session, C.byref(ref), C.byref(tokens), C.byref(reruns),
+                                          C.byref(local)))
+        return {"reference_order": bool(ref.value), "step_tokens": tokens.value,
+                "step_memory_reruns": reruns.value, "xcd_local": bool(local.value)}
 
     @property
     def vocabulary_size(self) -> int:

@@ -65,8 +65,9 @@ def ran_every_step(profile, steps):
     return steps <= launches <= steps + 4
 
 
-def greedy_against_oracle(rt, oracle, path, prompt, steps):
-    """Greedy decode on both sides; every step's logits bit-equal, same tokens."""
+def greedy_against_oracle(rt, oracle, path, prompt, steps, status=None):
+    """Greedy decode on both sides; every step's logits bit-equal, same tokens.
+    status, a list, receives the session's status at the end."""
     dec = rt.Decoder(path, 8, numerics="reference", max_context=len(prompt) + steps + 8)
     od = oracle.decoder(path, 8, False)
     a, b = dec.forward(prompt), od.forward(prompt)
@@ -82,6 +83,8 @@ def greedy_against_oracle(rt, oracle, path, prompt, steps):
         assert diff.size == 0, (f"step {step} (position {len(prompt) + step}): {diff.size} logits differ, "
                                 f"first {diff[:3]}, max |diff| {np.max(np.abs(a - b)):.3e}")
     profile = dec.profile()
+    if status is not None:
+        status.append(dec.status())
     dec.close()
     return tokens, profile
 
@@ -125,16 +128,24 @@ def test_reference_step_with_sliding_window(rt, oracle, tmp_path):
 def test_reference_step_xcd_local_and_memory_paths_are_bit_exact(rt, oracle, wide, monkeypatch):
     # Scores travel through one XCD's L2 (LEAF_DECODE_STEP_LOCAL_MERGE) with
     # the q rows (LEAF_DECODE_STEP_LOCAL_Q), or through uncached memory; a
-    # host-forced failed XCD check makes every step fall back.  All give the
-    # oracle's logits.
+    # host-forced failed XCD check makes every step fall back: four steps run
+    # again on the memory path, then the XCD-local exchange stays off, and the
+    # session's status says so.  All give the oracle's logits.
     prompt = np.arange(1, 90, dtype=np.uint32) * 11
     for merge, q, force in (("1", "1", "0"), ("1", "0", "0"), ("0", "0", "0"), ("1", "1", "1")):
         monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_MERGE", merge)
         monkeypatch.setenv("LEAF_DECODE_STEP_LOCAL_Q", q)
         monkeypatch.setenv("LEAF_DECODE_STEP_FORCE_XCD_MISMATCH", force)
         print(f"local merge {merge}, local q {q}, forced mismatch {force}", flush=True)
-        _, profile = greedy_against_oracle(rt, oracle, wide, prompt, 8)
+        status = []
+        _, profile = greedy_against_oracle(rt, oracle, wide, prompt, 8, status)
         assert profile.get("decode_step", {}).get("launches", 0) >= 8
+        st = status[0]
+        assert st["reference_order"] and st["step_tokens"] == 8
+        if force == "1":
+            assert st["step_memory_reruns"] == 4 and not st["xcd_local"]
+        elif merge == "0":
+            assert not st["xcd_local"]
 
 
 def test_reference_step_and_graph_path_agree(rt, small, monkeypatch):
