@@ -1021,7 +1021,7 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     // the first chunks' V rows load while the denominator is formed
 #pragma unroll
     for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
-    const float den = wave_sequential_sum(pe, n, area);
+    const float den = wave_sequential_sum<kSeqSumMaxPerLane, true>(pe, n, area);   // padding rows hold +0
     // p = e / den in key order (pnat), read four keys at a time below
     for (int i0 = 0; i0 < E; i0 += 8) {
         float e[8];
@@ -1052,30 +1052,41 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
             p[j] = *reinterpret_cast<const v4f*>(pnat + min(c * kChainKeys, kRefMaxKeys - kChainKeys) + 4 * j);
     };
     // Keys past a chunk's count add (+0) * v = +-0, which leaves the sum
-    // unchanged (it starts at +0 and is never -0); full chunks skip the select.
+    // unchanged (it starts at +0 and is never -0).
     auto add = [&](const float (&v)[kChainKeys], const v4f (&p)[kChainKeys / 4], int c) {
         const int keys = cached - c * kChainKeys;
-        if (keys >= kChainKeys) {
 #pragma unroll
-            for (int j = 0; j < kChainKeys; ++j) o = o + p[j / 4][j % 4] * v[j];
-        } else {
+        for (int j = 0; j < kChainKeys; ++j) o = o + (j < keys ? p[j / 4][j % 4] : 0.0f) * v[j];
+    };
+    auto add_full = [&](const float (&v)[kChainKeys], const v4f (&p)[kChainKeys / 4]) {
 #pragma unroll
-            for (int j = 0; j < kChainKeys; ++j) o = o + (j < keys ? p[j / 4][j % 4] : 0.0f) * v[j];
-        }
+        for (int j = 0; j < kChainKeys; ++j) o = o + p[j / 4][j % 4] * v[j];
     };
     if (chunks > 0) {
         stage_read(ring[0], 0, vv[0], pp[0]);
         load(ring[0], kChainDepth);
     }
-    for (int c0 = 0; c0 < chunks; c0 += kChainDepth) {
+    // Whole groups of kChainDepth full chunks: one straight-line body per
+    // group, so every staging waits only for the loads issued kChainDepth
+    // chunks earlier; the rest (at most kChainDepth - 1 full chunks and the
+    // partial one) after it.
+    const int groups = (cached / kChainKeys) / kChainDepth;
+    for (int g = 0; g < groups; ++g) {
 #pragma unroll
         for (int u = 0; u < kChainDepth; ++u) {
-            const int c = c0 + u;
-            if (c >= chunks) break;
+            const int c = g * kChainDepth + u;
             stage_read(ring[(u + 1) % kChainDepth], c + 1, vv[(u + 1) & 1], pp[(u + 1) & 1]);
             load(ring[(u + 1) % kChainDepth], c + 1 + kChainDepth);
-            add(vv[u & 1], pp[u & 1], c);
+            add_full(vv[u & 1], pp[u & 1]);
         }
+    }
+    static_assert(kChainDepth % 2 == 0, "the staged pair's parity carries over from the groups");
+#pragma unroll
+    for (int u = 0; u < kChainDepth; ++u) {
+        const int c = groups * kChainDepth + u;
+        if (c >= chunks) break;
+        if (c + 1 < chunks) stage_read(ring[(u + 1) % kChainDepth], c + 1, vv[(u + 1) & 1], pp[(u + 1) & 1]);
+        add(vv[u & 1], pp[u & 1], c);
     }
     lds_done();
     float vnew;

@@ -214,7 +214,7 @@ void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream
 // one lane's plain chain (method 1); cycles[i] (may be null) = the clock
 // cycles the sum took.  False when n or method is out of range.
 constexpr int kSequentialSumMax = 8192;
-inline int seq_per_lane_host(int n) { return (n + 63) / 64; }
+inline int seq_per_lane_host(int n) { return (n + 255) / 256 * 4; }
 bool launch_sequential_sum(const float* x, int n, int count, float* sums, long long* cycles, int method,
                            hipStream_t stream);
 // dot_avx / dot_source_bf16_avx order for FP32, BF16, INT8 and INT4 weights with

@@ -371,8 +371,13 @@ __global__ __launch_bounds__(kWave) void ro_sequential_sum_kernel(const float* x
     const SeqLayout lay(n);
     for (int j = threadIdx.x; j < n; j += kWave) v[lay.at(j)] = row[j];
     __syncthreads();
+    // wave_sequential_sum takes non-negative terms; a row with a negative
+    // one (not a norm's squares or a softmax's exponentials) takes the chain
+    bool negative = false;
+    for (int j = threadIdx.x; j < n; j += kWave) negative |= __float_as_uint(row[j]) > 0x80000000u;
+    const bool parallel = method == 0 && !__any(negative);
     const long long t0 = clock64();
-    const float s = method == 0 ? wave_sequential_sum(v, n, area) : seq_chain(v, n, lay.E);
+    const float s = parallel ? wave_sequential_sum(v, n, area) : seq_chain(v, n, lay.E);
     const long long t1 = clock64();
     if (threadIdx.x == 0) {
         sums[blockIdx.x] = s;

@@ -13,30 +13,37 @@
 // those where the sum enters the next binade (about log2(n) of them), those
 // whose binade is not certain, and ties, which round to the even neighbour.
 //
-// How.  Lane l takes elements [l E, (l + 1) E), E = ceil(n / 64).
+// How.  Lane l takes elements [l E, (l + 1) E), E = 4 ceil(n / 256).
 //   1. An approximate exclusive prefix P of every element (lane totals in
 //      f32, a scan over the lanes, running sums in the lane).
 //   2. The true running sum s_j differs from P_j by less than
 //      (j + 2E + 8) 2^-24 P_j (each of the j earlier steps rounds by at most
-//      2^-24 of the sum so far; P has at most 2E + 8 roundings on its path);
+//      2^-24 of the sum so far; P has at most 2E + 8 roundings on its path;
+//      sums in the subnormal range round not at all);
 //      with d a little wider than that, a step is safe when P_j (1 - d) and
-//      (P_j + a_j) (1 + d) lie in one binade, a_j / g is not a tie and g is
-//      at least 2^-27 of the total (so the increments' f64 prefix sums are
-//      exact).  Safe increments are added in f64 per lane and scanned over the
-//      lanes: I_j, the exact sum of the safe increments before element j.
+//      (P_j + a_j) (1 + d) lie in one binade 2^e, a_j / g is not a tie and g
+//      is at least 2^-27 of the total (so the increments' f64 prefix sums are
+//      exact).  The increment is (2^e + a_j) - 2^e: 2^e has an even
+//      significand, so the addition rounds a_j to the grid with ties to even,
+//      and the subtraction is exact; a tie is |a_j - increment| == g / 2.
+//      Safe increments are added in f64 per lane and scanned over the lanes:
+//      I_j, the exact sum of the safe increments before element j.
 //   3. Every other step (at most kSeqSumCap per lane) is recorded with its
 //      I_j and a_j, compacted in element order, and walked: between two such
 //      steps the sum grows by exactly I_q - I_p (a multiple of that run's g,
 //      so exact in f32 too); at each one, s = fl(s + a) is the real step.
 // Lane 0's chunk, where the binade changes at almost every doubling, is summed
-// one by one instead (its in-order total).  A lane with more than
-// kSeqSumCap unsafe steps, negative, infinite, NaN or subnormal terms, or a
-// total of 2^126 or more, falls back to the plain chain.
+// one by one instead (its in-order total).  A lane with more than kSeqSumCap
+// unsafe steps, or a total that is not below 2^126 (infinite or NaN terms
+// make it so), falls back to the plain chain.  Terms must not be negative;
+// -0 and subnormal terms are fine.
 //
 // The values sit in LDS in the transposed layout of SeqLayout: element j of
 // lane l's chunk at row j - l E, column l, so the lanes' reads of their chunks
 // meet different banks.  Every lane returns the sum.
 #pragma once
+
+#include <type_traits>
 
 #include "device_common.h"
 
@@ -45,13 +52,17 @@ namespace leafhip {
 constexpr int kSeqSumCap = 12;                    // unsafe steps one lane records
 constexpr int kSeqSumArea = kWave * (kSeqSumCap + 1);   // float4 of LDS scratch per wave (one spare per lane)
 
+// Elements per lane: a multiple of four, so that the lanes' chunks load and
+// step in whole groups of four.
+__host__ __device__ constexpr int seq_per_lane(int n) { return (n + 4 * kWave - 1) / (4 * kWave) * 4; }
+
 // Where element j of an n-element vector lives (E = seq_per_lane(n)):
 // (j mod E) * 64 + j / E.  The quotient comes from a float reciprocal and one
 // correction (exact for j < 2^24), not a 32-bit integer division.
 struct SeqLayout {
     int E;
     float inv;
-    __device__ explicit SeqLayout(int n) : E((n + kWave - 1) / kWave), inv(1.0f / (float)E) {}
+    __device__ explicit SeqLayout(int n) : E(seq_per_lane(n)), inv(1.0f / (float)E) {}
     __device__ __forceinline__ int at(int j) const {
         int q = (int)((float)j * inv);
         int r = j - q * E;
@@ -60,7 +71,6 @@ struct SeqLayout {
         return r * kWave + q;
     }
 };
-__device__ __forceinline__ int seq_per_lane(int n) { return (n + kWave - 1) / kWave; }
 
 // Elements [0, m) in order (lane by lane, a lane's chunk top to bottom), 32
 // LDS reads in flight at a time.
@@ -90,7 +100,10 @@ constexpr int kDppRowBcast31 = 0x143;
 constexpr int kDppWaveShr1 = 0x138;      // lane i reads lane i - 1 (lane 0: 0)
 template <int Ctrl, int RowMask = 0xF>
 __device__ __forceinline__ unsigned dpp_move(unsigned v) {
-    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, RowMask, 0xF, false);
+    if constexpr (RowMask == 0xF && Ctrl != kDppWaveShr1)   // row shifts: bound_ctrl reads 0 past the row
+        return (unsigned)__builtin_amdgcn_mov_dpp((int)v, Ctrl, RowMask, 0xF, true);
+    else
+        return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, RowMask, 0xF, false);
 }
 template <int Ctrl, int RowMask = 0xF>
 __device__ __forceinline__ double dpp_move(double v) {
@@ -128,71 +141,91 @@ __device__ __forceinline__ double lane_value(double v, int l) {
 
 // v: n >= 1 non-negative floats in the transposed layout; area: this wave's
 // kSeqSumArea float4 of LDS scratch.  Each lane holds its chunk in registers
-// (up to kSeqSumMaxPerLane values: n <= 2048; longer vectors take the chain).
-// Branch-free: loads and stores are unconditional (clamped indices, a
-// per-lane spare slot for the stores that record nothing), so every LDS
-// access of a phase is in flight at once.
+// (up to kMaxE values, at most kSeqSumMaxPerLane: n <= 2048; longer vectors
+// take the chain).  kZeroTail: the layout's slots past n hold +0 (otherwise
+// they are masked here).  Loads and stores are unconditional within a group
+// of four (a per-lane spare slot takes the stores that record nothing), so
+// every LDS access of a phase is in flight at once.
 constexpr int kSeqSumMaxPerLane = 32;
+template <int kMaxE = kSeqSumMaxPerLane, bool kZeroTail = false>
 __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
+    static_assert(kMaxE % 4 == 0 && kMaxE <= kSeqSumMaxPerLane, "chunks are whole groups of four");
     // A fresh lane index per call: callers inside long loops would otherwise
     // have the lane-dependent constants below hoisted and held in registers.
     int lane = threadIdx.x & (kWave - 1);
     asm volatile("" : "+v"(lane));
     const int E = seq_per_lane(n);
-    if (E > kSeqSumMaxPerLane) return seq_chain(v, n, E);
+    if (E > kMaxE) return seq_chain(v, n, E);
     const int j0 = lane * E;
-    const int valid = min(max(n - j0, 0), E);      // this lane's elements; the rest read as +0
-    const int spare = kWave * kSeqSumCap + lane;
-    // 1. this lane's chunk, its in-order total, and the inputs' check: the
-    // largest bit pattern (negative, infinite or NaN terms reach 0x7f800000)
-    // and the smallest nonzero one (subnormal terms are below 0x00800000)
-    float x[kSeqSumMaxPerLane];
+    // 1. this lane's chunk and its in-order total
+    float x[kMaxE];
 #pragma unroll
-    for (int i = 0; i < kSeqSumMaxPerLane; ++i) x[i] = v[min(i, E - 1) * kWave + lane];
-    float T = 0.0f;
-    unsigned umax = 0u, umin = 0xffffffffu;
+    for (int g = 0; g < kMaxE; g += 4)
+        if (g < E) {   // wave-uniform
 #pragma unroll
-    for (int i = 0; i < kSeqSumMaxPerLane; ++i) {
-        x[i] = i < valid ? x[i] : 0.0f;
-        T = T + x[i];   // padding adds +0, which leaves a sum of non-negative terms unchanged
-        const unsigned u = __float_as_uint(x[i]);
-        umax = max(umax, u);
-        umin = min(umin, u - 1u);   // 0 wraps to the top
+            for (int i = g; i < g + 4; ++i) x[i] = v[i * kWave + lane];
+        }
+    if (!kZeroTail && n < kWave * E) {
+#pragma unroll
+        for (int g = 0; g < kMaxE; g += 4)
+            if (g < E) {
+#pragma unroll
+                for (int i = g; i < g + 4; ++i) x[i] = j0 + i < n ? x[i] : 0.0f;
+            }
     }
+    float T = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kMaxE; g += 4)
+        if (g < E) {
+#pragma unroll
+            for (int i = g; i < g + 4; ++i) T = T + x[i];   // padding adds +0: no change
+        }
     const float incl = wave_inclusive_sum(T);
     const float S = lane_value(incl, kWave - 1);
     float P = dpp_move<kDppWaveShr1>(incl);   // the exclusive prefix (lane 0: 0)
-    if (__any(umax >= 0x7f800000u || umin < 0x007fffffu) || !(S < 0x1p126f)) return seq_chain(v, n, E);
+    if (!(S < 0x1p126f)) return seq_chain(v, n, E);
     if (S == 0.0f) return 0.0f;                     // all terms zero: the chain stays +0
     // the head: lane 0's chunk, whose in-order total is its T
     const float head = lane_value(T, 0);
-    // 2. safe increments, f64 per lane; unsafe steps recorded.  Padding terms
-    // (+0) change nothing: safe, they add 0; recorded, the walk adds 0.
+    // 2. safe increments, f64 per lane; unsafe steps recorded in this lane's
+    // slots [lane (kSeqSumCap + 1), +kSeqSumCap), the last slot a spare that
+    // absorbs the stores of safe steps and of records past the cap.
     const unsigned ebS = __float_as_uint(S) >> 23;
-    const unsigned ebmin = ebS > 51u ? ebS - 27u : 24u;
+    const unsigned thr = (ebS > 51u ? ebS - 27u : 24u) << 23;   // finer grids are unsafe
     const float d = (float)(j0 + 3 * E + 16) * 0x1.1p-24f;
     const float clo = 1.0f - d, chi = 1.0f + d;
-    const bool body = lane >= 1;
+    const int first = lane * (kSeqSumCap + 1);
+    const unsigned spare_at = (unsigned)(first + kSeqSumCap) * sizeof(float4);   // byte offsets into area
+    char* const base = reinterpret_cast<char*>(area);
     double J = 0.0;
-    int cnt = 0;
+    unsigned at = (unsigned)first * sizeof(float4);
 #pragma unroll
-    for (int i = 0; i < kSeqSumMaxPerLane; ++i) {
-        if (i < E) {   // wave-uniform
-            const float a = x[i];
-            const float Pn = P + a;
-            const unsigned blo = __float_as_uint(P * clo), bhi = __float_as_uint(Pn * chi);
-            const unsigned eb = bhi >> 23;
-            const float q = a * __uint_as_float((277u - eb) << 23);   // a / g, exact
-            const float inc = rintf(q) * __uint_as_float((eb - 23u) << 23);   // g rint(a / g)
-            const bool safe = (blo >> 23) == eb && eb - ebmin < 255u - ebmin && q - floorf(q) != 0.5f;
-            const bool rec = body && !safe;
-            const unsigned long long bits = (unsigned long long)__double_as_longlong(J);
-            area[rec && cnt < kSeqSumCap ? lane * kSeqSumCap + cnt : spare] =
-                make_float4(__uint_as_float((unsigned)bits), __uint_as_float((unsigned)(bits >> 32)), a, 0.0f);
-            cnt += rec ? 1 : 0;
-            J += body && safe ? (double)inc : 0.0;
-            P = Pn;
+    for (int g = 0; g < kMaxE; g += 4)
+        if (g < E) {   // wave-uniform
+#pragma unroll
+            for (int i = g; i < g + 4; ++i) {
+                const float a = x[i];
+                const float Pn = P + a;
+                const unsigned lo = __float_as_uint(P * clo), hi = __float_as_uint(Pn * chi);
+                const unsigned mb = hi & 0x7f800000u;
+                const float M = __uint_as_float(mb);
+                const float inc = (M + a) - M;                       // g rint(a / g), ties to even
+                const float h = __uint_as_float(mb - (24u << 23));   // g / 2
+                const bool safe = (lo ^ hi) < 0x00800000u && hi >= thr && fabsf(a - inc) != h;
+                const unsigned long long bits = (unsigned long long)__double_as_longlong(J);
+                *reinterpret_cast<float4*>(base + min(at, spare_at)) =
+                    make_float4(__uint_as_float((unsigned)bits), __uint_as_float((unsigned)(bits >> 32)), a, 0.0f);
+                at += safe ? 0u : (unsigned)sizeof(float4);
+                float add = safe ? inc : 0.0f;
+                asm volatile("" : "+v"(add));   // select in f32, convert once
+                J += (double)add;
+                P = Pn;
+            }
         }
+    int cnt = (int)(at / sizeof(float4)) - first;
+    if (lane == 0) {   // the head took lane 0's chunk
+        cnt = 0;
+        J = 0.0;
     }
     if (__any(cnt > kSeqSumCap)) return seq_chain(v, n, E);
     // 3. scans: the lanes' safe totals (exact in f64) and unsafe counts
@@ -202,21 +235,40 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
     const double Ibase = Jincl - J;                  // exact: every partial sum is
     const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
     const int off = cincl - cnt;
-    // compact the recorded steps in element order, with I = Ibase + J
-    float4 mine[kSeqSumCap];
+    // compact the recorded steps in element order, with I = Ibase + J, into
+    // records [0, K) of `area` (after every lane has read its own: the wave's
+    // LDS accesses complete in order); rounds = the most any lane recorded
+    int kmax = cnt;
+    kmax = max(kmax, dpp_move<kDppRowShr + 1>(kmax));
+    kmax = max(kmax, dpp_move<kDppRowShr + 2>(kmax));
+    kmax = max(kmax, dpp_move<kDppRowShr + 4>(kmax));
+    kmax = max(kmax, dpp_move<kDppRowShr + 8>(kmax));
+    kmax = max(kmax, dpp_move<kDppRowBcast15, 0xA>(kmax));
+    kmax = max(kmax, dpp_move<kDppRowBcast31, 0xC>(kmax));
+    const int rounds = __builtin_amdgcn_readlane(kmax, kWave - 1);
+    auto compact = [&](auto width) {
+        constexpr int kR = decltype(width)::value;
+        float4 mine[kR];
 #pragma unroll
-    for (int k = 0; k < kSeqSumCap; ++k) mine[k] = area[lane * kSeqSumCap + k];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int k = 0; k < kR; ++k) mine[k] = area[first + k];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < kSeqSumCap; ++k) {
-        const unsigned long long jb = (unsigned long long)__float_as_uint(mine[k].x) |
-                                      ((unsigned long long)__float_as_uint(mine[k].y) << 32);
-        const double I = Ibase + __longlong_as_double((long long)jb);
-        const unsigned long long ib = (unsigned long long)__double_as_longlong(I);
-        area[k < cnt ? off + k : spare] =
-            make_float4(__uint_as_float((unsigned)ib), __uint_as_float((unsigned)(ib >> 32)), mine[k].z, 0.0f);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int k = 0; k < kR; ++k) {
+            const unsigned long long jb = (unsigned long long)__float_as_uint(mine[k].x) |
+                                          ((unsigned long long)__float_as_uint(mine[k].y) << 32);
+            const double I = Ibase + __longlong_as_double((long long)jb);
+            const unsigned long long ib = (unsigned long long)__double_as_longlong(I);
+            area[k < cnt ? off + k : kWave * kSeqSumCap + lane] =   // past every record: K <= 63 kSeqSumCap
+                make_float4(__uint_as_float((unsigned)ib), __uint_as_float((unsigned)(ib >> 32)), mine[k].z, 0.0f);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    if (rounds <= 2)
+        compact(std::integral_constant<int, 2>());
+    else if (rounds <= 4)
+        compact(std::integral_constant<int, 4>());
+    else
+        compact(std::integral_constant<int, kSeqSumCap>());
     // 4. the walk, lane i taking recorded step i: the running sum moves one
     // lane up per step (wave_shr:1), lane i adds its exact jump R_i to the
     // step and then the step's term, fl(fl(s + R_i) + a_i).  Lane 0 of a batch
@@ -230,9 +282,14 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
         const double up = dpp_move<kDppWaveShr1>(I);
         float R = (float)(I - (lane == 0 ? prev : up));   // exact jump to this step
         if (lane == 0) R = s + R;                         // exact: the sum just before step b
-        const int m = min(kWave, K - b);
+        const int m = __builtin_amdgcn_readfirstlane(min(kWave, K - b));
+        // after step i lanes 0..i hold their final values, which further
+        // steps recompute unchanged: m rounds up to whole groups of four
         float t = 0.0f;
-        for (int i = 0; i < m; ++i) t = (dpp_move<kDppWaveShr1>(t) + R) + e.z;
+        for (int i = 0; i < m; i += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) t = (dpp_move<kDppWaveShr1>(t) + R) + e.z;
+        }
         s = lane_value(t, m - 1);
         prev = lane_value(I, m - 1);
     }

@@ -9,7 +9,8 @@ one.  Here it must equal numpy's float32 accumulate -- a plain loop, one
 rounding per element -- bit for bit, on the shapes it serves (2048 and 5632
 squares, a few hundred to 4,096 softmax terms) and on inputs built to defeat
 it: ties at every step, powers of two, two scales 2^30 apart, zeros, one
-element, subnormal and infinite terms (which take the plain chain).
+element, subnormal terms (summed like any other), and infinite, NaN or
+negative terms and totals past 2^126 (which take the plain chain).
 """
 from __future__ import annotations
 
@@ -57,9 +58,15 @@ def cases(n, rng):
     yield "two scales", two
     yield "heavy tail", np.abs(g) * np.where(rng.random((count, n)) < 0.01, 1e6, 1).astype(np.float32)
     yield "all zero", np.zeros((count, n), np.float32)
+    yield "softmax tail (subnormal terms)", np.exp(-rng.random((count, n)) * 110).astype(np.float32)
+    yield "subnormal terms", rng.integers(0, 1 << 23, (count, n)).astype(np.uint32).view(np.float32)
+    yield "squares near the subnormal range", (g * np.float32(1e-20)) ** 2
+    zeros_first = (g * scale) ** 2
+    zeros_first[:, : n // 3] = 0
+    yield "leading zeros", zeros_first
 
 
-@pytest.mark.parametrize("n", [1, 7, 33, 64, 600, 640, 2048, 4096, 5632])
+@pytest.mark.parametrize("n", [1, 7, 33, 64, 256, 257, 600, 640, 760, 1000, 2047, 2048, 4096, 5632])
 def test_parallel_column_sum_equals_the_chain(rt, n):
     rng = np.random.default_rng(n)
     for name, x in cases(n, rng):
@@ -69,12 +76,17 @@ def test_parallel_column_sum_equals_the_chain(rt, n):
         assert bad.size == 0, f"{name}, n={n}: {bad.size} of {len(want)} sums differ (row {bad[0]})"
 
 
-def test_unusual_terms_take_the_plain_chain(rt):
-    x = np.abs(np.random.default_rng(1).standard_normal((4, 2048))).astype(np.float32)
-    x[0, 100] = np.float32(1e-40)        # subnormal
+def test_unusual_terms(rt):
+    # a subnormal term and -0 are summed like any other; infinite, NaN and
+    # negative terms and a total past 2^126 take the plain chain
+    x = np.abs(np.random.default_rng(1).standard_normal((7, 2048))).astype(np.float32)
+    x[0, 100] = np.float32(1e-40)
     x[1, 5] = np.inf
     x[2, 7] = np.nan
-    x[3, :] *= np.float32(2.0 ** 110)    # total past 2^126
+    x[3, :] *= np.float32(2.0 ** 110)
+    x[4, 9] = np.float32(-0.0)
+    x[5, 11] = np.float32(-1.5)
+    x[6, :] = np.float32(1e-40)
     got, _ = gpu_sums(rt, x)
     want = column_sums(x)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
