@@ -112,12 +112,16 @@ struct __align__(16) Shared {
 // (scores, then exp(score - max), then the probabilities) in the transposed
 // layout of wave_sequential_sum, and per exchange wave the scratch of that
 // sum, which the p.v chain then uses to stage its V rows.
-constexpr int kRefMaxKeys = 2048;   // visible keys of the reference-order step (kSeqSumMaxPerLane per lane)
+constexpr int kRefMaxKeys = 2048;   // softmax terms one chain wave holds (kSeqSumMaxPerLane per lane)
 static_assert(kRefMaxKeys == kWave * kSeqSumMaxPerLane, "the denominator's terms fit one register chunk per lane");
+// Visible keys of the reference-order step: the p.v chain reads its last
+// group's p (fewer than 64 past the keys) inside the wave's kRefMaxKeys floats.
+constexpr int kRefStepKeys = kRefMaxKeys - kWave;
 static_assert(kA * kRefMaxKeys <= kStepSpanKeys * kStepDim, "s.v holds each chain wave's probabilities in key order");
 struct __align__(16) SharedRef : Shared {
     float pe[kA][kRefMaxKeys];
     float4 area[kA][kSeqSumArea];
+    uint64_t exp2[32];   // expf's table (libm_expf.h), read per lane
     // pe and area, both free then, stage the gated activation while its
     // maximum is traded (quantize_into)
     __device__ float* stage() { return &pe[0][0]; }
@@ -757,10 +761,15 @@ __device__ __forceinline__ float activate(int activation, float x) {
     return x < 0.0f ? 0.0f : x;
 }
 
+// glibc's expf with its table in LDS.
+__device__ __forceinline__ float lds_expf(float x, const uint64_t* table) {
+    return libm_expf_from(x, [table](uint32_t i) { return table[i]; });
+}
+
 // Decoder::Impl::activate in reference order: SiLU with glibc's expf, ReLU
 // as std::max(x, 0.0f).  (The step runs reference order only for these two.)
-__device__ __forceinline__ float ref_activate(int activation, float x) {
-    if (activation == 0) return x / (1.0f + libm_expf(-x));
+__device__ __forceinline__ float ref_activate(int activation, float x, const uint64_t* exp2) {
+    if (activation == 0) return x / (1.0f + lds_expf(-x, exp2));
     return x < 0.0f ? 0.0f : x;
 }
 
@@ -967,21 +976,19 @@ __device__ __forceinline__ void ref_score_item(const StepParams& P, Shared& s, i
 // (pe, in wave_sequential_sum's layout) -> the maximum (NaN scores never
 // become it, as with std::max) -> exp(s - max) with glibc's expf -> the
 // denominator summed in key order (wave_sequential_sum) -> p = e / denominator
-// -> output[d] += p * v[d] in key order, lane d.  V rows of the cached keys
-// come from the cache (this XCD's items loaded them a moment ago) as 16-byte
-// loads, kChainDepth chunks of kChainKeys keys in flight, each chunk staged
-// in `stage` (row-major) so that lane d reads its column; the new key's row
-// comes from the exchange words of q|k|v.  A fully masked or infinite row
-// leaves the zero output, like the CPU.  Returns false (abort raised) when a
-// wait failed; o is this lane's output element.
-constexpr int kChainKeys = 16;                                      // keys per V chunk
-constexpr int kChainDepth = 4;                                      // chunks in flight
-constexpr int kChainF4 = kChainKeys * kStepDim / 4 / kWave;         // float4 per lane per chunk
-static_assert(kChainKeys * kStepDim <= 4 * kSeqSumArea, "a V chunk fits the wave's staging area");
-__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float* pnat, float4* area, int n, float m,
-                                          const float* V, const u64* vnew_word, unsigned vnew_epoch, int lane,
-                                          float& o) {
+// -> output[d] += p * v[d] in key order, lane d.  Lane d loads column d of
+// the cached V rows itself (one coalesced 256-byte row per load), kChainDepth
+// chunks of kChainKeys keys in flight; the new key's row comes from the
+// exchange words of q|k|v.  A fully masked or infinite row leaves the zero
+// output, like the CPU.  Returns false (abort raised) when a wait failed; o is
+// this lane's output element.
+constexpr int kChainKeys = 12;                                      // keys per chunk: three float4 of p
+constexpr int kChainDepth = 4;                                      // chunks in flight (48 loads)
+__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float* pnat, float4* area,
+                                          const uint64_t* exp2, int n, float m, const float* V,
+                                          const u64* vnew_word, unsigned vnew_epoch, int lane, float& o) {
     constexpr int dim = kStepDim;
+    constexpr int kRowBytes = dim * (int)sizeof(float);
     o = 0.0f;
     const float maximum = dpp_max_f32(m);
     if (!isfinite(maximum)) return true;
@@ -989,19 +996,17 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     const int valid = min(max(n - lane * E, 0), E);
     const int cached = n - 1;   // the new key is the last visible one
     const int chunks = (cached + kChainKeys - 1) / kChainKeys;
+    const int groups = (chunks + kChainDepth - 1) / kChainDepth;
     // V rows through a bounds-checked buffer view of the cached rows: rows
-    // past them read as 0, so the loads need no clamping.  Lane l's float4 i
-    // of a chunk: key 4 i + l / 16, columns 4 (l % 16) ..
+    // past them read as 0, so the loads need no clamping.
     const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(V), (short)0, cached * dim * (int)sizeof(float), kRawBufferWord3);
-    const int voff = (lane >> 4) * dim * (int)sizeof(float) + (lane & 15) * 16;
-    constexpr int kChunkBytes = kChainKeys * kStepDim * (int)sizeof(float);
-    v4u ring[kChainDepth][kChainF4];
-    auto load = [&](v4u (&r)[kChainF4], int c) {
-        const int at = voff + c * kChunkBytes;
+        const_cast<float*>(V), (short)0, cached * kRowBytes, kRawBufferWord3);
+    float ring[kChainDepth][kChainKeys];
+    auto load = [&](float (&r)[kChainKeys], int c) {
+        const int at = lane * (int)sizeof(float) + c * kChainKeys * kRowBytes;
 #pragma unroll
-        for (int i = 0; i < kChainF4; ++i)
-            r[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, at + i * 4 * dim * (int)sizeof(float), 0, 0);
+        for (int j = 0; j < kChainKeys; ++j)
+            r[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vbuf, at + j * kRowBytes, 0, 0));
     };
     lds_done();
     // exp(s - max) of this lane's keys (lane * E + i, at row i of column lane),
@@ -1012,81 +1017,52 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = pe[min(i0 + i, E - 1) * kWave + lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = i0 + i < valid ? libm_expf(e[i] - maximum) : 0.0f;
+        for (int i = 0; i < 4; ++i) e[i] = i0 + i < valid ? lds_expf(e[i] - maximum, exp2) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             if (i0 + i < E) pe[(i0 + i) * kWave + lane] = e[i];
     }
     lds_done();
-    // the first chunks' V rows load while the denominator is formed
+    // the first chunks' V columns load while the denominator is formed
 #pragma unroll
     for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
     const float den = wave_sequential_sum<kSeqSumMaxPerLane, true>(pe, n, area);   // padding rows hold +0
-    // p = e / den in key order (pnat), read four keys at a time below
-    for (int i0 = 0; i0 < E; i0 += 8) {
-        float e[8];
+    // p = e / den in key order (pnat), read four keys at a time below; the
+    // padding rows (e = +0) give p = +0 for keys [n, 64 E), and the keys the
+    // last group runs past that (fewer than kChainDepth * kChainKeys) +0 too
+    for (int i0 = 0; i0 < E; i0 += 4) {
+        float e[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = pe[min(i0 + i, E - 1) * kWave + lane];
+        for (int i = 0; i < 4; ++i) e[i] = pe[(i0 + i) * kWave + lane];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (i0 + i < valid) pnat[lane * E + i0 + i] = e[i] / den;
+        for (int i = 0; i < 4; ++i) pnat[lane * E + i0 + i] = e[i] / den;
     }
+    if (kWave * E + lane < kRefMaxKeys) pnat[kWave * E + lane] = 0.0f;
     lds_done();
-    float* stage = reinterpret_cast<float*>(area);
-    // Software-pipelined: chunk c + 1 is staged (the wave's LDS accesses
-    // complete in order, so one staging buffer serves every chunk) and read
-    // into registers while chunk c is added; its loads are replaced by those
-    // of chunk c + 1 + kChainDepth right after staging, unconditionally, so
-    // the wait before staging a chunk counts exactly the loads issued after it.
-    float vv[2][kChainKeys];
+    // Whole groups of kChainDepth chunks, one straight-line body per group:
+    // a chunk's loads are replaced by those kChainDepth chunks on as soon as
+    // it is added, and its p come from LDS one chunk ahead.  Keys from the
+    // new one on add p * (+0) with p finite: their rows lie past the buffer
+    // view's cached rows and read as 0, which leaves the sum unchanged (it
+    // starts at +0 and is never -0).
+    static_assert(kChainDepth % 2 == 0 && kChainKeys % 4 == 0, "p pairs alternate; p loads are float4");
+    static_assert(kChainDepth * kChainKeys <= kWave, "the zeroed p past 64 E cover the last group");
     v4f pp[2][kChainKeys / 4];
-    auto stage_read = [&](const v4u (&r)[kChainF4], int c, float (&v)[kChainKeys], v4f (&p)[kChainKeys / 4]) {
+    auto read_p = [&](v4f (&p)[kChainKeys / 4], int c) {
+        const float* at = pnat + c * kChainKeys;   // < kRefMaxKeys: n <= kRefStepKeys
 #pragma unroll
-        for (int i = 0; i < kChainF4; ++i)
-            *reinterpret_cast<v4u*>(stage + (4 * i + (lane >> 4)) * dim + 4 * (lane & 15)) = r[i];
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < kChainKeys; ++j) v[j] = stage[j * dim + lane];
-#pragma unroll
-        for (int j = 0; j < kChainKeys / 4; ++j)
-            p[j] = *reinterpret_cast<const v4f*>(pnat + min(c * kChainKeys, kRefMaxKeys - kChainKeys) + 4 * j);
+        for (int j = 0; j < kChainKeys / 4; ++j) p[j] = *reinterpret_cast<const v4f*>(at + 4 * j);
     };
-    // Keys past a chunk's count add (+0) * v = +-0, which leaves the sum
-    // unchanged (it starts at +0 and is never -0).
-    auto add = [&](const float (&v)[kChainKeys], const v4f (&p)[kChainKeys / 4], int c) {
-        const int keys = cached - c * kChainKeys;
-#pragma unroll
-        for (int j = 0; j < kChainKeys; ++j) o = o + (j < keys ? p[j / 4][j % 4] : 0.0f) * v[j];
-    };
-    auto add_full = [&](const float (&v)[kChainKeys], const v4f (&p)[kChainKeys / 4]) {
-#pragma unroll
-        for (int j = 0; j < kChainKeys; ++j) o = o + p[j / 4][j % 4] * v[j];
-    };
-    if (chunks > 0) {
-        stage_read(ring[0], 0, vv[0], pp[0]);
-        load(ring[0], kChainDepth);
-    }
-    // Whole groups of kChainDepth full chunks: one straight-line body per
-    // group, so every staging waits only for the loads issued kChainDepth
-    // chunks earlier; the rest (at most kChainDepth - 1 full chunks and the
-    // partial one) after it.
-    const int groups = (cached / kChainKeys) / kChainDepth;
+    read_p(pp[0], 0);
     for (int g = 0; g < groups; ++g) {
 #pragma unroll
         for (int u = 0; u < kChainDepth; ++u) {
             const int c = g * kChainDepth + u;
-            stage_read(ring[(u + 1) % kChainDepth], c + 1, vv[(u + 1) & 1], pp[(u + 1) & 1]);
-            load(ring[(u + 1) % kChainDepth], c + 1 + kChainDepth);
-            add_full(vv[u & 1], pp[u & 1]);
-        }
-    }
-    static_assert(kChainDepth % 2 == 0, "the staged pair's parity carries over from the groups");
+            read_p(pp[(u + 1) & 1], c + 1);
 #pragma unroll
-    for (int u = 0; u < kChainDepth; ++u) {
-        const int c = groups * kChainDepth + u;
-        if (c >= chunks) break;
-        if (c + 1 < chunks) stage_read(ring[(u + 1) % kChainDepth], c + 1, vv[(u + 1) & 1], pp[(u + 1) & 1]);
-        add(vv[u & 1], pp[u & 1], c);
+            for (int j = 0; j < kChainKeys; ++j) o = o + pp[u & 1][j / 4][j % 4] * ring[u][j];
+            load(ring[u], c + kChainDepth);
+        }
     }
     lds_done();
     float vnew;
@@ -1408,7 +1384,8 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
                 }
                 float o = 0.0f;
                 if (ok)
-                    ok = ref_chain(P, pe, s.v + aw * kRefMaxKeys, static_cast<SharedRef&>(s).area[aw], n, m,
+                    ok = ref_chain(P, pe, s.v + aw * kRefMaxKeys, static_cast<SharedRef&>(s).area[aw],
+                                   static_cast<SharedRef&>(s).exp2, n, m,
                                    Vc + ((size_t)g * P.capacity + begin) * dim,
                                    P.x_qkv + qw + kvw + g * dim + lane, epoch(L, 1), lane, o);
                 if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), o);
@@ -1744,9 +1721,14 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
             const float mine = dequant(total, sx, w.gs.scale, w.gs.bias);
             const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
                                                                              __float_as_uint(mine), false, false)[1]);
-            if (lane < 32 && (lane & 7) == 0 && g_live)
-                publish(P.x_act + g_pair, epoch(L, 5), up * (REF ? ref_activate(P.activation, mine)
-                                                                  : activate(P.activation, mine)));
+            if (lane < 32 && (lane & 7) == 0 && g_live) {
+                float act;
+                if constexpr (REF)
+                    act = ref_activate(P.activation, mine, static_cast<SharedRef&>(s).exp2);
+                else
+                    act = activate(P.activation, mine);
+                publish(P.x_act + g_pair, epoch(L, 5), up * act);
+            }
         }
         note_published(s);
         stamp(P.trace, b, 64 * L + 13 + 8 * bw, kAT + kWave * bw);
@@ -1794,6 +1776,8 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         s.abort = 0;
         s.pair[0][0] = s.pair[0][1] = s.pair[1][0] = s.pair[1][1] = 0;
     }
+    if constexpr (REF)
+        if (t < 32) s.exp2[t] = kExp2Table32[t];
     {
         const int words = P.layers * (int)(sizeof(StepLayer) / 16);
         const v4u* src = reinterpret_cast<const v4u*>(P.layer);
@@ -1987,7 +1971,7 @@ bool decode_step_fits(int hidden, int ffn, int heads, int kv_heads, int dim, int
            (ffn + blocks - 1) / blocks <= kGP * kB;
 }
 
-int decode_step_reference_keys() { return kRefMaxKeys; }
+int decode_step_reference_keys() { return kRefStepKeys; }
 
 bool decode_step_fits_reference(int hidden, int activation) {
     // the head's dot_avx chains cover the row in whole 32-column blocks;

@@ -53,7 +53,11 @@ static const uint64_t kExp2Table32[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-LEAF_HOST_DEVICE inline float libm_expf(float x) {
+// table(i) returns kExp2Table32[i]: kernels that call expf often pass a copy
+// in LDS, since the per-lane index makes every read of the constant table a
+// memory round trip.
+template <typename Table>
+LEAF_HOST_DEVICE inline float libm_expf_from(float x, const Table& table) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
     if (abstop >= 0x42b) {                              // |x| >= 88 or x is NaN
@@ -72,7 +76,7 @@ LEAF_HOST_DEVICE inline float libm_expf(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd); // z - k
-    uint64_t t = kExp2Table32[ki % 32];
+    uint64_t t = table((uint32_t)(ki % 32));
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double p = __builtin_fma(c0, r, c1);
@@ -81,6 +85,10 @@ LEAF_HOST_DEVICE inline float libm_expf(float x) {
     y = __builtin_fma(p, r2, y);
     y = y * s;
     return (float)y;
+}
+
+LEAF_HOST_DEVICE inline float libm_expf(float x) {
+    return libm_expf_from(x, [](uint32_t i) { return kExp2Table32[i]; });
 }
 
 }  // namespace leafhip
