@@ -1059,6 +1059,14 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
         for (int u = 0; u < kChainDepth; ++u) {
             const int c = g * kChainDepth + u;
             read_p(pp[(u + 1) & 1], c + 1);
+            // one wait for the whole chunk: every product below reads the
+            // values through this statement, which needs all of them loaded
+            static_assert(kChainKeys == 12, "the statement names twelve values");
+            float (&r)[kChainKeys] = ring[u];
+            v4f (&q)[kChainKeys / 4] = pp[u & 1];
+            asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
+                              "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(q[0]), "+v"(q[1]),
+                              "+v"(q[2]));
 #pragma unroll
             for (int j = 0; j < kChainKeys; ++j) o = o + pp[u & 1][j / 4][j % 4] * ring[u][j];
             load(ring[u], c + kChainDepth);
