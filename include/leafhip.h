@@ -210,10 +210,11 @@ lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream);
 /* sums[i] = (...((0 + x[i][0]) + x[i][1]) + ...) + x[i][n - 1] in float, the
  * order in which norm() sums its squares and attention_impl its softmax
  * denominator (decoder.cpp:716-718, transformer.cpp:127-130), for count rows
- * of n <= 8192 values; values must be >= 0 for method 0, which forms that sum
- * in parallel (the reference-order decode step's way; bit-identical), while
- * method 1 adds one by one.  cycles (may be NULL): the GPU clock cycles each
- * row's sum took.  No reference counterpart: a diagnostic of this build. */
+ * of n <= 8192 values.  Method 0 forms that sum in parallel on one wave and
+ * method 2 on two waves (the reference-order decode step's ways;
+ * bit-identical); method 1 adds one by one.  Rows with a negative value take
+ * method 1.  cycles (may be NULL): the GPU clock cycles each row's sum took.
+ * No reference counterpart: a diagnostic of this build. */
 lh_status lh_sequential_sum(const float* x, size_t n, size_t count, float* sums, int64_t* cycles,
                             uint32_t method, lh_stream stream);
 

@@ -565,7 +565,7 @@ lh_status lh_sequential_sum(const float* x, size_t n, size_t count, float* sums,
                             lh_stream stream) {
     return guarded([&] {
         require_arg(x && sums && n >= 1 && n <= size_t(leafhip::kSequentialSumMax) && count >= 1 &&
-                        count <= 0x7fffffff && method <= 1,
+                        count <= 0x7fffffff && method <= 2,
                     "invalid sequential sum call");
         leafhip::launch_sequential_sum(x, int(n), int(count), sums, reinterpret_cast<long long*>(cycles),
                                        int(method), as_stream(stream));

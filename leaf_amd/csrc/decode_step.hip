@@ -125,7 +125,11 @@ struct __align__(16) SharedRef : Shared {
     // pe and area, both free then, stage the gated activation while its
     // maximum is traded (quantize_into)
     __device__ float* stage() { return &pe[0][0]; }
+    // the RMSNorm's pair sum: the waves' trade and compaction space in pe
+    __device__ float4* seq_xchg() { return reinterpret_cast<float4*>(&pe[0][0]); }
+    __device__ float4* seq_comp(int w) { return seq_xchg() + kSeqPairXchg + w * kSeqPairComp; }
 };
+static_assert(kA == 2 && (kSeqPairXchg + kA * kSeqPairComp) * 4 <= kA * kRefMaxKeys, "pe holds the pair sum's space");
 static_assert(sizeof(float) * kA * kRefMaxKeys + sizeof(float4) * kA * kSeqSumArea >= sizeof(float) * kNF * kAT,
               "pe and area hold an ffn-wide vector's runs");
 static_assert(sizeof(SharedRef) <= 160 * 1024, "one block per CU holds the reference-order LDS");
@@ -493,9 +497,10 @@ __device__ __forceinline__ void post(Shared& s, int phase) {
 // RMSNorm of the n values held as runs (decoder.cpp:706-727).  In reference
 // order the squares are summed in column order, as norm() sums them: every
 // lane stores its runs' squares (s.xf is free until the head) in the layout
-// of wave_sequential_sum, and each exchange wave forms the column-order sum
-// itself (no second trade); the normalized value is (x - 0) * scale * gamma
-// + 0, norm()'s expression with mean 0 and no beta.
+// of wave_sequential_sum, and the two exchange waves form the column-order
+// sum together (wave_pair_sequential_sum: each steps half of every chunk, one
+// trade between them); the normalized value is (x - 0) * scale * gamma + 0,
+// norm()'s expression with mean 0 and no beta.
 template <bool REF, int N>
 __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
                                               Shared& s, int& round) {
@@ -511,8 +516,14 @@ __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float 
                 s.xf[lay.at(e)] = x0 * x0;
                 s.xf[lay.at(e + 1)] = x1 * x1;
             }
+        seq_zero_tail(s.xf, n, a, kAT);
         if (!a_sync(s, round)) return false;   // both waves' squares are in place
-        sq = wave_sequential_sum(s.xf, n, static_cast<SharedRef&>(s).area[a >> 6]);
+        // each exchange wave steps half of every lane's chunk
+        SharedRef& r = static_cast<SharedRef&>(s);
+        const int w = __builtin_amdgcn_readfirstlane(a >> 6);
+        if (!wave_pair_sequential_sum(s.xf, n, r.area[0], r.area[1], r.seq_xchg(), r.seq_comp(w), w,
+                                      [&] { return a_sync(s, round); }, sq))
+            return false;
         const float scale = 1.0f / sqrtf(sq / (float)n + eps);
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = (x[i] - 0.0f) * scale * gamma[i] + 0.0f;
@@ -1026,7 +1037,7 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     // the first chunks' V columns load while the denominator is formed
 #pragma unroll
     for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
-    const float den = wave_sequential_sum<kSeqSumMaxPerLane, true>(pe, n, area);   // padding rows hold +0
+    const float den = wave_sequential_sum(pe, n, area);   // the padding rows hold +0
     // p = e / den in key order (pnat), read four keys at a time below; the
     // padding rows (e = +0) give p = +0 for keys [n, 64 E), and the keys the
     // last group runs past that (fewer than kChainDepth * kChainKeys) +0 too

@@ -359,28 +359,44 @@ __global__ void ro_activation_kernel(const float* gate_up, int tokens, int width
     }
 }
 
-// One wave per vector: the vector staged in LDS in wave_sequential_sum's
-// layout, then its column-order sum by that function (method 0) or by the
-// plain chain (method 1), with the clock cycles the sum took.
-__global__ __launch_bounds__(kWave) void ro_sequential_sum_kernel(const float* x, int n, float* sums,
-                                                                  long long* cycles, int method) {
+// One block per vector: the vector staged in LDS in wave_sequential_sum's
+// layout, then its column-order sum by that function (method 0, one wave),
+// by the plain chain (method 1) or by wave_pair_sequential_sum (method 2, two
+// waves), with the clock cycles the sum took.
+__global__ __launch_bounds__(2 * kWave) void ro_sequential_sum_kernel(const float* x, int n, float* sums,
+                                                                      long long* cycles, int method) {
     extern __shared__ float lds[];
-    float4* area = reinterpret_cast<float4*>(lds);
-    float* v = lds + 4 * kSeqSumArea;
+    float4* area0 = reinterpret_cast<float4*>(lds);
+    float4* area1 = area0 + kSeqSumArea;
+    float4* xchg = area1 + kSeqSumArea;
+    float4* comp = xchg + kSeqPairXchg;
+    float* v = reinterpret_cast<float*>(comp + 2 * kSeqPairComp);
     const float* row = x + (size_t)blockIdx.x * n;
     const SeqLayout lay(n);
-    for (int j = threadIdx.x; j < n; j += kWave) v[lay.at(j)] = row[j];
-    __syncthreads();
-    // wave_sequential_sum takes non-negative terms; a row with a negative
-    // one (not a norm's squares or a softmax's exponentials) takes the chain
+    const int w = threadIdx.x / kWave;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) v[lay.at(j)] = row[j];
+    seq_zero_tail(v, n, threadIdx.x, blockDim.x);
+    // the sums take non-negative terms; a row with a negative one (not a
+    // norm's squares or a softmax's exponentials) takes the chain
     bool negative = false;
-    for (int j = threadIdx.x; j < n; j += kWave) negative |= __float_as_uint(row[j]) > 0x80000000u;
-    const bool parallel = method == 0 && !__any(negative);
+    for (int j = threadIdx.x; j < n; j += blockDim.x) negative |= __float_as_uint(row[j]) > 0x80000000u;
+    const bool parallel = method != 1 && !__syncthreads_or(negative);
     const long long t0 = clock64();
-    const float s = parallel ? wave_sequential_sum(v, n, area) : seq_chain(v, n, lay.E);
+    float s;
+    if (!parallel)
+        s = seq_chain(v, n, lay.E);
+    else if (method == 0)
+        s = wave_sequential_sum(v, n, area0);
+    else
+        wave_pair_sequential_sum(v, n, area0, area1, xchg, comp + w * kSeqPairComp, w,
+                                 [] { __syncthreads(); return true; }, s);
     const long long t1 = clock64();
+    // method 2: both waves formed the sum; they must agree bit for bit
+    __shared__ unsigned second;
+    if (threadIdx.x == kWave) second = __float_as_uint(s);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        sums[blockIdx.x] = s;
+        sums[blockIdx.x] = method == 2 && second != __float_as_uint(s) ? __uint_as_float(0x7fc0deadu) : s;
         if (cycles) cycles[blockIdx.x] = t1 - t0;
     }
 }
@@ -587,9 +603,10 @@ void launch_activation_reference_order(const float* gate_up, int tokens, int wid
 
 bool launch_sequential_sum(const float* x, int n, int count, float* sums, long long* cycles, int method,
                            hipStream_t stream) {
-    if (n < 1 || n > kSequentialSumMax || count < 1 || (method != 0 && method != 1)) return false;
-    const size_t lds = (size_t)kSeqSumArea * sizeof(float4) + (size_t)seq_per_lane_host(n) * kWave * sizeof(float);
-    ro_sequential_sum_kernel<<<count, kWave, lds, stream>>>(x, n, sums, cycles, method);
+    if (n < 1 || n > kSequentialSumMax || count < 1 || method < 0 || method > 2) return false;
+    const size_t lds = (size_t)(2 * kSeqSumArea + kSeqPairXchg + 2 * kSeqPairComp) * sizeof(float4) +
+                       (size_t)seq_per_lane_host(n) * kWave * sizeof(float);
+    ro_sequential_sum_kernel<<<count, method == 2 ? 2 * kWave : kWave, lds, stream>>>(x, n, sums, cycles, method);
     return true;
 }
 

@@ -72,6 +72,13 @@ struct SeqLayout {
     }
 };
 
+// The layout's slots past the n values ([n, 64 E)) set to +0, as the sums
+// below require; `first`, `stride`: this thread's share of them.
+__device__ __forceinline__ void seq_zero_tail(float* v, int n, int first, int stride) {
+    const SeqLayout lay(n);
+    for (int e = n + first; e < kWave * lay.E; e += stride) v[lay.at(e)] = 0.0f;
+}
+
 // Elements [0, m) in order (lane by lane, a lane's chunk top to bottom), 32
 // LDS reads in flight at a time.
 __device__ __forceinline__ float seq_chain(const float* v, int m, int E) {
@@ -139,146 +146,136 @@ __device__ __forceinline__ double lane_value(double v, int l) {
     return __longlong_as_double((long long)((unsigned long long)lo | ((unsigned long long)hi << 32)));
 }
 
-// v: n >= 1 non-negative floats in the transposed layout; area: this wave's
-// kSeqSumArea float4 of LDS scratch.  Each lane holds its chunk in registers
-// (up to kMaxE values, at most kSeqSumMaxPerLane: n <= 2048; longer vectors
-// take the chain).  kZeroTail: the layout's slots past n hold +0 (otherwise
-// they are masked here).  Loads and stores are unconditional within a group
-// of four (a per-lane spare slot takes the stores that record nothing), so
-// every LDS access of a phase is in flight at once.
-constexpr int kSeqSumMaxPerLane = 32;
-template <int kMaxE = kSeqSumMaxPerLane, bool kZeroTail = false>
-__device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
-    static_assert(kMaxE % 4 == 0 && kMaxE <= kSeqSumMaxPerLane, "chunks are whole groups of four");
-    // A fresh lane index per call: callers inside long loops would otherwise
-    // have the lane-dependent constants below hoisted and held in registers.
-    int lane = threadIdx.x & (kWave - 1);
-    asm volatile("" : "+v"(lane));
-    const int E = seq_per_lane(n);
-    if (E > kMaxE) return seq_chain(v, n, E);
-    const int j0 = lane * E;
-    // 1. this lane's chunk and its in-order total
-    float x[kMaxE];
+// Building blocks of the column-order sum (below).  The passes over a lane's
+// chunk are loops over groups of four elements read from LDS (the next
+// group's loads go out before the current group's work): one group's code
+// instead of a fully unrolled chunk keeps the decode step's instruction
+// working set inside the instruction cache.
+
+// Elements g .. g + 3 of this lane's chunk.
+__device__ __forceinline__ void seq_group(const float* v, int g, int lane, float (&a)[4]) {
 #pragma unroll
-    for (int g = 0; g < kMaxE; g += 4)
-        if (g < E) {   // wave-uniform
+    for (int i = 0; i < 4; ++i) a[i] = v[(g + i) * kWave + lane];
+}
+
+// The in-order sum of this lane's elements [i0, i1) added to t (i0, i1
+// multiples of 4; slots past n hold +0 and add nothing).
+__device__ __forceinline__ float seq_total(const float* v, int lane, int i0, int i1, float t) {
+    if (i0 >= i1) return t;
+    float cur[4], nxt[4];
+    seq_group(v, i0, lane, cur);
+    for (int g = i0; g < i1; g += 4) {
+        seq_group(v, min(g + 4, i1 - 4), lane, nxt);   // the last round reloads its own group
 #pragma unroll
-            for (int i = g; i < g + 4; ++i) x[i] = v[i * kWave + lane];
-        }
-    if (!kZeroTail && n < kWave * E) {
+        for (int i = 0; i < 4; ++i) t = t + cur[i];
 #pragma unroll
-        for (int g = 0; g < kMaxE; g += 4)
-            if (g < E) {
-#pragma unroll
-                for (int i = g; i < g + 4; ++i) x[i] = j0 + i < n ? x[i] : 0.0f;
-            }
+        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
     }
-    float T = 0.0f;
-#pragma unroll
-    for (int g = 0; g < kMaxE; g += 4)
-        if (g < E) {
-#pragma unroll
-            for (int i = g; i < g + 4; ++i) T = T + x[i];   // padding adds +0: no change
-        }
-    const float incl = wave_inclusive_sum(T);
-    const float S = lane_value(incl, kWave - 1);
-    float P = dpp_move<kDppWaveShr1>(incl);   // the exclusive prefix (lane 0: 0)
-    if (!(S < 0x1p126f)) return seq_chain(v, n, E);
-    if (S == 0.0f) return 0.0f;                     // all terms zero: the chain stays +0
-    // the head: lane 0's chunk, whose in-order total is its T
-    const float head = lane_value(T, 0);
-    // 2. safe increments, f64 per lane; unsafe steps recorded in this lane's
-    // slots [lane (kSeqSumCap + 1), +kSeqSumCap), the last slot a spare that
-    // absorbs the stores of safe steps and of records past the cap.
-    const unsigned ebS = __float_as_uint(S) >> 23;
-    const unsigned thr = (ebS > 51u ? ebS - 27u : 24u) << 23;   // finer grids are unsafe
-    const float d = (float)(j0 + 3 * E + 16) * 0x1.1p-24f;
-    const float clo = 1.0f - d, chi = 1.0f + d;
-    const int first = lane * (kSeqSumCap + 1);
-    const unsigned spare_at = (unsigned)(first + kSeqSumCap) * sizeof(float4);   // byte offsets into area
+    return t;
+}
+
+// What the steps of one lane's elements [i0, i1) need to know: the margins of
+// the binade test for this lane and the finest grid that is safe.
+struct SeqBounds {
+    float clo, chi;
+    unsigned thr;
+    __device__ SeqBounds(float S, int j0, int E) {
+        const unsigned ebS = __float_as_uint(S) >> 23;
+        thr = (ebS > 51u ? ebS - 27u : 24u) << 23;   // finer grids are unsafe
+        const float d = (float)(j0 + 3 * E + 16) * 0x1.1p-24f;
+        clo = 1.0f - d;
+        chi = 1.0f + d;
+    }
+};
+
+// Steps over this lane's elements [i0, i1) from the approximate prefix P:
+// safe increments into J (f64), unsafe steps recorded (J before the step, the
+// term) in the lane's slots [first, first + kSeqSumCap) of area, the slot
+// after them a spare that absorbs the stores of safe steps and of records
+// past the cap.  Returns the number of records (more than kSeqSumCap: too
+// many).
+__device__ __forceinline__ int seq_steps(const float* v, int lane, int i0, int i1, float P, const SeqBounds& b,
+                                         float4* area, int first, double& J) {
     char* const base = reinterpret_cast<char*>(area);
-    double J = 0.0;
+    const unsigned spare_at = (unsigned)(first + kSeqSumCap) * sizeof(float4);   // byte offsets into area
     unsigned at = (unsigned)first * sizeof(float4);
+    J = 0.0;
+    if (i0 < i1) {
+        float cur[4], nxt[4];
+        seq_group(v, i0, lane, cur);
+        for (int g = i0; g < i1; g += 4) {
+            seq_group(v, min(g + 4, i1 - 4), lane, nxt);
 #pragma unroll
-    for (int g = 0; g < kMaxE; g += 4)
-        if (g < E) {   // wave-uniform
-#pragma unroll
-            for (int i = g; i < g + 4; ++i) {
-                const float a = x[i];
+            for (int i = 0; i < 4; ++i) {
+                const float a = cur[i];
                 const float Pn = P + a;
-                const unsigned lo = __float_as_uint(P * clo), hi = __float_as_uint(Pn * chi);
+                const unsigned lo = __float_as_uint(P * b.clo), hi = __float_as_uint(Pn * b.chi);
                 const unsigned mb = hi & 0x7f800000u;
                 const float M = __uint_as_float(mb);
                 const float inc = (M + a) - M;                       // g rint(a / g), ties to even
                 const float h = __uint_as_float(mb - (24u << 23));   // g / 2
-                const bool safe = (lo ^ hi) < 0x00800000u && hi >= thr && fabsf(a - inc) != h;
-                const unsigned long long bits = (unsigned long long)__double_as_longlong(J);
-                *reinterpret_cast<float4*>(base + min(at, spare_at)) =
-                    make_float4(__uint_as_float((unsigned)bits), __uint_as_float((unsigned)(bits >> 32)), a, 0.0f);
+                const bool safe = (lo ^ hi) < 0x00800000u && hi >= b.thr && fabsf(a - inc) != h;
+                char* const rec = base + min(at, spare_at);
+                *reinterpret_cast<double*>(rec) = J;
+                *reinterpret_cast<float*>(rec + 8) = a;
                 at += safe ? 0u : (unsigned)sizeof(float4);
                 float add = safe ? inc : 0.0f;
                 asm volatile("" : "+v"(add));   // select in f32, convert once
                 J += (double)add;
                 P = Pn;
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
         }
-    int cnt = (int)(at / sizeof(float4)) - first;
-    if (lane == 0) {   // the head took lane 0's chunk
-        cnt = 0;
-        J = 0.0;
     }
-    if (__any(cnt > kSeqSumCap)) return seq_chain(v, n, E);
-    // 3. scans: the lanes' safe totals (exact in f64) and unsafe counts
-    const double Jincl = wave_inclusive_sum(J);
-    const int cincl = wave_inclusive_sum(cnt);
-    const double Itot = lane_value(Jincl, kWave - 1);
-    const double Ibase = Jincl - J;                  // exact: every partial sum is
-    const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
-    const int off = cincl - cnt;
-    // compact the recorded steps in element order, with I = Ibase + J, into
-    // records [0, K) of `area` (after every lane has read its own: the wave's
-    // LDS accesses complete in order); rounds = the most any lane recorded
-    int kmax = cnt;
-    kmax = max(kmax, dpp_move<kDppRowShr + 1>(kmax));
-    kmax = max(kmax, dpp_move<kDppRowShr + 2>(kmax));
-    kmax = max(kmax, dpp_move<kDppRowShr + 4>(kmax));
-    kmax = max(kmax, dpp_move<kDppRowShr + 8>(kmax));
-    kmax = max(kmax, dpp_move<kDppRowBcast15, 0xA>(kmax));
-    kmax = max(kmax, dpp_move<kDppRowBcast31, 0xC>(kmax));
-    const int rounds = __builtin_amdgcn_readlane(kmax, kWave - 1);
-    auto compact = [&](auto width) {
+    return (int)(at / sizeof(float4)) - first;
+}
+
+__device__ __forceinline__ double seq_record_j(const float4& e) {
+    return __longlong_as_double((long long)((unsigned long long)__float_as_uint(e.x) |
+                                            ((unsigned long long)__float_as_uint(e.y) << 32)));
+}
+__device__ __forceinline__ float4 seq_record(double I, float a) {
+    const unsigned long long ib = (unsigned long long)__double_as_longlong(I);
+    return make_float4(__uint_as_float((unsigned)ib), __uint_as_float((unsigned)(ib >> 32)), a, 0.0f);
+}
+
+// Moves this lane's records src[first + k], k < cnt, to dst[off + k] with
+// I = base + (their J); lanes past their count write dst[spare].  All reads
+// complete before any write, so src and dst may be the same.
+__device__ __forceinline__ void seq_compact(const float4* src, int first, int cnt, double base, float4* dst, int off,
+                                            int spare) {
+    auto move = [&](auto width) {
         constexpr int kR = decltype(width)::value;
         float4 mine[kR];
 #pragma unroll
-        for (int k = 0; k < kR; ++k) mine[k] = area[first + k];
+        for (int k = 0; k < kR; ++k) mine[k] = src[first + k];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int k = 0; k < kR; ++k) {
-            const unsigned long long jb = (unsigned long long)__float_as_uint(mine[k].x) |
-                                          ((unsigned long long)__float_as_uint(mine[k].y) << 32);
-            const double I = Ibase + __longlong_as_double((long long)jb);
-            const unsigned long long ib = (unsigned long long)__double_as_longlong(I);
-            area[k < cnt ? off + k : kWave * kSeqSumCap + lane] =   // past every record: K <= 63 kSeqSumCap
-                make_float4(__uint_as_float((unsigned)ib), __uint_as_float((unsigned)(ib >> 32)), mine[k].z, 0.0f);
-        }
+        for (int k = 0; k < kR; ++k)
+            dst[k < cnt ? off + k : spare] = seq_record(base + seq_record_j(mine[k]), mine[k].z);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    if (rounds <= 2)
-        compact(std::integral_constant<int, 2>());
-    else if (rounds <= 4)
-        compact(std::integral_constant<int, 4>());
+    if (!__any(cnt > 0)) return;
+    if (!__any(cnt > 2))
+        move(std::integral_constant<int, 2>());
+    else if (!__any(cnt > 4))
+        move(std::integral_constant<int, 4>());
     else
-        compact(std::integral_constant<int, kSeqSumCap>());
-    // 4. the walk, lane i taking recorded step i: the running sum moves one
-    // lane up per step (wave_shr:1), lane i adds its exact jump R_i to the
-    // step and then the step's term, fl(fl(s + R_i) + a_i).  Lane 0 of a batch
-    // starts from the sum so far (folded into its jump, exactly).
-    float s = head;
+        move(std::integral_constant<int, kSeqSumCap>());
+}
+
+// The walk over the K compacted records rec[0, K), lane i taking recorded
+// step i: the running sum moves one lane up per step (wave_shr:1), lane i
+// adds its exact jump R_i to the step and then the step's term,
+// fl(fl(s + R_i) + a_i).  Lane 0 of a batch starts from the sum so far
+// (folded into its jump, exactly).  s starts at the head's total; Itot is the
+// exact sum of every safe increment.
+__device__ __forceinline__ float seq_walk(const float4* rec, int K, float s, double Itot, int lane) {
     double prev = 0.0;
     for (int b = 0; b < K; b += kWave) {
-        const float4 e = area[min(b + lane, K - 1)];
-        const double I = __longlong_as_double((long long)((unsigned long long)__float_as_uint(e.x) |
-                                                          ((unsigned long long)__float_as_uint(e.y) << 32)));
+        const float4 e = rec[min(b + lane, K - 1)];
+        const double I = seq_record_j(e);
         const double up = dpp_move<kDppWaveShr1>(I);
         float R = (float)(I - (lane == 0 ? prev : up));   // exact jump to this step
         if (lane == 0) R = s + R;                         // exact: the sum just before step b
@@ -294,6 +291,115 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
         prev = lane_value(I, m - 1);
     }
     return s + (float)(Itot - prev);
+}
+
+// v: n >= 1 non-negative floats in the transposed layout, its slots past n
+// holding +0 (seq_zero_tail); area: this wave's kSeqSumArea float4 of LDS
+// scratch.  n <= kSeqSumMaxPerLane * 64 = 2048; longer vectors take the chain.
+constexpr int kSeqSumMaxPerLane = 32;
+__device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
+    // A fresh lane index per call: callers inside long loops would otherwise
+    // have the lane-dependent constants below hoisted and held in registers.
+    int lane = threadIdx.x & (kWave - 1);
+    asm volatile("" : "+v"(lane));
+    const int E = seq_per_lane(n);
+    if (E > kSeqSumMaxPerLane) return seq_chain(v, n, E);
+    // 1. this lane's in-order total, the lanes' prefixes
+    const float T = seq_total(v, lane, 0, E, 0.0f);
+    const float incl = wave_inclusive_sum(T);
+    const float S = lane_value(incl, kWave - 1);
+    const float P = dpp_move<kDppWaveShr1>(incl);   // the exclusive prefix (lane 0: 0)
+    if (!(S < 0x1p126f)) return seq_chain(v, n, E);
+    if (S == 0.0f) return 0.0f;                     // all terms zero: the chain stays +0
+    const float head = lane_value(T, 0);            // lane 0's chunk: its in-order total
+    // 2. safe increments and recorded steps
+    const int first = lane * (kSeqSumCap + 1);
+    double J;
+    int cnt = seq_steps(v, lane, 0, E, P, SeqBounds(S, lane * E, E), area, first, J);
+    if (lane == 0) {   // the head took lane 0's chunk
+        cnt = 0;
+        J = 0.0;
+    }
+    if (__any(cnt > kSeqSumCap)) return seq_chain(v, n, E);
+    // 3. scans: the lanes' safe totals (exact in f64) and record counts; the
+    // records compacted in element order with I = (safe increments before)
+    const double Jincl = wave_inclusive_sum(J);
+    const int cincl = wave_inclusive_sum(cnt);
+    const double Itot = lane_value(Jincl, kWave - 1);
+    const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
+    seq_compact(area, first, cnt, Jincl - J, area, cincl - cnt,
+                kWave * kSeqSumCap + lane);   // past every record: K <= 63 kSeqSumCap
+    // 4. the walk
+    return seq_walk(area, K, head, Itot, lane);
+}
+
+// The same sum formed by the two waves of a pair, each stepping half of every
+// lane's chunk.  h: this wave (0 or 1); area0, area1: each wave's
+// kSeqSumArea float4; xchg: 2 * 64 float4 both waves see; comp: this wave's 128 float4.
+// trade(): the pair's barrier (false: leave, the sum is not formed).  Both
+// waves get the same bits.  Up to 64 recorded steps in all; more take the
+// plain chain (both waves).
+constexpr int kSeqPairRecords = kWave;
+constexpr int kSeqPairXchg = 2 * kWave;      // float4
+constexpr int kSeqPairComp = 2 * kWave;      // float4 per wave
+template <typename Trade>
+__device__ __forceinline__ bool wave_pair_sequential_sum(const float* v, int n, float4* area0, float4* area1,
+                                                         float4* xchg, float4* comp, int h, Trade&& trade,
+                                                         float& sum) {
+    int lane = threadIdx.x & (kWave - 1);
+    asm volatile("" : "+v"(lane));
+    const int E = seq_per_lane(n);
+    if (E > kSeqSumMaxPerLane) {
+        sum = seq_chain(v, n, E);
+        return true;
+    }
+    // 1. as above, with the in-order total of the chunk's first part
+    const int half = E / 8 * 4;   // wave 0 steps [0, half), wave 1 [half, E)
+    const float Th = seq_total(v, lane, 0, half, 0.0f);
+    const float T = seq_total(v, lane, half, E, Th);
+    const float incl = wave_inclusive_sum(T);
+    const float S = lane_value(incl, kWave - 1);
+    const float P = dpp_move<kDppWaveShr1>(incl);
+    if (!(S < 0x1p126f)) {
+        sum = seq_chain(v, n, E);
+        return true;
+    }
+    if (S == 0.0f) {
+        sum = 0.0f;
+        return true;
+    }
+    const float head = lane_value(T, 0);
+    // 2. this wave's part of every chunk (from P + Th: a few more roundings
+    // on the prefix's path, within the margin)
+    const int first = lane * (kSeqSumCap + 1);
+    double J;
+    int cnt = seq_steps(v, lane, h == 0 ? 0 : half, h == 0 ? half : E, h == 0 ? P : P + Th,
+                        SeqBounds(S, lane * E, E), h == 0 ? area0 : area1, first, J);
+    if (lane == 0) {
+        cnt = 0;
+        J = 0.0;
+    }
+    xchg[h * kWave + lane] = seq_record(J, __int_as_float(cnt));
+    if (!trade()) return false;
+    const float4 other = xchg[(h ^ 1) * kWave + lane];
+    const double J0 = h == 0 ? J : seq_record_j(other), J1 = h == 0 ? seq_record_j(other) : J;
+    const int c0 = h == 0 ? cnt : __float_as_int(other.z), c1 = h == 0 ? __float_as_int(other.z) : cnt;
+    // 3. both waves: the same scans, compaction into their own records, walk
+    const double Jl = J0 + J1;   // exact
+    const int cl = c0 + c1;
+    const double Jincl = wave_inclusive_sum(Jl);
+    const int cincl = wave_inclusive_sum(cl);
+    const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
+    if (__any(c0 > kSeqSumCap || c1 > kSeqSumCap) || K > kSeqPairRecords) {
+        sum = seq_chain(v, n, E);
+        return true;
+    }
+    const double Ibase = Jincl - Jl;
+    const int off = cincl - cl, spare = kSeqPairRecords + lane;
+    seq_compact(area0, first, c0, Ibase, comp, off, spare);
+    seq_compact(area1, first, c1, Ibase + J0, comp, off + c0, spare);
+    sum = seq_walk(comp, K, head, lane_value(Jincl, kWave - 1), lane);
+    return true;
 }
 
 }  // namespace leafhip

@@ -3,9 +3,10 @@
 norm() sums a row's squares and attention_impl its softmax denominator one
 element after another in float (decoder.cpp:716-718, transformer.cpp:127-130).
 The decode step forms that sum with one wave (wave_sequential_sum in
-leaf_amd/csrc/sequential_sum.h): runs of steps whose rounding cannot depend on
-the running sum are added as exact jumps and only the others are taken one by
-one.  Here it must equal numpy's float32 accumulate -- a plain loop, one
+leaf_amd/csrc/sequential_sum.h; the softmax denominator) or two
+(wave_pair_sequential_sum; the RMSNorm squares): runs of steps whose rounding
+cannot depend on the running sum are added as exact jumps and only the others
+are taken one by one.  Here it must equal numpy's float32 accumulate -- a plain loop, one
 rounding per element -- bit for bit, on the shapes it serves (2048 and 5632
 squares, a few hundred to 4,096 softmax terms) and on inputs built to defeat
 it: ties at every step, powers of two, two scales 2^30 apart, zeros, one
@@ -66,17 +67,19 @@ def cases(n, rng):
     yield "leading zeros", zeros_first
 
 
+@pytest.mark.parametrize("method", [0, 2], ids=["one wave", "two waves"])
 @pytest.mark.parametrize("n", [1, 7, 33, 64, 256, 257, 600, 640, 760, 1000, 2047, 2048, 4096, 5632])
-def test_parallel_column_sum_equals_the_chain(rt, n):
+def test_parallel_column_sum_equals_the_chain(rt, n, method):
     rng = np.random.default_rng(n)
     for name, x in cases(n, rng):
-        got, _ = gpu_sums(rt, x)
+        got, _ = gpu_sums(rt, x, method)
         want = column_sums(x)
         bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
         assert bad.size == 0, f"{name}, n={n}: {bad.size} of {len(want)} sums differ (row {bad[0]})"
 
 
-def test_unusual_terms(rt):
+@pytest.mark.parametrize("method", [0, 2], ids=["one wave", "two waves"])
+def test_unusual_terms(rt, method):
     # a subnormal term and -0 are summed like any other; infinite, NaN and
     # negative terms and a total past 2^126 take the plain chain
     x = np.abs(np.random.default_rng(1).standard_normal((7, 2048))).astype(np.float32)
@@ -87,7 +90,7 @@ def test_unusual_terms(rt):
     x[4, 9] = np.float32(-0.0)
     x[5, 11] = np.float32(-1.5)
     x[6, :] = np.float32(1e-40)
-    got, _ = gpu_sums(rt, x)
+    got, _ = gpu_sums(rt, x, method)
     want = column_sums(x)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
@@ -106,7 +109,10 @@ def test_parallel_sum_is_faster_than_the_chain(rt):
     for n in (600, 2048):
         x = (rng.standard_normal((256, n)) ** 2).astype(np.float32)
         fast, c0 = gpu_sums(rt, x, 0)
+        pair, c2 = gpu_sums(rt, x, 2)
         slow, c1 = gpu_sums(rt, x, 1)
         assert np.array_equal(fast.view(np.uint32), slow.view(np.uint32))
-        print(f"n={n}: parallel {np.median(c0):.0f} cycles, chain {np.median(c1):.0f} cycles")
-        assert np.median(c0) < np.median(c1)
+        assert np.array_equal(pair.view(np.uint32), slow.view(np.uint32))
+        print(f"n={n}: one wave {np.median(c0):.0f} cycles, two waves {np.median(c2):.0f}, "
+              f"chain {np.median(c1):.0f}")
+        assert np.median(c0) < np.median(c1) and np.median(c2) < np.median(c1)
