@@ -79,18 +79,19 @@ __device__ __forceinline__ void seq_zero_tail(float* v, int n, int first, int st
     for (int e = n + first; e < kWave * lay.E; e += stride) v[lay.at(e)] = 0.0f;
 }
 
-// Elements [0, m) in order (lane by lane, a lane's chunk top to bottom), 32
-// LDS reads in flight at a time.
+// Elements [0, m) in order (lane by lane, a lane's chunk top to bottom), 8
+// LDS reads in flight at a time.  The fallback of the parallel sums below:
+// one call site each, small code.
 __device__ __forceinline__ float seq_chain(const float* v, int m, int E) {
     float s = 0.0f;
     for (int l = 0; l * E < m; ++l) {
         const int end = min(E, m - l * E);
-        for (int i0 = 0; i0 < end; i0 += 32) {
-            float e[32];
+        for (int i0 = 0; i0 < end; i0 += 8) {
+            float e[8];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) e[i] = v[min(i0 + i, end - 1) * kWave + l];
+            for (int i = 0; i < 8; ++i) e[i] = v[min(i0 + i, end - 1) * kWave + l];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) s = s + (i0 + i < end ? e[i] : 0.0f);   // + 0 leaves s unchanged
+            for (int i = 0; i < 8; ++i) s = s + (i0 + i < end ? e[i] : 0.0f);   // + 0 leaves s unchanged
         }
     }
     return s;
@@ -257,12 +258,20 @@ __device__ __forceinline__ void seq_compact(const float4* src, int first, int cn
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
     if (!__any(cnt > 0)) return;
-    if (!__any(cnt > 2))
-        move(std::integral_constant<int, 2>());
-    else if (!__any(cnt > 4))
+    if (!__any(cnt > 4))
         move(std::integral_constant<int, 4>());
     else
         move(std::integral_constant<int, kSeqSumCap>());
+}
+
+// The same from src into a distinct dst, one record per round (rounds: while
+// any lane has one left).
+__device__ __forceinline__ void seq_copy_records(const float4* src, int first, int cnt, double base, float4* dst,
+                                                 int off, int spare) {
+    for (int k = 0; __any(k < cnt); ++k) {
+        const float4 e = src[first + k];
+        dst[k < cnt ? off + k : spare] = seq_record(base + seq_record_j(e), e.z);
+    }
 }
 
 // The walk over the K compacted records rec[0, K), lane i taking recorded
@@ -297,20 +306,18 @@ __device__ __forceinline__ float seq_walk(const float4* rec, int K, float s, dou
 // holding +0 (seq_zero_tail); area: this wave's kSeqSumArea float4 of LDS
 // scratch.  n <= kSeqSumMaxPerLane * 64 = 2048; longer vectors take the chain.
 constexpr int kSeqSumMaxPerLane = 32;
-__device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
-    // A fresh lane index per call: callers inside long loops would otherwise
-    // have the lane-dependent constants below hoisted and held in registers.
-    int lane = threadIdx.x & (kWave - 1);
-    asm volatile("" : "+v"(lane));
-    const int E = seq_per_lane(n);
-    if (E > kSeqSumMaxPerLane) return seq_chain(v, n, E);
+// The parallel form; false where the chain must be taken.
+__device__ __forceinline__ bool seq_parallel(const float* v, int n, int E, int lane, float4* area, float& sum) {
     // 1. this lane's in-order total, the lanes' prefixes
     const float T = seq_total(v, lane, 0, E, 0.0f);
     const float incl = wave_inclusive_sum(T);
     const float S = lane_value(incl, kWave - 1);
     const float P = dpp_move<kDppWaveShr1>(incl);   // the exclusive prefix (lane 0: 0)
-    if (!(S < 0x1p126f)) return seq_chain(v, n, E);
-    if (S == 0.0f) return 0.0f;                     // all terms zero: the chain stays +0
+    if (!(S < 0x1p126f)) return false;
+    if (S == 0.0f) {   // all terms zero: the chain stays +0
+        sum = 0.0f;
+        return true;
+    }
     const float head = lane_value(T, 0);            // lane 0's chunk: its in-order total
     // 2. safe increments and recorded steps
     const int first = lane * (kSeqSumCap + 1);
@@ -320,7 +327,7 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
         cnt = 0;
         J = 0.0;
     }
-    if (__any(cnt > kSeqSumCap)) return seq_chain(v, n, E);
+    if (__any(cnt > kSeqSumCap)) return false;
     // 3. scans: the lanes' safe totals (exact in f64) and record counts; the
     // records compacted in element order with I = (safe increments before)
     const double Jincl = wave_inclusive_sum(J);
@@ -330,7 +337,19 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
     seq_compact(area, first, cnt, Jincl - J, area, cincl - cnt,
                 kWave * kSeqSumCap + lane);   // past every record: K <= 63 kSeqSumCap
     // 4. the walk
-    return seq_walk(area, K, head, Itot, lane);
+    sum = seq_walk(area, K, head, Itot, lane);
+    return true;
+}
+
+__device__ __forceinline__ float wave_sequential_sum(const float* v, int n, float4* area) {
+    // A fresh lane index per call: callers inside long loops would otherwise
+    // have the lane-dependent constants below hoisted and held in registers.
+    int lane = threadIdx.x & (kWave - 1);
+    asm volatile("" : "+v"(lane));
+    const int E = seq_per_lane(n);
+    float sum;
+    if (!(E <= kSeqSumMaxPerLane && seq_parallel(v, n, E, lane, area, sum))) sum = seq_chain(v, n, E);
+    return sum;
 }
 
 // The same sum formed by the two waves of a pair, each stepping half of every
@@ -342,17 +361,12 @@ __device__ __forceinline__ float wave_sequential_sum(const float* v, int n, floa
 constexpr int kSeqPairRecords = kWave;
 constexpr int kSeqPairXchg = 2 * kWave;      // float4
 constexpr int kSeqPairComp = 2 * kWave;      // float4 per wave
+// The pair's parallel form: 0 done, 1 the chain must be taken, 2 the trade
+// failed.
 template <typename Trade>
-__device__ __forceinline__ bool wave_pair_sequential_sum(const float* v, int n, float4* area0, float4* area1,
-                                                         float4* xchg, float4* comp, int h, Trade&& trade,
-                                                         float& sum) {
-    int lane = threadIdx.x & (kWave - 1);
-    asm volatile("" : "+v"(lane));
-    const int E = seq_per_lane(n);
-    if (E > kSeqSumMaxPerLane) {
-        sum = seq_chain(v, n, E);
-        return true;
-    }
+__device__ __forceinline__ int seq_pair_parallel(const float* v, int n, int E, int lane, float4* area0,
+                                                 float4* area1, float4* xchg, float4* comp, int h, Trade&& trade,
+                                                 float& sum) {
     // 1. as above, with the in-order total of the chunk's first part
     const int half = E / 8 * 4;   // wave 0 steps [0, half), wave 1 [half, E)
     const float Th = seq_total(v, lane, 0, half, 0.0f);
@@ -360,13 +374,10 @@ __device__ __forceinline__ bool wave_pair_sequential_sum(const float* v, int n, 
     const float incl = wave_inclusive_sum(T);
     const float S = lane_value(incl, kWave - 1);
     const float P = dpp_move<kDppWaveShr1>(incl);
-    if (!(S < 0x1p126f)) {
-        sum = seq_chain(v, n, E);
-        return true;
-    }
+    if (!(S < 0x1p126f)) return 1;
     if (S == 0.0f) {
         sum = 0.0f;
-        return true;
+        return 0;
     }
     const float head = lane_value(T, 0);
     // 2. this wave's part of every chunk (from P + Th: a few more roundings
@@ -380,25 +391,38 @@ __device__ __forceinline__ bool wave_pair_sequential_sum(const float* v, int n, 
         J = 0.0;
     }
     xchg[h * kWave + lane] = seq_record(J, __int_as_float(cnt));
-    if (!trade()) return false;
+    if (!trade()) return 2;
     const float4 other = xchg[(h ^ 1) * kWave + lane];
     const double J0 = h == 0 ? J : seq_record_j(other), J1 = h == 0 ? seq_record_j(other) : J;
     const int c0 = h == 0 ? cnt : __float_as_int(other.z), c1 = h == 0 ? __float_as_int(other.z) : cnt;
-    // 3. both waves: the same scans, compaction into their own records, walk
+    // 3. both waves: the same scans, the records copied into their own
+    // list, the walk
     const double Jl = J0 + J1;   // exact
     const int cl = c0 + c1;
     const double Jincl = wave_inclusive_sum(Jl);
     const int cincl = wave_inclusive_sum(cl);
     const int K = __builtin_amdgcn_readlane(cincl, kWave - 1);
-    if (__any(c0 > kSeqSumCap || c1 > kSeqSumCap) || K > kSeqPairRecords) {
-        sum = seq_chain(v, n, E);
-        return true;
-    }
+    if (__any(c0 > kSeqSumCap || c1 > kSeqSumCap) || K > kSeqPairRecords) return 1;
     const double Ibase = Jincl - Jl;
     const int off = cincl - cl, spare = kSeqPairRecords + lane;
-    seq_compact(area0, first, c0, Ibase, comp, off, spare);
-    seq_compact(area1, first, c1, Ibase + J0, comp, off + c0, spare);
+    seq_copy_records(area0, first, c0, Ibase, comp, off, spare);
+    seq_copy_records(area1, first, c1, Ibase + J0, comp, off + c0, spare);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     sum = seq_walk(comp, K, head, lane_value(Jincl, kWave - 1), lane);
+    return 0;
+}
+
+template <typename Trade>
+__device__ __forceinline__ bool wave_pair_sequential_sum(const float* v, int n, float4* area0, float4* area1,
+                                                         float4* xchg, float4* comp, int h, Trade&& trade,
+                                                         float& sum) {
+    int lane = threadIdx.x & (kWave - 1);
+    asm volatile("" : "+v"(lane));
+    const int E = seq_per_lane(n);
+    const int state = E <= kSeqSumMaxPerLane ? seq_pair_parallel(v, n, E, lane, area0, area1, xchg, comp, h, trade, sum)
+                                             : 1;
+    if (state == 2) return false;
+    if (state == 1) sum = seq_chain(v, n, E);
     return true;
 }
 
