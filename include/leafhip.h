@@ -205,7 +205,8 @@ lh_status lh_timer_stop(lh_timer* timer, lh_stream stream, double* milliseconds)
 lh_status lh_set_kernel_numerics(uint32_t numerics);
 /* y[i] = expf(x[i]) with the result glibc 2.35's expf returns on x86-64 with
  * FMA (the exp of the CPU path's softmax and SiLU, transformer.cpp:134,
- * decoder.cpp:983), for every float input. */
+ * decoder.cpp:983), for every float input (a NaN input gives a NaN, its
+ * payload unspecified). */
 lh_status lh_expf(const float* x, size_t count, float* y, lh_stream stream);
 /* sums[i] = (...((0 + x[i][0]) + x[i][1]) + ...) + x[i][n - 1] in float, the
  * order in which norm() sums its squares and attention_impl its softmax

@@ -1021,17 +1021,31 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     };
     lds_done();
     // exp(s - max) of this lane's keys (lane * E + i, at row i of column lane),
-    // four at a time (a wider unroll interleaves so many expf evaluations that
-    // their registers spill)
-    for (int i0 = 0; i0 < E; i0 += 4) {
-        float e[4];
+    // eight at a time, the next eight scores read before these are formed
+    {
+        float cur[8], nxt[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = pe[min(i0 + i, E - 1) * kWave + lane];
+        for (int i = 0; i < 8; ++i) cur[i] = pe[min(i, E - 1) * kWave + lane];
+        for (int i0 = 0; i0 < E; i0 += 8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = i0 + i < valid ? lds_expf(e[i] - maximum, exp2) : 0.0f;
+            for (int i = 0; i < 8; ++i) nxt[i] = pe[min(i0 + 8 + i, E - 1) * kWave + lane];
+            float e[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i0 + i < E) pe[(i0 + i) * kWave + lane] = e[i];
+            for (int i = 0; i < 8; ++i) e[i] = cur[i] - maximum;
+            libm_expf_batch(e, [exp2](uint32_t k) { return exp2[k]; });
+            // every lane forms all eight (a select per key, no branch around
+            // an evaluation)
+            asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]),
+                              "+v"(e[7]));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cur[i] = i0 + i < valid ? e[i] : 0.0f;
+            // rows past E (at most to row 31: E <= 32, a multiple of 4) take
+            // zeros no sum reads
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pe[(i0 + i) * kWave + lane] = cur[i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        }
     }
     lds_done();
     // the first chunks' V columns load while the denominator is formed

@@ -87,6 +87,47 @@ LEAF_HOST_DEVICE inline float libm_expf_from(float x, const Table& table) {
     return (float)y;
 }
 
+#if defined(__HIP__)
+// N evaluations of libm_expf_from at once, for kernels: in phases (every
+// table read issued before any is used) and without branches (the special
+// cases selected afterwards), so the evaluations interleave.  Equal to N
+// separate calls bit for bit, except that a NaN input gives a NaN of another
+// payload.
+template <int N, typename Table>
+__device__ inline void libm_expf_batch(float (&x)[N], const Table& table) {
+    const double inv_ln2_n = 0x1.71547652b82fep+5;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-20;
+    const double c1 = 0x1.ebfce50fac4f3p-13;
+    const double c2 = 0x1.62e42ff0c52d6p-6;
+    double r[N];
+    uint64_t ki[N], t[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const double xd = (double)x[i];
+        double kd = __builtin_fma(inv_ln2_n, xd, shift);
+        ki[i] = __builtin_bit_cast(uint64_t, kd);
+        kd -= shift;
+        r[i] = __builtin_fma(inv_ln2_n, xd, -kd);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = table((uint32_t)(ki[i] % 32));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const double s = __builtin_bit_cast(double, t[i] + (ki[i] << 47));
+        const double p = __builtin_fma(c0, r[i], c1);
+        const double r2 = r[i] * r[i];
+        double y = __builtin_fma(c2, r[i], 1.0);
+        y = __builtin_fma(p, r2, y);
+        y = y * s;
+        float result = (float)y;                                      // NaN stays NaN
+        result = x[i] < -0x1.9fe368p6f ? 0.0f : result;              // exp(x) < 2^-150, and -inf
+        result = x[i] > 0x1.62e42ep6f ? __builtin_inff() : result;   // exp(x) > 2^128, and +inf
+        x[i] = result;
+    }
+}
+#endif
+
 LEAF_HOST_DEVICE inline float libm_expf(float x) {
     return libm_expf_from(x, [](uint32_t i) { return kExp2Table32[i]; });
 }

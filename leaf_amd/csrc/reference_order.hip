@@ -401,9 +401,19 @@ __global__ __launch_bounds__(2 * kWave) void ro_sequential_sum_kernel(const floa
     }
 }
 
+// Eight inputs per thread through libm_expf_batch (the decode step's softmax
+// form), so that lh_expf checks that form.
 __global__ void ro_expf_kernel(const float* x, size_t count, float* y) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < count; i += (size_t)gridDim.x * blockDim.x)
-        y[i] = libm_expf(x[i]);
+    const size_t stride = (size_t)gridDim.x * blockDim.x * 8;
+    for (size_t i0 = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) * 8; i0 < count; i0 += stride) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k < count ? x[i0 + k] : 0.0f;
+        libm_expf_batch(v, [](uint32_t k) { return kExp2Table32[k]; });
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (i0 + k < count) y[i0 + k] = v[k];
+    }
 }
 
 // ------------------------------------------------------------------ dot ----
