@@ -629,6 +629,75 @@ def derive_prefill_counters(base: Path) -> dict:
     return out
 
 
+def derive_f32_gemm_counters(base: Path) -> dict:
+    """MFMA utilisation of the f32 prefill GEMMs of the Qwen INT4 (4096-token)
+    and SmolLM2 BF16 (2048-token) prefills, from rocprofv3 --pmc runs under
+    `base` with SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE:
+      qwen/ smollm2/   leaf_decoder, one prefill of the configuration's prompt,
+                       counters on the gemm_f32 kernels only
+      peak/            leaf_amd/bin/mfma_peak (its v_mfma_f32_16x16x4_f32 loop)
+    Busy fractions are relative to what the same ratios read for that loop."""
+    import re
+
+    from leaf_amd import models
+
+    def db(name):
+        return next((base / name).glob("*.db"))
+
+    peak = [v for name, _, v in _db_counters(db("peak")) if "mfma_f32_kernel" in name]
+    peak_busy = max(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["GRBM_GUI_ACTIVE"] for v in peak)
+    peak_cu = max(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["SQ_BUSY_CU_CYCLES"] for v in peak)
+    meta = golden()[0]
+    out = {"peak_reference": "leaf_amd/bin/mfma_peak v_mfma_f32_16x16x4_f32 loop", "configs": {}}
+    for family in ("qwen", "smollm2"):
+        spec = models.PRESETS[family]()
+        M = meta[family]["prompt_tokens"]
+        qkv_rows = spec.heads * spec.head_dim + 2 * spec.kv_heads * spec.head_dim
+        up_rows = 2 * spec.intermediate if spec.gated else spec.intermediate
+        shapes = {"qkv": (qkv_rows, spec.hidden), "o": (spec.hidden, spec.heads * spec.head_dim),
+                  "gate_up": (up_rows, spec.hidden), "down": (spec.hidden, spec.intermediate)}
+        entries = [(name, blocks, v) for name, blocks, v in _db_counters(db(family)) if "gemm_f32" in name]
+        # A layer launches q|k|v, o, gate|up, down in that order; o and down
+        # can share a kernel and grid, so they are told apart by what came before.
+        keys = [(name, blocks) for name, blocks, _ in entries[:4]]
+        table, previous = {}, None
+        for name, blocks, v in entries:
+            key = (name, blocks)
+            label = ("qkv" if key == keys[0] else "gate_up" if key == keys[2]
+                     else "o" if key == keys[1] and previous == "qkv"
+                     else "down" if key == keys[3] and previous == "gate_up" else None)
+            previous = label
+            if label is None:
+                continue
+            kernel = re.sub(r"leafhip::|\(anonymous namespace\)::", "", name).split("(")[0]
+            t = table.setdefault(label, {"kernel": kernel, "blocks": blocks, "wall": [], "cu": []})
+            t["wall"].append(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["GRBM_GUI_ACTIVE"] / peak_busy)
+            t["cu"].append(v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["SQ_BUSY_CU_CYCLES"] / peak_cu)
+        out["configs"][family] = {
+            label: {"M": M, "N": shapes[label][0], "K": shapes[label][1], "kernel": t["kernel"],
+                    "blocks": t["blocks"], "dispatches": len(t["wall"]),
+                    "mfma_busy_of_peak_loop_wall": round(sum(t["wall"]) / len(t["wall"]), 4),
+                    "mfma_busy_of_peak_loop_cu_busy": round(sum(t["cu"]) / len(t["cu"]), 4)}
+            for label, t in table.items()}
+    return out
+
+
+def summarize_counters(base: Path) -> str:
+    """Mean counter values per dispatch, per kernel, over every rocprofv3 --pmc
+    run under `base` (each a directory holding one *_results.db)."""
+    import re
+    per: dict = {}
+    for db in sorted(base.glob("*/*_results.db")):
+        for name, _, values in _db_counters(db):
+            kernel = re.sub(r"leafhip::|\(anonymous namespace\)::", "", name).split("(")[0]
+            for counter, value in values.items():
+                per.setdefault((kernel, counter), []).append(value)
+    lines = ["| Kernel | Counter | Dispatches | Mean per dispatch |", "|---|---|---:|---:|"]
+    for (kernel, counter), vals in sorted(per.items()):
+        lines.append(f"| `{kernel}` | {counter} | {len(vals)} | {sum(vals) / len(vals):,.1f} |")
+    return "\n".join(lines)
+
+
 def summarize_trace(db: Path, top: int = 25) -> str:
     """Markdown tables from a rocprofv3 --kernel-trace run (rocpd SQLite output):
     the top kernels by total time, and the prefill W8A8 GEMMs by shape (labelled
@@ -748,6 +817,8 @@ def main() -> int:
     parser.add_argument("--no-fast", action="store_true", help="skip the fast-numerics extra")
     parser.add_argument("--derive-traffic", type=Path, default=None)
     parser.add_argument("--derive-prefill-counters", type=Path, default=None)
+    parser.add_argument("--derive-f32-gemm-counters", type=Path, default=None)
+    parser.add_argument("--summarize-counters", type=Path, default=None)
     parser.add_argument("--summarize-trace", type=Path, default=None)
     parser.add_argument("--summarize-config-trace", type=Path, default=None)
     args = parser.parse_args()
@@ -759,6 +830,12 @@ def main() -> int:
         return 0
     if args.derive_prefill_counters is not None:
         print(json.dumps(derive_prefill_counters(args.derive_prefill_counters), indent=1))
+        return 0
+    if args.summarize_counters is not None:
+        print(summarize_counters(args.summarize_counters))
+        return 0
+    if args.derive_f32_gemm_counters is not None:
+        print(json.dumps(derive_f32_gemm_counters(args.derive_f32_gemm_counters), indent=1))
         return 0
     if args.derive_traffic is not None:
         traffic = derive_traffic(args.derive_traffic)

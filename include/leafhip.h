@@ -108,8 +108,12 @@ lh_status lh_model_destroy(lh_model* model);
  *    LEAF_DISABLE_VNNI is set, a multiply and an add (quant_vnni_tile,
  *    :661-702; selection at :780-782, 1022).  REFERENCE follows this host as
  *    the CPU path would; REFERENCE_AVX2 / REFERENCE_VNNI pin either form.
- *  DEFAULT: FAST, unless the environment variable LEAF_GPU_NUMERICS names a
- *    mode: reference, reference-avx2 or reference-vnni. */
+ *    A REFERENCE session holds at most 32,448 visible keys per query (one
+ *    query's scores sit in LDS); a larger requested max_context is refused
+ *    with LH_ERROR_UNSUPPORTED, and max_context 0 stops there.
+ *  DEFAULT: REFERENCE for a model loaded with 8-bit activations (W8A8),
+ *    FAST otherwise, unless the environment variable LEAF_GPU_NUMERICS names
+ *    a mode: fast, reference, reference-avx2 or reference-vnni. */
 #define LH_NUMERICS_DEFAULT 0
 #define LH_NUMERICS_FAST 1
 #define LH_NUMERICS_REFERENCE 2
@@ -180,6 +184,11 @@ lh_status lh_copy_to_device(void* device_dst, const void* host_src, size_t bytes
 lh_status lh_copy_to_host(void* host_dst, const void* device_src, size_t bytes);
 lh_status lh_memset_device(void* device_dst, int value, size_t bytes);
 lh_status lh_synchronize(void);
+/* The kernel-level entry points keep their device scratch per (device, stream
+ * handle), at least 1 MiB per stream once used.  lh_stream_destroy waits for
+ * the stream and frees that scratch; the scratch of a stream that was ever
+ * captured stays allocated until the process ends, since a graph captured
+ * from it may still be launched. */
 lh_status lh_stream_create(lh_stream* out);
 lh_status lh_stream_destroy(lh_stream stream);
 lh_status lh_stream_synchronize(lh_stream stream);

@@ -57,24 +57,51 @@ hipStream_t as_stream(lh_stream s) { return static_cast<hipStream_t>(s); }
 // Device scratch of the kernel-level entry points (quantized inputs, split-K
 // sums, attention partials), one set per (device, stream): calls on different
 // streams never share memory.  A buffer that must grow is replaced and the old
-// one is kept until the process ends, so work already queued on it, or a
-// graph captured with it, stays valid without any synchronization.  Growth
-// while the stream is capturing is refused: run the call once before
-// capturing it.  The sets are never freed -- in particular not by static
-// destructors, which run after the HIP runtime and a profiler may have shut
-// down.
+// one is kept with the stream's set, so work already queued on it, or a graph
+// captured with it, stays valid without any synchronization.  Growth while
+// the stream is capturing is refused: run the call once before capturing it.
+// lh_stream_destroy waits for the stream and frees its sets, unless the
+// stream has been captured: a graph captured from it may be launched later on
+// another stream, so such a set is kept until the process ends.  Nothing is
+// freed by static destructors, which run after the HIP runtime and a
+// profiler may have shut down.
 struct StreamScratch {
     leafhip::DeviceBuffer* work = nullptr;       // grown on demand
     leafhip::DeviceBuffer* counters = nullptr;   // zeroed once; the attention kernel resets what it uses
+    std::vector<leafhip::DeviceBuffer*> retired;  // outgrown work buffers
+    bool captured = false;                        // a graph may hold these buffers
 };
 std::mutex g_scratch_lock;
 auto* g_scratch = new std::map<std::pair<int, hipStream_t>, StreamScratch>();
-auto* g_retired = new std::vector<leafhip::DeviceBuffer*>();
 
 StreamScratch& scratch_of(hipStream_t stream) {
     int dev = 0;
     leafhip::hip_check(hipGetDevice(&dev), "hipGetDevice");
     return (*g_scratch)[{dev, stream}];
+}
+
+// Called with the stream idle and about to be destroyed.
+void release_stream_scratch(hipStream_t stream) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    for (auto it = g_scratch->begin(); it != g_scratch->end();) {
+        if (it->first.second != stream) {
+            ++it;
+            continue;
+        }
+        StreamScratch& sc = it->second;
+        if (!sc.captured) {
+            delete sc.work;
+            delete sc.counters;
+            for (leafhip::DeviceBuffer* b : sc.retired) delete b;
+        }
+        it = g_scratch->erase(it);
+    }
+}
+
+void mark_stream_captured(hipStream_t stream) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    for (auto& [key, sc] : *g_scratch)
+        if (key.second == stream) sc.captured = true;
 }
 
 bool capturing(hipStream_t stream) {
@@ -91,7 +118,7 @@ void* scratch_bytes(size_t bytes, hipStream_t stream) {
             throw leafhip::Error(LH_ERROR_STATE, "Leaf decoder: kernel scratch must grow outside stream capture "
                                                  "(run the call once before capturing it)");
         auto* grown = new leafhip::DeviceBuffer(std::max(bytes, sc.work ? 2 * sc.work->bytes : size_t(1) << 20));
-        if (sc.work) g_retired->push_back(sc.work);
+        if (sc.work) sc.retired.push_back(sc.work);
         sc.work = grown;
     }
     return sc.work->ptr;
@@ -483,7 +510,12 @@ lh_status lh_stream_create(lh_stream* out) {
     });
 }
 lh_status lh_stream_destroy(lh_stream stream) {
-    return guarded([&] { leafhip::hip_check(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy"); });
+    return guarded([&] {
+        require_arg(stream, "only a created stream can be destroyed");
+        leafhip::hip_check(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+        release_stream_scratch(as_stream(stream));
+        leafhip::hip_check(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+    });
 }
 lh_status lh_stream_synchronize(lh_stream stream) {
     return guarded([&] { leafhip::hip_check(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); });
@@ -491,6 +523,7 @@ lh_status lh_stream_synchronize(lh_stream stream) {
 lh_status lh_stream_begin_capture(lh_stream stream) {
     return guarded([&] {
         require_arg(stream, "capture needs a created stream");
+        mark_stream_captured(as_stream(stream));
         leafhip::hip_check(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
                            "hipStreamBeginCapture");
     });

@@ -37,7 +37,8 @@
 namespace leafhip {
 
 // T[i] = bits(nearest double to 2^(i/32)) - (i << 47).  The values follow from
-// the definition alone: tests/test_expf_table.py recomputes them in decimal
+// the definition alone: tests/test_libm_expf.py::
+// test_exp2_table_follows_from_its_definition recomputes them in decimal
 // arithmetic.
 #if defined(__HIP__)
 __device__ __constant__

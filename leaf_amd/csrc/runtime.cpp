@@ -100,6 +100,14 @@ struct Plan {
 std::unique_ptr<Model> Model::load(Context& context, const uint8_t* data, size_t size, uint32_t activation_bits,
                                    uint32_t fp32_math) {
     ArtifactContents artifact = read_artifact(data, size, activation_bits, fp32_math);
+    // The loader's size rule computes rows·cols·bits/8 in 64 bits, as the
+    // reference's does, so a shape of 2^59 elements or more can wrap to the
+    // stored byte count.  Kernels index by shape: recheck without wrapping.
+    for (const auto& [name, t] : artifact.tensors) {
+        const unsigned __int128 bits = static_cast<unsigned __int128>(uint64_t(t.rows) * t.cols) * t.bits;
+        if (bits != static_cast<unsigned __int128>(t.size) * 8)
+            throw Error(LH_ERROR_ARTIFACT, "Leaf decoder: invalid tensor data range " + name);
+    }
     auto model = std::make_unique<Model>(context);
     Model& m = *model;
     m.config = artifact.config;

@@ -181,6 +181,24 @@ def mutants(blob: bytes, version: int, full: bool):
     return out
 
 
+def with_extra_tensor(blob: bytes, version: int, name: str, rows: int, cols: int, bits: int,
+                      size: int = 0) -> bytes:
+    """The artifact with one more tensor descriptor (rank 2, no group or scales,
+    data at offset 0) after the others; the payload moves with the data base."""
+    lay = layout(blob, version)
+    last = lay.descriptors[-1]
+    end = last[2] + DESCRIPTOR.size
+    entry = struct.pack("<I", len(name)) + name.encode() + DESCRIPTOR.pack(2, rows, cols, bits, 0, 0, size, 0, 0)
+    base = (end + len(entry) + 63) & ~63
+    out = bytearray(blob[:end] + entry)
+    out += bytes(base - len(out))
+    out += blob[lay.base:]
+    (count,) = struct.unpack_from("<I", blob, 12)
+    struct.pack_into("<I", out, 12, count + 1)
+    struct.pack_into("<Q", out, 16, base)
+    return bytes(out)
+
+
 def reference_verdict(tmp: Path, blob: bytes, bits: int, tag: str = "m") -> str | None:
     """None when the reference loads the artifact and runs a one-token forward,
     else its error line (kept verbatim: messages may end in a space)."""
@@ -223,3 +241,24 @@ def test_validator_matches_the_reference_loader(base):
                 differences.append(f"{label}: reference {want!r}, here {got!r}")
         print(f"{base} (LEAFDC0{report['version']}): {len(cases)} mutants, {len(differences)} differences")
         assert not differences, "\n".join(differences[:20])
+
+
+def test_a_shape_whose_byte_count_wraps_passes_the_loader_rules():
+    """rows·cols·bits/8 is computed in 64 bits by the reference's loader
+    (decoder.cpp:875-877), so an extra tensor of 2^31 x 2^28 FP32 elements
+    and 0 stored bytes passes it, and lh_artifact_check agrees.  The GPU load
+    path rechecks the shape without wrapping
+    (tests/test_gpu_decoder.py::test_gpu_load_rejects_a_wrapping_tensor_shape)."""
+    from leaf_amd import runtime
+    spec, bits = bases()["w8a8"]
+    with tempfile.TemporaryDirectory() as d:
+        tmp = Path(d)
+        report = write_artifact(tmp / "base.leaf", spec, seed=11)
+        blob = with_extra_tensor((tmp / "base.leaf").read_bytes(), report["version"], "model.extra.weight",
+                                 1 << 31, 1 << 28, 32)
+        assert reference_verdict(tmp, blob, bits) is None
+        assert runtime.artifact_check(blob, bits) is None
+        unwrapped = with_extra_tensor((tmp / "base.leaf").read_bytes(), report["version"], "model.extra.weight",
+                                      1 << 20, 1 << 20, 32)
+        want = reference_verdict(tmp, unwrapped, bits)
+        assert want is not None and want == "Leaf decoder: " + runtime.artifact_check(unwrapped, bits)

@@ -122,6 +122,25 @@ def test_rejects_corrupt_artifacts(runtime, tmp_path, artifacts):
         runtime.Decoder(artifacts["smollm2"], 8)
 
 
+def test_gpu_load_rejects_a_wrapping_tensor_shape(runtime, tmp_path, artifacts):
+    """An extra tensor of 2^31 x 2^28 FP32 elements and 0 stored bytes passes
+    the loader's 64-bit size rule (lh_artifact_check accepts it, like the
+    reference); loading it onto the device rechecks the shape without wrapping."""
+    import struct
+    from tests.test_artifact_validation import with_extra_tensor
+    blob = artifacts["tinyllama"].read_bytes()
+    (version,) = struct.unpack_from("<I", blob, 8)
+    bad = with_extra_tensor(blob, version, "model.extra.weight", 1 << 31, 1 << 28, 32)
+    assert runtime.artifact_check(bad, 8) is None
+    path = tmp_path / "wrap.leaf"
+    path.write_bytes(bad)
+    with pytest.raises(runtime.LeafError, match="invalid tensor data range model.extra.weight"):
+        runtime.Decoder(path, 8)
+    fine = with_extra_tensor(blob, version, "model.extra.weight", 1, 16, 32, size=64)
+    path.write_bytes(fine)
+    runtime.Decoder(path, 8).close()
+
+
 @pytest.mark.parametrize("family,prompt_tokens", [("gpt2", 150), ("tinyllama", 230), ("qwen", 230),
                                                   ("smollm2", 230), ("gpt2", 20), ("qwen", 20)])
 def test_graph_replayed_decode_is_bit_identical_to_eager(runtime, artifacts, monkeypatch, family, prompt_tokens):

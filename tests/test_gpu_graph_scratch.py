@@ -67,3 +67,53 @@ def test_captured_linear_replays_and_scratch_growth_is_refused_in_capture(rt):
     assert replay_matches(), "replay after the scratch grew differs"
     graph.close()
     stream.close()
+
+
+def test_destroyed_streams_release_their_scratch_and_captured_ones_keep_it(rt):
+    """lh_stream_destroy frees the stream's kernel scratch (a caller that makes
+    a stream per request does not leak device memory), except for a stream
+    that was captured: its graph may still be launched on another stream."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+
+    def free_bytes():
+        free, total = C.c_size_t(), C.c_size_t()
+        assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+        return free.value
+
+    rng = np.random.default_rng(31)
+    K, N, M = 2048, 2048, 64
+    data, scales = quantize((0.02 * rng.standard_normal((N, K))).astype(np.float32), 8, K)
+    dw = rt.DeviceWeight(data, 8, K, scales, K)
+    dx = rt.DeviceArray.of(rng.standard_normal((M, K), dtype=np.float32))
+    dy = rt.DeviceArray((M, N), np.float32)
+    rt.linear(dw, dx, M, 8, dy, stream=None)
+    rt.synchronize()
+    want = dy.numpy()
+
+    streams = 48
+    before = free_bytes()
+    for _ in range(streams):
+        s = rt.Stream()
+        rt.linear(dw, dx, M, 8, dy, stream=s.handle)   # at least 1 MiB of scratch for this stream
+        s.close()
+    dropped = before - free_bytes()
+    print(f"device memory after {streams} streams: {dropped / 2**20:.1f} MiB less free")
+    assert dropped < 16 << 20, f"{streams} destroyed streams kept {dropped} bytes"
+    assert np.array_equal(dy.numpy().view(np.uint32), want.view(np.uint32))
+
+    captured = rt.Stream()
+    rt.linear(dw, dx, M, 8, dy, stream=captured.handle)
+    captured.synchronize()
+    graph = rt.Graph(captured, lambda: rt.linear(dw, dx, M, 8, dy, stream=captured.handle))
+    captured.close()
+    other = rt.Stream()
+    for replay in range(3):
+        dy.zero()
+        rt.synchronize()
+        rt.check(rt.library().lh_graph_launch(graph.handle, other.handle))
+        other.synchronize()
+        assert np.array_equal(dy.numpy().view(np.uint32), want.view(np.uint32)), f"replay {replay} differs"
+    graph.close()
+    other.close()
