@@ -291,7 +291,6 @@ __device__ __forceinline__ int run_of(int g, int a) { return g * kAT + a; }
 // 32-bit offset plus a wave-uniform SGPR offset, so a lane's runs need one
 // address register rather than one 64-bit address per word.  Loads use sc1
 // (coherent at agent scope), like the atomic loads of fetch().
-constexpr int kRawBufferWord3 = 0x00020000;   // descriptor word 3 of a raw (untyped) buffer on gfx9
 constexpr int kLoadSc1 = 16;                  // cache-policy bit sc1
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t exchange_view(const u64* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(base), (short)0, 0x7fffffff, kRawBufferWord3);

@@ -20,6 +20,10 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
+// Descriptor word 3 of a raw (untyped) buffer resource on gfx9: loads through
+// it are bounds-checked against the resource's size (reads past it return 0).
+constexpr int kRawBufferWord3 = 0x00020000;
+
 // 128-bit streaming load (non-temporal: weights are read once per forward).
 __device__ __forceinline__ uint4 load_stream16(const void* p) {
     const v4u v = __builtin_nontemporal_load(static_cast<const v4u*>(p));

@@ -157,6 +157,172 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
     }
 }
 
+// The same arithmetic for head dim 64, one block per (query token, KV head)
+// with one wave per query head of the group: the lanes are the keys for the
+// scores (q in scalar registers; the group's K rows of 64 keys staged in LDS
+// once by coalesced loads, then each lane's row read back) and the output
+// elements for p.v, so no lane idles through a dependent sum and many rows
+// share each SIMD.  The denominator is the plain in-order chain, every lane
+// forming it alike.  Blocks run from the last token down: the longest rows
+// start first.
+constexpr int kRoWaveDim = 64;
+constexpr int kRoWaveKeys = 12;    // keys per chunk of the p.v chain (three float4 of p)
+constexpr int kRoWaveDepth = 4;    // chunks of V in flight
+constexpr int kRoKPitch = kRoWaveDim + 4;   // floats per staged K row: lanes' 16-byte reads meet distinct banks
+constexpr int kRoMaxGroup = 16;    // query heads per KV head (waves per block)
+// Floats of a row's scores: its keys rounded up to whole groups of chunks,
+// plus the chunk the chain reads ahead.
+__host__ __device__ constexpr int ro_wave_row_floats(int keys) {
+    return (keys + kRoWaveKeys * kRoWaveDepth - 1) / (kRoWaveKeys * kRoWaveDepth) * (kRoWaveKeys * kRoWaveDepth) +
+           kRoWaveKeys * kRoWaveDepth + kRoWaveKeys;
+}
+__global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(AttentionCall p, int row_floats) {
+    extern __shared__ float lds[];
+    constexpr int dim = kRoWaveDim;
+    constexpr int kRowBytes = dim * (int)sizeof(float);
+    const int group = p.heads / p.kv_heads;
+    const int lane = threadIdx.x & (kWave - 1), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = p.tokens - 1 - (int)blockIdx.x / p.kv_heads, kvh = (int)blockIdx.x % p.kv_heads;
+    const int h = kvh * group + w;
+    const int position = p.position_ptr ? *p.position_ptr : p.position;
+    const int end = position + t + 1;
+    const int begin = (p.window && end > p.window) ? end - p.window : 0;
+    const int n = end - begin;
+    float* kt = lds;                                       // [kWave][kRoKPitch]: 64 keys' rows
+    float* sc = lds + kWave * kRoKPitch + w * row_floats;  // this head's scores, then exp, then p
+    const float* q = p.q_heads + ((size_t)h * p.tokens + t) * dim;
+    float* K = const_cast<float*>(p.keys) + ((size_t)kvh * p.capacity + begin) * dim;
+    float* V = const_cast<float*>(p.values) + ((size_t)kvh * p.capacity + begin) * dim;
+    // bounds-checked views of the n visible rows: rows past them read as 0
+    const __amdgpu_buffer_rsrc_t kbuf = __builtin_amdgcn_make_buffer_rsrc(K, (short)0, n * kRowBytes, kRawBufferWord3);
+    const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(V, (short)0, n * kRowBytes, kRawBufferWord3);
+    float qs[dim];
+#pragma unroll
+    for (int d = 0; d < dim; ++d) qs[d] = q[d];
+    // scores (s += q[d] * k[d] in column order, then * scale * scale) and
+    // their maximum (NaN scores never become it, as with std::max)
+    float m = -INFINITY;
+    for (int k0 = 0; k0 < n; k0 += kWave) {
+        __syncthreads();   // every wave is done with the previous keys' rows
+        for (int f = threadIdx.x; f < kWave * dim / 4; f += blockDim.x) {
+            const int row = f / (dim / 4), part = f % (dim / 4);
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(kbuf, (k0 + row) * kRowBytes + 16 * part, 0, 0);
+            *reinterpret_cast<v4u*>(kt + row * kRoKPitch + 4 * part) = v;
+        }
+        __syncthreads();
+        v4f kr[dim / 4];
+#pragma unroll
+        for (int j = 0; j < dim / 4; ++j) kr[j] = *reinterpret_cast<const v4f*>(kt + lane * kRoKPitch + 4 * j);
+        float s = 0.0f;
+#pragma unroll
+        for (int d = 0; d < dim; ++d) s = s + qs[d] * kr[d / 4][d % 4];
+        s = s * p.scale * p.scale;
+        const int key = k0 + lane;
+        if (key < n) {
+            sc[key] = s;
+            m = m < s ? s : m;
+        }
+    }
+    // from here on each wave works alone (no block barrier)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float other = __shfl_xor(m, off, kWave);
+        m = m < other ? other : m;
+    }
+    const float maximum = m;
+    float* o = p.out + ((size_t)t * p.heads + h) * dim;
+    if (!isfinite(maximum)) {   // fully masked (or infinite) row: the CPU leaves the zero-filled output
+        o[lane] = 0.0f;
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // exp(s - max) with glibc's expf, eight per lane at a time
+    for (int k0 = 0; k0 < n; k0 += 8 * kWave) {
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = k0 + i * kWave + lane;
+            e[i] = (k < n ? sc[k] : 0.0f) - maximum;
+        }
+        libm_expf_batch(e, [](uint32_t k) { return kExp2Table32[k]; });
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = k0 + i * kWave + lane;
+            if (k < n) sc[k] = e[i];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the denominator in key order, every lane alike
+    float den = 0.0f;
+    {
+        int k = 0;
+        for (; k + 8 <= n; k += 8) {
+            const v4f a = *reinterpret_cast<const v4f*>(sc + k), b = *reinterpret_cast<const v4f*>(sc + k + 4);
+            den = den + a[0];
+            den = den + a[1];
+            den = den + a[2];
+            den = den + a[3];
+            den = den + b[0];
+            den = den + b[1];
+            den = den + b[2];
+            den = den + b[3];
+        }
+        for (; k < n; ++k) den = den + sc[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // p = e / den; the slots past n hold +0, so the chain's reads past the
+    // keys add p * v = +0 * 0, which leaves a sum that started at +0 unchanged
+    const int slots = ro_wave_row_floats(n);
+    for (int k = lane; k < slots; k += kWave) sc[k] = k < n ? sc[k] / den : 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // output[d] += p * v[d] in key order, lane d; kRoWaveDepth chunks of V in
+    // flight, each chunk's p read one chunk ahead
+    const int chunks = (n + kRoWaveKeys - 1) / kRoWaveKeys;
+    const int groups = (chunks + kRoWaveDepth - 1) / kRoWaveDepth;
+    float ring[kRoWaveDepth][kRoWaveKeys];
+    auto load = [&](float (&r)[kRoWaveKeys], int c) {
+        const int at = lane * (int)sizeof(float) + c * kRoWaveKeys * kRowBytes;
+#pragma unroll
+        for (int j = 0; j < kRoWaveKeys; ++j)
+            r[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vbuf, at + j * kRowBytes, 0, 0));
+    };
+    v4f pp[2][kRoWaveKeys / 4];
+    auto read_p = [&](v4f (&pr)[kRoWaveKeys / 4], int c) {
+#pragma unroll
+        for (int j = 0; j < kRoWaveKeys / 4; ++j) pr[j] = *reinterpret_cast<const v4f*>(sc + c * kRoWaveKeys + 4 * j);
+    };
+#pragma unroll
+    for (int u = 0; u < kRoWaveDepth; ++u) load(ring[u], u);
+    read_p(pp[0], 0);
+    float acc = 0.0f;
+    static_assert(kRoWaveDepth % 2 == 0 && kRoWaveKeys == 12, "p pairs alternate; the wait names twelve values");
+    for (int g = 0; g < groups; ++g) {
+#pragma unroll
+        for (int u = 0; u < kRoWaveDepth; ++u) {
+            const int c = g * kRoWaveDepth + u;
+            read_p(pp[(u + 1) & 1], c + 1);
+            float (&r)[kRoWaveKeys] = ring[u];
+            v4f (&pq)[kRoWaveKeys / 4] = pp[u & 1];
+            // one wait for the whole chunk
+            asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
+                              "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(pq[0]), "+v"(pq[1]),
+                              "+v"(pq[2]));
+#pragma unroll
+            for (int j = 0; j < kRoWaveKeys; ++j) acc = acc + pp[u & 1][j / 4][j % 4] * ring[u][j];
+            load(ring[u], c + kRoWaveDepth);
+        }
+    }
+    o[lane] = acc;
+}
+
 // Single-token attention at head dim 64 (decode): the same arithmetic as
 // ro_attention_kernel, arranged so that no dependent sum waits on memory.
 //   * Scores: thread k takes keys k, k + 512, ...; the next key's row loads
@@ -571,7 +737,7 @@ bool allow_lds(K kernel, size_t bytes, int& allowed) {
     allowed = (int)bytes;
     return true;
 }
-int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0;
+int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds = 0;
 
 }  // namespace
 
@@ -596,6 +762,15 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
         if (!allow_lds(ro_attention_decode_kernel, lds, g_attention_decode_lds)) return false;
         ro_attention_decode_kernel<<<p.heads, kRoDecodeBlock, lds, stream>>>(p);
         return true;
+    }
+    const int group = p.heads / p.kv_heads;
+    if (p.dim == kRoWaveDim && group <= kRoMaxGroup) {
+        const int row_floats = ro_wave_row_floats(max_keys);
+        const size_t lds = ((size_t)kWave * kRoKPitch + (size_t)group * row_floats) * sizeof(float);
+        if (allow_lds(ro_attention_wave_kernel, lds, g_attention_wave_lds)) {
+            ro_attention_wave_kernel<<<p.kv_heads * p.tokens, group * kWave, lds, stream>>>(p, row_floats);
+            return true;
+        }
     }
     const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
     if (!allow_lds(ro_attention_kernel, lds, g_attention_lds)) return false;
