@@ -176,6 +176,9 @@ __host__ __device__ constexpr int ro_wave_row_floats(int keys) {
     return (keys + kRoWaveKeys * kRoWaveDepth - 1) / (kRoWaveKeys * kRoWaveDepth) * (kRoWaveKeys * kRoWaveDepth) +
            kRoWaveKeys * kRoWaveDepth + kRoWaveKeys;
 }
+// PER: 16-byte K loads per thread per 64 keys (64 * 16 / blockDim.x, rounded up
+// to a power of two); the next keys' loads are in flight while these are scored.
+template <int PER>
 __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(AttentionCall p, int row_floats) {
     extern __shared__ float lds[];
     constexpr int dim = kRoWaveDim;
@@ -202,14 +205,25 @@ __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(
     // scores (s += q[d] * k[d] in column order, then * scale * scale) and
     // their maximum (NaN scores never become it, as with std::max)
     float m = -INFINITY;
+    v4u pre[PER];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = threadIdx.x + i * (int)blockDim.x;   // past 64 * 16: a row past the keys (reads 0)
+            pre[i] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, (k0 + f / (dim / 4)) * kRowBytes + 16 * (f % (dim / 4)),
+                                                           0, 0);
+        }
+    };
+    fetch(0);
     for (int k0 = 0; k0 < n; k0 += kWave) {
         __syncthreads();   // every wave is done with the previous keys' rows
-        for (int f = threadIdx.x; f < kWave * dim / 4; f += blockDim.x) {
-            const int row = f / (dim / 4), part = f % (dim / 4);
-            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(kbuf, (k0 + row) * kRowBytes + 16 * part, 0, 0);
-            *reinterpret_cast<v4u*>(kt + row * kRoKPitch + 4 * part) = v;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = threadIdx.x + i * (int)blockDim.x;
+            if (f < kWave * dim / 4) *reinterpret_cast<v4u*>(kt + f / (dim / 4) * kRoKPitch + 4 * (f % (dim / 4))) = pre[i];
         }
         __syncthreads();
+        if (k0 + kWave < n) fetch(k0 + kWave);
         v4f kr[dim / 4];
 #pragma unroll
         for (int j = 0; j < dim / 4; ++j) kr[j] = *reinterpret_cast<const v4f*>(kt + lane * kRoKPitch + 4 * j);
@@ -737,7 +751,7 @@ bool allow_lds(K kernel, size_t bytes, int& allowed) {
     allowed = (int)bytes;
     return true;
 }
-int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds = 0;
+int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds[4] = {};
 
 }  // namespace
 
@@ -755,6 +769,17 @@ bool launch_norm_reference_order(const float* x, int rows, int width, const Norm
 // scores; 1 KiB stays for the static arrays.
 int reference_order_attention_keys() { return (160 * 1024 - 1024) / 4 - kRoDecodeDim - kRoChunk * kRoDecodeDim; }
 
+namespace {
+// One block per (query head, query token), any head width.
+bool launch_attention_rows(const AttentionCall& p, int max_keys, hipStream_t stream) {
+    const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
+    if (!allow_lds(ro_attention_kernel, lds, g_attention_lds)) return false;
+    dim3 grid(p.heads, p.tokens);
+    ro_attention_kernel<<<grid, kRoBlock, lds, stream>>>(p);
+    return true;
+}
+}  // namespace
+
 bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipStream_t stream) {
     if (max_keys > reference_order_attention_keys() || p.dim > 256) return false;
     if (p.tokens == 1 && p.dim == kRoDecodeDim) {
@@ -767,16 +792,18 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
     if (p.dim == kRoWaveDim && group <= kRoMaxGroup) {
         const int row_floats = ro_wave_row_floats(max_keys);
         const size_t lds = ((size_t)kWave * kRoKPitch + (size_t)group * row_floats) * sizeof(float);
-        if (allow_lds(ro_attention_wave_kernel, lds, g_attention_wave_lds)) {
-            ro_attention_wave_kernel<<<p.kv_heads * p.tokens, group * kWave, lds, stream>>>(p, row_floats);
+        const int threads = group * kWave, per = (kWave * kRoWaveDim / 4 + threads - 1) / threads;
+        auto run = [&](auto kernel, int& allowed) {
+            if (!allow_lds(kernel, lds, allowed)) return launch_attention_rows(p, max_keys, stream);
+            kernel<<<p.kv_heads * p.tokens, threads, lds, stream>>>(p, row_floats);
             return true;
-        }
+        };
+        if (per <= 2) return run(ro_attention_wave_kernel<2>, g_attention_wave_lds[0]);
+        if (per <= 4) return run(ro_attention_wave_kernel<4>, g_attention_wave_lds[1]);
+        if (per <= 8) return run(ro_attention_wave_kernel<8>, g_attention_wave_lds[2]);
+        return run(ro_attention_wave_kernel<16>, g_attention_wave_lds[3]);
     }
-    const size_t lds = ((size_t)p.dim + max_keys) * sizeof(float);
-    if (!allow_lds(ro_attention_kernel, lds, g_attention_lds)) return false;
-    dim3 grid(p.heads, p.tokens);
-    ro_attention_kernel<<<grid, kRoBlock, lds, stream>>>(p);
-    return true;
+    return launch_attention_rows(p, max_keys, stream);
 }
 
 void launch_activation_reference_order(const float* gate_up, int tokens, int width, int gated, int activation,
