@@ -507,13 +507,18 @@ __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float 
     float sq = 0.0f;
     if constexpr (REF) {
         const SeqLayout lay(n);
+        // A run's two elements are consecutive rows of one column; when E
+        // divides the kRun * kAT elements between a lane's runs, run g sits
+        // kRun * kAT / E columns past run 0.
+        const int at0 = lay.at(kRun * a);
+        const int step = (kRun * kAT) % lay.E == 0 ? kRun * kAT / lay.E : -1;
 #pragma unroll
         for (int g = 0; g < N / kRun; ++g)
             if (g * kAT < live) {
-                const int e = kRun * run_of(g, a);
+                const int at = step >= 0 ? at0 + step * g : lay.at(kRun * run_of(g, a));
                 const float x0 = x[kRun * g] - 0.0f, x1 = x[kRun * g + 1] - 0.0f;
-                s.xf[lay.at(e)] = x0 * x0;
-                s.xf[lay.at(e + 1)] = x1 * x1;
+                s.xf[at] = x0 * x0;
+                s.xf[at + kWave] = x1 * x1;
             }
         seq_zero_tail(s.xf, n, a, kAT);
         if (!a_sync(s, round)) return false;   // both waves' squares are in place
