@@ -1025,31 +1025,24 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     };
     lds_done();
     // exp(s - max) of this lane's keys (lane * E + i, at row i of column lane),
-    // eight at a time, the next eight scores read before these are formed
+    // eight at a time and the last four alone (E is a multiple of 4)
     {
-        float cur[8], nxt[8];
+        auto exps = [&](auto width, int i0) {
+            constexpr int W = decltype(width)::value;
+            float e[W];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cur[i] = pe[min(i, E - 1) * kWave + lane];
-        for (int i0 = 0; i0 < E; i0 += 8) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) nxt[i] = pe[min(i0 + 8 + i, E - 1) * kWave + lane];
-            float e[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = cur[i] - maximum;
+            for (int i = 0; i < W; ++i) e[i] = pe[(i0 + i) * kWave + lane] - maximum;
             libm_expf_batch(e, [exp2](uint32_t k) { return exp2[k]; });
-            // every lane forms all eight (a select per key, no branch around
-            // an evaluation)
-            asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]),
-                              "+v"(e[7]));
+            // every lane forms all of them (a select per key, no branch
+            // around an evaluation)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) cur[i] = i0 + i < valid ? e[i] : 0.0f;
-            // rows past E (at most to row 31: E <= 32, a multiple of 4) take
-            // zeros no sum reads
+            for (int i = 0; i < W; ++i) asm volatile("" : "+v"(e[i]));
 #pragma unroll
-            for (int i = 0; i < 8; ++i) pe[(i0 + i) * kWave + lane] = cur[i];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
-        }
+            for (int i = 0; i < W; ++i) pe[(i0 + i) * kWave + lane] = i0 + i < valid ? e[i] : 0.0f;
+        };
+        int i0 = 0;
+        for (; i0 + 8 <= E; i0 += 8) exps(std::integral_constant<int, 8>(), i0);
+        if (i0 < E) exps(std::integral_constant<int, 4>(), i0);
     }
     lds_done();
     // the first chunks' V columns load while the denominator is formed
