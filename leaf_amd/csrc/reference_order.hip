@@ -672,6 +672,67 @@ __global__ __launch_bounds__(kRoBlock) void ro_gemv_kernel(WeightView w, const f
     }
 }
 
+// One token, FP32 rows whose width is a multiple of 32: ro_gemv_kernel's
+// single-token order with eight lanes per row, eight rows per wave.  Lane j
+// of a row loads columns 32 s + 4 j .. + 3 with one 16-byte load and runs
+// their four chain lanes (lanes 4 (j % 2) .. + 3 of chain j / 2 of the four
+// 8-lane chains a, b, c, d), so a wave's load covers eight whole 128-byte row
+// segments; the chains are then combined, (a + b) + (c + d), and reduced as
+// reduce8 does.
+__global__ __launch_bounds__(kRoBlock) void ro_gemv_f32_rows_kernel(WeightView w, const float* __restrict__ x,
+                                                                    float* y, int epilogue) {
+    const int lane = threadIdx.x & 63, j = lane & 7;
+    const int row = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 3);
+    const bool live = row < w.rows;
+    const int K = w.cols;
+    const v4f* wr = reinterpret_cast<const v4f*>(static_cast<const float*>(w.data) + (size_t)(live ? row : 0) * K) + j;
+    const v4f* xr = reinterpret_cast<const v4f*>(x) + j;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = K / 32;
+    constexpr int kU = 16;  // steps in flight
+    int s = 0;
+    for (; s + kU <= steps; s += kU) {
+        v4f wv[kU], xv[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            wv[u] = __builtin_nontemporal_load(wr + (size_t)(s + u) * 8);
+            xv[u] = xr[(s + u) * 8];
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = fmaf(wv[u][i], xv[u][i], acc[i]);
+    }
+    for (; s < steps; ++s) {
+        const v4f wv = __builtin_nontemporal_load(wr + (size_t)s * 8), xv = xr[s * 8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(wv[i], xv[i], acc[i]);
+    }
+    // lanes j = 0, 1 (chain a) combine chain lane 4 j + i with b, c, d:
+    // (a + b) + (c + d)
+    const int base = lane & ~7;
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float b = __shfl(acc[i], base + (j & 1) + 2, kWave);
+        const float cc = __shfl(acc[i], base + (j & 1) + 4, kWave);
+        const float d = __shfl(acc[i], base + (j & 1) + 6, kWave);
+        c[i] = (acc[i] + b) + (cc + d);
+    }
+    // reduce8 over the combined lanes 0-7 (lane 0 of the row holds 0-3,
+    // lane 1 holds 4-7): (l0 + l4, l1 + l5, l2 + l6, l3 + l7) -> (h0 + h2,
+    // h1 + h3) -> p0 + p1
+    float h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = c[i] + __shfl(c[i], base + 1, kWave);
+    const float partial = (h[0] + h[2]) + (h[1] + h[3]);
+    const float result = fmaf(partial, 1.0f, 0.0f);
+    if (live && j == 0) {
+        const float v = result + (w.bias ? w.bias[row] : 0.0f);
+        y[row] = epilogue == kAccumulate ? y[row] + v : v;
+    }
+}
+
 // Full groups of four tokens (every group but a ragged last one), TG groups
 // per 32-lane worker: lane 8 tt + l runs lane l of token tt's chain in each
 // group, so one load of a weight element serves all 4 TG tokens.  The order
@@ -840,6 +901,13 @@ void launch_ro_linear(const WeightView& w, const float* x, int tokens, float* y,
         ro_gemm_kernel<BITS, TG><<<grid, kRoBlock, 0, stream>>>(w, x, batched, y, epilogue);
     }
     const int rest = tokens - 4 * batched;
+    if constexpr (BITS == 32) {
+        if (tokens == 1 && w.cols % 32 == 0) {
+            const int grid = (int)(((size_t)w.rows * 8 + kRoBlock - 1) / kRoBlock);
+            ro_gemv_f32_rows_kernel<<<grid, kRoBlock, 0, stream>>>(w, x, y, epilogue);
+            return;
+        }
+    }
     if (rest > 0) {
         const size_t workers = (size_t)w.rows * ((rest + 3) / 4);
         const int grid = (int)((workers * 32 + kRoBlock - 1) / kRoBlock);
