@@ -959,18 +959,42 @@ __device__ __forceinline__ void ref_score_item(const StepParams& P, Shared& s, i
     float sum[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) sum[h] = 0.0f;
+    if constexpr (HPW <= 2) {
+        // the next step's reads in flight while one is summed
+        v4f kc, qc[HPW], kn, qn[HPW];
+        auto read = [&](int d4, v4f& k, v4f (&q)[HPW]) {
+            k = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
+#pragma unroll
+            for (int h = 0; h < HPW; ++h)
+                q[h] = *reinterpret_cast<const v4f*>(s.q + min(h0 + aw + kA * h, h_end - 1) * dim + 4 * d4);
+        };
+        read(0, kc, qc);
+#pragma unroll 2
+        for (int d4 = 0; d4 < dim / 4; ++d4) {
+            read(min(d4 + 1, dim / 4 - 1), kn, qn);   // the last step reads its own again
+            all_loaded(kc, qc);
+#pragma unroll
+            for (int h = 0; h < HPW; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum[h] = sum[h] + qc[h][j] * kc[j];
+            kc = kn;
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) qc[h] = qn[h];
+        }
+    } else {
 #pragma unroll(8 / HPW)
-    for (int d4 = 0; d4 < dim / 4; ++d4) {
-        const v4f kv = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
-        v4f qv[HPW];
+        for (int d4 = 0; d4 < dim / 4; ++d4) {
+            const v4f kv = *reinterpret_cast<const v4f*>(s.k + lane * kKStride + 4 * d4);
+            v4f qv[HPW];
 #pragma unroll
-        for (int h = 0; h < HPW; ++h)
-            qv[h] = *reinterpret_cast<const v4f*>(s.q + min(h0 + aw + kA * h, h_end - 1) * dim + 4 * d4);
-        all_loaded(kv, qv);
+            for (int h = 0; h < HPW; ++h)
+                qv[h] = *reinterpret_cast<const v4f*>(s.q + min(h0 + aw + kA * h, h_end - 1) * dim + 4 * d4);
+            all_loaded(kv, qv);
 #pragma unroll
-        for (int h = 0; h < HPW; ++h)
+            for (int h = 0; h < HPW; ++h)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sum[h] = sum[h] + qv[h][j] * kv[j];
+                for (int j = 0; j < 4; ++j) sum[h] = sum[h] + qv[h][j] * kv[j];
+        }
     }
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
