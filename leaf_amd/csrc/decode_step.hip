@@ -1010,27 +1010,33 @@ __device__ __forceinline__ void ref_score_item(const StepParams& P, Shared& s, i
     }
 }
 
-// Reference order, the rest of one query head's attention in one wave
-// (attention_impl, transformer.cpp:122-143): the scores of its n visible keys
-// (pe, in wave_sequential_sum's layout) -> the maximum (NaN scores never
-// become it, as with std::max) -> exp(s - max) with glibc's expf -> the
-// denominator summed in key order (wave_sequential_sum) -> p = e / denominator
-// -> output[d] += p * v[d] in key order, lane d.  Lane d loads column d of
-// the cached V rows itself (one coalesced 256-byte row per load), kChainDepth
-// chunks of kChainKeys keys in flight; the new key's row comes from the
-// exchange words of q|k|v.  A fully masked or infinite row leaves the zero
-// output, like the CPU.  Returns false (abort raised) when a wait failed; o is
-// this lane's output element.
+// Reference order, the rest of one query head's attention (attention_impl,
+// transformer.cpp:122-143), by both exchange waves of its merge block (h: this
+// wave): the scores of its n visible keys (pe[0], in the column-order sum's
+// layout; m: this wave's maximum of those it gathered) -> the maximum (NaN
+// scores never become it, as with std::max) -> exp(s - max) with glibc's
+// expf, row blocks split between the waves -> the denominator summed in key
+// order by the pair (wave_pair_sequential_sum) -> p = e / denominator, row
+// groups split -> output[d] += p * v[d] in key order, lane d of wave 0.  Lane
+// d loads column d of the cached V rows itself (one coalesced 256-byte row
+// per load), kChainDepth chunks of kChainKeys keys in flight; the new key's
+// row comes from the exchange words of q|k|v.  A fully masked or infinite row
+// leaves the zero output, like the CPU.  Returns false (abort raised) when a
+// wait failed; o is lane d's output element in wave 0.
 constexpr int kChainKeys = 12;                                      // keys per chunk: three float4 of p
 constexpr int kChainDepth = 4;                                      // chunks in flight (48 loads)
-__device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float* pnat, float4* area,
-                                          const uint64_t* exp2, int n, float m, const float* V,
-                                          const u64* vnew_word, unsigned vnew_epoch, int lane, float& o) {
+__device__ __forceinline__ bool ref_merge(const StepParams& P, SharedRef& r, int& round, int h, int n, float m,
+                                          const float* V, const u64* vnew_word, unsigned vnew_epoch, int lane,
+                                          float& o) {
     constexpr int dim = kStepDim;
     constexpr int kRowBytes = dim * (int)sizeof(float);
     o = 0.0f;
-    const float maximum = dpp_max_f32(m);
+    float maximum = m;
+    if (!a_max(maximum, r, round)) return false;
     if (!isfinite(maximum)) return true;
+    float* pe = r.pe[0];
+    float* pnat = r.v;   // p in key order
+    const uint64_t* exp2 = r.exp2;
     const int E = seq_per_lane(n);
     const int valid = min(max(n - lane * E, 0), E);
     const int cached = n - 1;   // the new key is the last visible one
@@ -1041,15 +1047,15 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(V), (short)0, cached * kRowBytes, kRawBufferWord3);
     float ring[kChainDepth][kChainKeys];
-    auto load = [&](float (&r)[kChainKeys], int c) {
+    auto load = [&](float (&rr)[kChainKeys], int c) {
         const int at = lane * (int)sizeof(float) + c * kChainKeys * kRowBytes;
 #pragma unroll
         for (int j = 0; j < kChainKeys; ++j)
-            r[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vbuf, at + j * kRowBytes, 0, 0));
+            rr[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vbuf, at + j * kRowBytes, 0, 0));
     };
-    lds_done();
-    // exp(s - max) of this lane's keys (lane * E + i, at row i of column lane),
-    // eight at a time and the last four alone (E is a multiple of 4)
+    // exp(s - max) of this lane's keys (lane * E + i, at row i of column
+    // lane): blocks of eight rows, the last one four (E is a multiple of 4),
+    // alternating between the waves
     {
         auto exps = [&](auto width, int i0) {
             constexpr int W = decltype(width)::value;
@@ -1064,27 +1070,35 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
 #pragma unroll
             for (int i = 0; i < W; ++i) pe[(i0 + i) * kWave + lane] = i0 + i < valid ? e[i] : 0.0f;
         };
-        int i0 = 0;
-        for (; i0 + 8 <= E; i0 += 8) exps(std::integral_constant<int, 8>(), i0);
+        int i0 = 8 * h;
+        for (; i0 + 8 <= E; i0 += 16) exps(std::integral_constant<int, 8>(), i0);
         if (i0 < E) exps(std::integral_constant<int, 4>(), i0);
     }
-    lds_done();
-    // the first chunks' V columns load while the denominator is formed
+    if (!a_sync(r, round)) return false;
+    // wave 0: the first chunks' V columns load while the denominator is formed
+    if (h == 0) {
 #pragma unroll
-    for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
-    const float den = wave_sequential_sum(pe, n, area);   // the padding rows hold +0
-    // p = e / den in key order (pnat), read four keys at a time below; the
-    // padding rows (e = +0) give p = +0 for keys [n, 64 E), and the keys the
-    // last group runs past that (fewer than kChainDepth * kChainKeys) +0 too
-    for (int i0 = 0; i0 < E; i0 += 4) {
+        for (int u = 0; u < kChainDepth; ++u) load(ring[u], u);
+    }
+    float den;
+    float4* xchg = reinterpret_cast<float4*>(&r.pe[1][0]);   // the pair's trade and compaction space
+    if (!wave_pair_sequential_sum(pe, n, r.area[0], r.area[1], xchg, xchg + kSeqPairXchg + h * kSeqPairComp, h,
+                                  [&] { return a_sync(r, round); }, den))
+        return false;
+    // p = e / den in key order (pnat), groups of four rows alternating between
+    // the waves; the padding rows (e = +0) give p = +0 for keys [n, 64 E), and
+    // the keys the last group of the chain runs past that (fewer than
+    // kChainDepth * kChainKeys) +0 too
+    for (int i0 = 4 * h; i0 < E; i0 += 8) {
         float e[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = pe[(i0 + i) * kWave + lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) pnat[lane * E + i0 + i] = e[i] / den;
     }
-    if (kWave * E + lane < kRefMaxKeys) pnat[kWave * E + lane] = 0.0f;
-    lds_done();
+    if (h == 0 && kWave * E + lane < kRefMaxKeys) pnat[kWave * E + lane] = 0.0f;
+    if (!a_sync(r, round)) return false;
+    if (h != 0) return true;
     // Whole groups of kChainDepth chunks, one straight-line body per group:
     // a chunk's loads are replaced by those kChainDepth chunks on as soon as
     // it is added, and its p come from LDS one chunk ahead.  Keys from the
@@ -1094,10 +1108,10 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
     static_assert(kChainDepth % 2 == 0 && kChainKeys % 4 == 0, "p pairs alternate; p loads are float4");
     static_assert(kChainDepth * kChainKeys <= kWave, "the zeroed p past 64 E cover the last group");
     v4f pp[2][kChainKeys / 4];
-    auto read_p = [&](v4f (&p)[kChainKeys / 4], int c) {
+    auto read_p = [&](v4f (&pr)[kChainKeys / 4], int c) {
         const float* at = pnat + c * kChainKeys;   // < kRefMaxKeys: n <= kRefStepKeys
 #pragma unroll
-        for (int j = 0; j < kChainKeys / 4; ++j) p[j] = *reinterpret_cast<const v4f*>(at + 4 * j);
+        for (int j = 0; j < kChainKeys / 4; ++j) pr[j] = *reinterpret_cast<const v4f*>(at + 4 * j);
     };
     read_p(pp[0], 0);
     for (int g = 0; g < groups; ++g) {
@@ -1108,11 +1122,11 @@ __device__ __forceinline__ bool ref_chain(const StepParams& P, float* pe, float*
             // one wait for the whole chunk: every product below reads the
             // values through this statement, which needs all of them loaded
             static_assert(kChainKeys == 12, "the statement names twelve values");
-            float (&r)[kChainKeys] = ring[u];
+            float (&rr)[kChainKeys] = ring[u];
             v4f (&q)[kChainKeys / 4] = pp[u & 1];
-            asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
-                              "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(q[0]), "+v"(q[1]),
-                              "+v"(q[2]));
+            asm volatile("" : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]), "+v"(rr[5]),
+                              "+v"(rr[6]), "+v"(rr[7]), "+v"(rr[8]), "+v"(rr[9]), "+v"(rr[10]), "+v"(rr[11]),
+                              "+v"(q[0]), "+v"(q[1]), "+v"(q[2]));
 #pragma unroll
             for (int j = 0; j < kChainKeys; ++j) o = o + pp[u & 1][j / 4][j % 4] * ring[u][j];
             load(ring[u], c + kChainDepth);
@@ -1249,6 +1263,21 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
     // merge blocks: the last ceil(heads / kA) blocks, one query head per wave
     // (local mode: the last `per` blocks of each XCD, one head slice each)
     const bool merge_block = local ? merge_sigma >= 0 : (G - 1 - b) * kA < P.heads;
+    // reference order: the last `heads` blocks merge one query head each, with
+    // both exchange waves (local mode: the last per * kA blocks of each XCD,
+    // one head of the XCD's slices each)
+    int ref_mh = -1;
+    if (REF) {
+        if (local) {
+            const int idx = G / 8 - 1 - (b >> 3);
+            if (idx >= 0 && idx < per * kA) {
+                const int sl = (b & 7) + 8 * (idx / kA), hs = idx % kA;
+                if (sl % slices * kA + hs < group) ref_mh = sl / slices * group + sl % slices * kA + hs;
+            }
+        } else if (G - 1 - b < P.heads) {
+            ref_mh = G - 1 - b;
+        }
+    }
     u64* const part_base = local ? P.x_part_local : P.x_part;
 
     float x[kNH];
@@ -1410,43 +1439,39 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
             stamp(P.trace, b, 64 * L + 57);
         }
-        if (merge_block && REF) {
-            // reference order: this wave's query head mh, all of it (ref_chain)
+        if (REF && ref_mh >= 0) {
+            // reference order: both exchange waves on query head ref_mh
             bool ok = true;
-            const int mh = local ? merge_sigma / slices * group + merge_sigma % slices * kA + aw : (G - 1 - b) * kA + aw;
-            const bool mine = local ? merge_sigma % slices * kA + aw < group : mh < P.heads;
-            if (mine) {
-                const int g = mh / group, gh = mh % group;
-                const size_t stride = (size_t)group * (dim + 2);
-                const u64* base = part_base + ((size_t)g * spans * group + gh) * (dim + 2);
-                float* pe = static_cast<SharedRef&>(s).pe[aw];
-                const int n = end - begin;
-                float m = -INFINITY;
-                v2f ml;
-                float os[kMergeBatch];
-                const SeqLayout lay(n);
-                for (int s0 = 0; s0 < spans && ok; s0 += kMergeBatch) {
-                    ok = await_partials(base, (int)stride, spans, s0, lane, epoch(L, 2), ml, os, P);
+            const int g = ref_mh / group, gh = ref_mh % group;
+            const size_t stride = (size_t)group * (dim + 2);
+            const u64* base = part_base + ((size_t)g * spans * group + gh) * (dim + 2);
+            SharedRef& r = static_cast<SharedRef&>(s);
+            float* pe = r.pe[0];
+            const int n = end - begin;
+            float m = -INFINITY;
+            v2f ml;
+            float os[kMergeBatch];
+            const SeqLayout lay(n);
+            // the waves gather alternate batches of spans
+            for (int s0 = aw * kMergeBatch; s0 < spans && ok; s0 += kA * kMergeBatch) {
+                ok = await_partials(base, (int)stride, spans, s0, lane, epoch(L, 2), ml, os, P);
 #pragma unroll
-                    for (int j = 0; j < kMergeBatch; ++j) {
-                        const int k = (s0 + j) * kStepSpanKeys + lane;
-                        if (ok && k < n) {
-                            pe[lay.at(k)] = os[j];
-                            m = m < os[j] ? os[j] : m;
-                        }
+                for (int j = 0; j < kMergeBatch; ++j) {
+                    const int k = (s0 + j) * kStepSpanKeys + lane;
+                    if (ok && k < n) {
+                        pe[lay.at(k)] = os[j];
+                        m = m < os[j] ? os[j] : m;
                     }
                 }
-                float o = 0.0f;
-                if (ok)
-                    ok = ref_chain(P, pe, s.v + aw * kRefMaxKeys, static_cast<SharedRef&>(s).area[aw],
-                                   static_cast<SharedRef&>(s).exp2, n, m,
-                                   Vc + ((size_t)g * P.capacity + begin) * dim,
-                                   P.x_qkv + qw + kvw + g * dim + lane, epoch(L, 1), lane, o);
-                if (ok) publish(P.x_attn + mh * dim + lane, epoch(L, 3), o);
             }
             if (!a_check(ok, s, P)) return false;
+            float o = 0.0f;
+            ok = ref_merge(P, r, round, aw, n, m, Vc + ((size_t)g * P.capacity + begin) * dim,
+                           P.x_qkv + qw + kvw + g * dim + lane, epoch(L, 1), lane, o);
+            if (ok && aw == 0) publish(P.x_attn + ref_mh * dim + lane, epoch(L, 3), o);
+            if (!a_check(ok, s, P)) return false;
             stamp(P.trace, b, 64 * L + 60);
-        } else if (merge_block) {
+        } else if (!REF && merge_block) {
             // this wave's query head mh: combine its spans (lane s holds span
             // s's max and sum; lane d accumulates output element d)
             bool ok = true;
