@@ -1101,34 +1101,35 @@ __device__ __forceinline__ bool ref_merge(const StepParams& P, SharedRef& r, int
     if (h != 0) return true;
     // Whole groups of kChainDepth chunks, one straight-line body per group:
     // a chunk's loads are replaced by those kChainDepth chunks on as soon as
-    // it is added, and its p come from LDS one chunk ahead.  Keys from the
+    // it is added, and its p come from LDS two chunks ahead.  Keys from the
     // new one on add p * (+0) with p finite: their rows lie past the buffer
     // view's cached rows and read as 0, which leaves the sum unchanged (it
     // starts at +0 and is never -0).
-    static_assert(kChainDepth % 2 == 0 && kChainKeys % 4 == 0, "p pairs alternate; p loads are float4");
-    static_assert(kChainDepth * kChainKeys <= kWave, "the zeroed p past 64 E cover the last group");
-    v4f pp[2][kChainKeys / 4];
+    static_assert(kChainKeys % 4 == 0, "p loads are float4");
+    static_assert((kChainDepth + 1) * kChainKeys <= kWave, "the zeroed p past 64 E cover what the last group reads");
+    v4f pp[kChainDepth][kChainKeys / 4];
     auto read_p = [&](v4f (&pr)[kChainKeys / 4], int c) {
         const float* at = pnat + c * kChainKeys;   // < kRefMaxKeys: n <= kRefStepKeys
 #pragma unroll
         for (int j = 0; j < kChainKeys / 4; ++j) pr[j] = *reinterpret_cast<const v4f*>(at + 4 * j);
     };
     read_p(pp[0], 0);
+    read_p(pp[1], 1);
     for (int g = 0; g < groups; ++g) {
 #pragma unroll
         for (int u = 0; u < kChainDepth; ++u) {
             const int c = g * kChainDepth + u;
-            read_p(pp[(u + 1) & 1], c + 1);
+            read_p(pp[(u + 2) % kChainDepth], c + 2);
             // one wait for the whole chunk: every product below reads the
             // values through this statement, which needs all of them loaded
             static_assert(kChainKeys == 12, "the statement names twelve values");
             float (&rr)[kChainKeys] = ring[u];
-            v4f (&q)[kChainKeys / 4] = pp[u & 1];
+            v4f (&q)[kChainKeys / 4] = pp[u];
             asm volatile("" : "+v"(rr[0]), "+v"(rr[1]), "+v"(rr[2]), "+v"(rr[3]), "+v"(rr[4]), "+v"(rr[5]),
                               "+v"(rr[6]), "+v"(rr[7]), "+v"(rr[8]), "+v"(rr[9]), "+v"(rr[10]), "+v"(rr[11]),
                               "+v"(q[0]), "+v"(q[1]), "+v"(q[2]));
 #pragma unroll
-            for (int j = 0; j < kChainKeys; ++j) o = o + pp[u & 1][j / 4][j % 4] * ring[u][j];
+            for (int j = 0; j < kChainKeys; ++j) o = o + pp[u][j / 4][j % 4] * ring[u][j];
             load(ring[u], c + kChainDepth);
         }
     }
