@@ -108,6 +108,9 @@ struct __align__(16) Shared {
     int abort;
 };
 
+// Where element e of a staged product vector (SharedRef::xg) sits.
+__device__ __forceinline__ int xg_at(int e) { return e + 4 * (e >> 4); }
+
 // Reference order adds each chain wave's softmax terms of one query head
 // (scores, then exp(score - max), then the probabilities) in the transposed
 // layout of wave_sequential_sum, and per exchange wave the scratch of that
@@ -122,6 +125,16 @@ struct __align__(16) SharedRef : Shared {
     float pe[kA][kRefMaxKeys];
     float4 area[kA][kSeqSumArea];
     uint64_t exp2[32];   // expf's table (libm_expf.h), read per lane
+    // The RMSNorms before q|k|v and gate|up (wave_speculate, wave_confirm):
+    // the products x * gamma (element e at xg_at(e): 16-element chunks 20
+    // floats apart, so a lane's 16-byte reads of its chunks meet no bank
+    // conflict), the gamma of the norm before gate|up (natural element order;
+    // the input norm's waits in gamma_in), the column-order square sums, and
+    // the last phase whose vectors each exchange wave has stored.
+    float xg[kStepMaxHidden / 16 * 20];
+    float gamma_mid[kNH * kAT];
+    float sq[2];
+    int staged[kA];
     // pe and area, both free then, stage the gated activation while its
     // maximum is traded (quantize_into)
     __device__ float* stage() { return &pe[0][0]; }
@@ -493,49 +506,77 @@ __device__ __forceinline__ void post(Shared& s, int phase) {
     if ((threadIdx.x & 63) == 0) lds_store(&s.ready[threadIdx.x >> 6], phase);
 }
 
+// Reference order: stores this exchange wave's runs of x * gamma (the
+// products the weight waves quantize speculatively, wave_speculate) and notes
+// that its part of the vector that phase `phase` normalizes, and of its
+// gamma, is in LDS; the exchange waves then form the column-order square sum.
+template <int N>
+__device__ __forceinline__ void stage_products(SharedRef& r, const float (&x)[N], const float (&gamma)[N], int a,
+                                               int phase) {
+    static_assert(N % kRun == 0 && kRun == 2, "runs of two");
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g) {
+        const int e = kRun * run_of(g, a);   // even: both elements of a run share a 16-element chunk
+        *reinterpret_cast<v2f*>(r.xg + xg_at(e)) = v2f{x[kRun * g] * gamma[kRun * g], x[kRun * g + 1] * gamma[kRun * g + 1]};
+    }
+    lds_done();
+    if ((threadIdx.x & 63) == 0) lds_store(&r.staged[threadIdx.x >> 6], phase);
+}
+
+// RMSNorm scale of a square sum, norm()'s expression (decoder.cpp:719-721).
+__device__ __forceinline__ float rms_scale(float sq, int n, float eps) { return 1.0f / sqrtf(sq / (float)n + eps); }
+
+// The squares of the n values held as runs, summed in column order as
+// norm() sums them (decoder.cpp:716-718): every lane stores its runs' squares
+// (s.xf is free until the head) in the layout of wave_sequential_sum, and the
+// two exchange waves form the column-order sum together
+// (wave_pair_sequential_sum: each steps half of every chunk, one trade
+// between them); both get the same bits.
+template <int N>
+__device__ __forceinline__ bool ref_square_sum(const float (&x)[N], int n, int a, Shared& s, int& round, float& sq) {
+    const int live = n / kRun - a;
+    const SeqLayout lay(n);
+    // A run's two elements are consecutive rows of one column; when E
+    // divides the kRun * kAT elements between a lane's runs, run g sits
+    // kRun * kAT / E columns past run 0.
+    const int at0 = lay.at(kRun * a);
+    const int step = (kRun * kAT) % lay.E == 0 ? kRun * kAT / lay.E : -1;
+#pragma unroll
+    for (int g = 0; g < N / kRun; ++g)
+        if (g * kAT < live) {
+            const int at = step >= 0 ? at0 + step * g : lay.at(kRun * run_of(g, a));
+            const float x0 = x[kRun * g] - 0.0f, x1 = x[kRun * g + 1] - 0.0f;
+            s.xf[at] = x0 * x0;
+            s.xf[at + kWave] = x1 * x1;
+        }
+    seq_zero_tail(s.xf, n, a, kAT);
+    if (!a_sync(s, round)) return false;   // both waves' squares are in place
+    // each exchange wave steps half of every lane's chunk
+    SharedRef& r = static_cast<SharedRef&>(s);
+    const int w = __builtin_amdgcn_readfirstlane(a >> 6);
+    return wave_pair_sequential_sum(s.xf, n, r.area[0], r.area[1], r.seq_xchg(), r.seq_comp(w), w,
+                                    [&] { return a_sync(s, round); }, sq);
+}
+
 // RMSNorm of the n values held as runs (decoder.cpp:706-727).  In reference
-// order the squares are summed in column order, as norm() sums them: every
-// lane stores its runs' squares (s.xf is free until the head) in the layout
-// of wave_sequential_sum, and the two exchange waves form the column-order
-// sum together (wave_pair_sequential_sum: each steps half of every chunk, one
-// trade between them); the normalized value is (x - 0) * scale * gamma + 0,
-// norm()'s expression with mean 0 and no beta.
+// order the squares are summed in column order (ref_square_sum) and the
+// normalized value is (x - 0) * scale * gamma + 0, norm()'s expression with
+// mean 0 and no beta.
 template <bool REF, int N>
 __device__ __forceinline__ bool rms_normalize(float (&x)[N], int n, const float (&gamma)[N], float eps, int a,
                                               Shared& s, int& round) {
     const int live = n / kRun - a;
     float sq = 0.0f;
     if constexpr (REF) {
-        const SeqLayout lay(n);
-        // A run's two elements are consecutive rows of one column; when E
-        // divides the kRun * kAT elements between a lane's runs, run g sits
-        // kRun * kAT / E columns past run 0.
-        const int at0 = lay.at(kRun * a);
-        const int step = (kRun * kAT) % lay.E == 0 ? kRun * kAT / lay.E : -1;
-#pragma unroll
-        for (int g = 0; g < N / kRun; ++g)
-            if (g * kAT < live) {
-                const int at = step >= 0 ? at0 + step * g : lay.at(kRun * run_of(g, a));
-                const float x0 = x[kRun * g] - 0.0f, x1 = x[kRun * g + 1] - 0.0f;
-                s.xf[at] = x0 * x0;
-                s.xf[at + kWave] = x1 * x1;
-            }
-        seq_zero_tail(s.xf, n, a, kAT);
-        if (!a_sync(s, round)) return false;   // both waves' squares are in place
-        // each exchange wave steps half of every lane's chunk
-        SharedRef& r = static_cast<SharedRef&>(s);
-        const int w = __builtin_amdgcn_readfirstlane(a >> 6);
-        if (!wave_pair_sequential_sum(s.xf, n, r.area[0], r.area[1], r.seq_xchg(), r.seq_comp(w), w,
-                                      [&] { return a_sync(s, round); }, sq))
-            return false;
-        const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+        if (!ref_square_sum(x, n, a, s, round, sq)) return false;
+        const float scale = rms_scale(sq, n, eps);
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = (x[i] - 0.0f) * scale * gamma[i] + 0.0f;
     } else {
 #pragma unroll
         for (int i = 0; i < N; ++i) sq += (i / kRun) * kAT < live ? x[i] * x[i] : 0.0f;
         if (!a_sum(sq, s, round)) return false;
-        const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+        const float scale = rms_scale(sq, n, eps);
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = x[i] * scale * gamma[i];
     }
@@ -735,6 +776,174 @@ __device__ __forceinline__ int sum2_transposed(int v0, int v1) {
     g += dpp<kDppXor2>(g);
     g += dpp<kDppXor1>(g);
     return g;
+}
+
+// ---- Reference order: each weight wave quantizes the normalized input itself ---
+// The exchange waves form only the column-order square sum of the RMSNorms
+// before q|k|v and gate|up (ref_square_sum), the one step whose order the
+// result depends on.  Meanwhile every weight wave quantizes the whole vector
+// speculatively itself, lane l taking the 16-element chunks l + 64 j of its
+// dots, and takes its int8 dots with those values; when the exact sum lands
+// it confirms them.  The values (decoder.cpp:706-727, 1028-1043):
+//   y = ((x - 0) * s) * g + 0,   t = y * (1 / max(max|y| / 127, 1e-12)),   q = rint(t) in [-127, 127].
+// The int8 values do not depend on the RMSNorm scale s but through
+// roundings: the speculation quantizes y~ = x * g instead (wave_speculate).
+// Every y is y~ * s up to three roundings and so is max|y| (against max|y~|),
+// so t/t~ lies within 12 units of roundoff (2^-24) of 1: |t| <= 127 moves by
+// less than 1e-4.  An element more than kQuantMargin from a rounding boundary
+// (a half-integer) therefore keeps its int8 value; the few nearer ones are
+// quantized again with the exact scale (wave_confirm), and the exact maximum,
+// which sets the per-token scale, is the largest |y| among the candidates
+// |y~| >= max|y~| * kCandidate (no other element can reach it).  A changed
+// value, two candidates in one lane, a maximum near the 1e-12 floor or a
+// value that is not finite: the wave quantizes again with the exact scale
+// (wave_quantize) and takes its dots again.  (Products x * s below the
+// normal range would void the bound; they can only occur for elements whose
+// t is below 1e-6, as long as no |gamma| exceeds 1e20, which the host checks
+// before it runs this step.)
+constexpr float kQuantMargin = 4e-4f;
+constexpr float kCandidate = 1.0f - 1e-6f;
+
+struct WaveQuant {
+    float multiplier;    // 1 / the speculative per-token scale (wave-uniform)
+    float amax;          // max |y~| over the vector (wave-uniform)
+    float top, second;   // this lane's two largest |y~|
+    int top_e;           // element of `top`
+    unsigned near;       // this lane's elements near a rounding boundary (bit 16 j + i: chunk j, element i)
+    bool odd;            // this lane holds a value that is not finite
+};
+
+// Four staged products of this lane's chunk j, elements 4 q .. 4 q + 3 (zero past the vector).
+__device__ __forceinline__ v4f products4(const float* xg, int n, int lane, int j, int q) {
+    const int c = lane + kWave * j;
+    const bool live = c < n / 16;
+    const v4f v = *reinterpret_cast<const v4f*>(xg + 20 * (live ? c : 0) + 4 * q);
+    return live ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// The speculative int8 values of this lane's chunks (row_part's layout) from
+// the staged products, and what wave_confirm needs.  The products are read
+// twice (for the maximum, then for the quantization) rather than held in
+// registers; the loops stay rolled for the same reason.
+template <int KC>
+__device__ __forceinline__ void wave_speculate(const float* xg, int n, int lane, v4u (&xc)[KC], WaveQuant& st) {
+    float top = 0.0f, second = 0.0f;
+    int top_e = 0;
+    bool odd = false;
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const v4f y = products4(xg, n, lane, j, q);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = fabsf(y[k]);
+                odd |= __builtin_amdgcn_class(y[k], 0x207);   // NaN, infinities
+                const bool first = m > top;
+                second = first ? top : fmaxf(second, m);
+                top_e = first ? 16 * (lane + kWave * j) + 4 * q + k : top_e;
+                top = first ? m : top;
+            }
+        }
+    }
+    const float amax = dpp_max_f32(top);
+    const float multiplier = 1.0f / fmaxf(amax / 127.0f, 1e-12f);
+    unsigned near = 0;
+    v4u words[KC] = {};
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const v4f y = products4(xg, n, lane, j, q);
+            unsigned word = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // quantize_one, with the distance of t from the nearest integer
+                const float t = y[k] * multiplier;
+                const float r = __builtin_rintf(t);
+                word |= (unsigned)((int)fminf(fmaxf(r, -127.0f), 127.0f) & 255) << (8 * k);
+                near |= fabsf(t - r) > 0.5f - kQuantMargin ? 1u << (16 * j + 4 * q + k) : 0u;
+            }
+            words[j] = v4u{words[j][1], words[j][2], words[j][3], word};   // word q ends in slot q
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KC; ++j) xc[j] = words[j];
+    st = WaveQuant{multiplier, amax, top, second, top_e, near, odd};
+}
+
+// Four normalized values of this lane's chunk j, elements 4 q .. 4 q + 3 (zero past the vector).
+__device__ __forceinline__ v4f normalized4(const float* x, const float* gamma, int n, float scale, int lane, int j,
+                                           int q) {
+    const int c = lane + kWave * j;
+    const bool live = c < n / 16;
+    const int at = 16 * (live ? c : 0) + 4 * q;
+    const v4f xv = *reinterpret_cast<const v4f*>(x + at);
+    const v4f gv = *reinterpret_cast<const v4f*>(gamma + at);
+    v4f y;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = live ? (xv[k] - 0.0f) * scale * gv[k] + 0.0f : 0.0f;
+    return y;
+}
+
+// The exact int8 values of this lane's chunks (x and gamma in natural
+// element order, `scale` the RMSNorm scale); returns the per-token scale.
+template <int KC>
+__device__ __forceinline__ float wave_quantize(const float* x, const float* gamma, int n, float scale, int lane,
+                                               v4u (&xc)[KC]) {
+    float top = 0.0f;
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const v4f y = normalized4(x, gamma, n, scale, lane, j, q);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) top = fmaxf(top, fabsf(y[k]));
+        }
+    }
+    const float sx = fmaxf(dpp_max_f32(top) / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+    v4u words[KC] = {};
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const v4f y = normalized4(x, gamma, n, scale, lane, j, q);
+            unsigned word = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) word |= (unsigned)(quantize_one(y[k], multiplier) & 255) << (8 * k);
+            words[j] = v4u{words[j][1], words[j][2], words[j][3], word};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KC; ++j) xc[j] = words[j];
+    return sx;
+}
+
+// Whether the int8 values wave_speculate formed are the ones the exact
+// RMSNorm `scale` gives; sets sx, the vector's exact per-token scale.
+__device__ __forceinline__ bool wave_confirm(const float* x, const float* gamma, const float* xg, float scale,
+                                             const WaveQuant& st, int lane, float& sx) {
+    const float bound = st.amax * kCandidate;
+    const bool candidate = st.top >= bound;
+    bool bad = st.odd || (candidate && st.second >= bound);
+    float ye = 0.0f;
+    if (candidate) {
+        const int e = st.top_e;
+        ye = fabsf((x[e] - 0.0f) * scale * gamma[e] + 0.0f);
+    }
+    const float amax = dpp_max_f32(ye);
+    sx = fmaxf(amax / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+    for (unsigned m = st.near; m != 0; m &= m - 1) {
+        const int i = __builtin_ctz(m);
+        const int e = 16 * (lane + kWave * (i >> 4)) + (i & 15);
+        bad |= quantize_one((x[e] - 0.0f) * scale * gamma[e] + 0.0f, multiplier) !=
+               quantize_one(xg[xg_at(e)], st.multiplier);
+    }
+    // both maxima clear of the 1e-12 floor (NaN fails), the exact one finite
+    const bool range = st.amax / 127.0f > 1e-11f && amax / 127.0f > 1e-11f && amax <= 3.0e38f;
+    return range && __builtin_amdgcn_ballot_w64(bad) == 0;
 }
 
 // ((float)acc * s_x) * s_w + b  (decoder.cpp:568, 1229), separate roundings.
@@ -1215,6 +1424,31 @@ __device__ __forceinline__ void capture_input(const StepParams& P, const Shared&
     }
 }
 
+// Block 0's record of a weight wave's normalized input (reference order):
+// the values from the exact scale, the int8 values its dots used and the
+// per-token scale (CAP only).
+template <bool CAP, int KC>
+__device__ __forceinline__ void capture_wave_input(const StepParams& P, const float* x, const float* gamma, int n,
+                                                   float scale, const v4u (&xc)[KC], float sx, int L, int phase,
+                                                   int lane) {
+    if constexpr (CAP) {
+        if (blockIdx.x != 0) return;
+        const size_t at = ((size_t)L * 4 + phase) * kStepMaxFfn;
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int c = lane + kWave * j;
+            if (c >= n / 16) continue;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int e = 16 * c + i;
+                P.capture.x[at + e] = (x[e] - 0.0f) * scale * gamma[e] + 0.0f;
+                P.capture.q[at + e] = (int8_t)(xc[j][i / 4] >> (8 * (i % 4)));
+            }
+        }
+        if (lane == 0) P.capture.sx[L * 4 + phase] = sx;
+    }
+}
+
 // The exact int32 dot of output row `row` of phase `phase` (CAP only).
 template <bool CAP>
 __device__ __forceinline__ void capture_acc(const StepParams& P, int L, int phase, int row, int acc) {
@@ -1326,8 +1560,18 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
             }
         }
         store_runs(s.h_in, x, a);
-        if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
-        capture_input<CAP>(P, s, x, H, 0, L, 0, a);
+        if constexpr (REF) {
+            // the weight waves normalize and quantize; this is the exact sum for them
+            SharedRef& r = static_cast<SharedRef&>(s);
+            stage_products(r, x, gamma, a, 4 * L + 0);
+            float sq;
+            if (!ref_square_sum(x, H, a, s, round, sq)) return false;
+            if (a == 0) r.sq[0] = sq;
+        } else {
+            if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round))
+                return false;
+            capture_input<CAP>(P, s, x, H, 0, L, 0, a);
+        }
         post(s, 4 * L + 0);
         stamp(P.trace, b, 64 * L + 2);
         if (has_item) {
@@ -1533,8 +1777,18 @@ __device__ __forceinline__ bool exchange_role(const StepParams& P, Shared& s) {
         stamp(P.trace, b, 64 * L + 6);
         stamp(P.trace, b, 64 * L + 59, kWave);
         store_runs(s.h_mid, x, a);
-        if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round)) return false;
-        capture_input<CAP>(P, s, x, H, 0, L, 2, a);
+        if constexpr (REF) {
+            SharedRef& r = static_cast<SharedRef&>(s);
+            store_runs(r.gamma_mid, gamma, a);
+            stage_products(r, x, gamma, a, 4 * L + 2);
+            float sq;
+            if (!ref_square_sum(x, H, a, s, round, sq)) return false;
+            if (a == 0) r.sq[1] = sq;
+        } else {
+            if (!rms_normalize<REF>(x, H, gamma, P.epsilon, a, s, round) || !quantize_into(x, H, 0, a, s, round))
+                return false;
+            capture_input<CAP>(P, s, x, H, 0, L, 2, a);
+        }
         post(s, 4 * L + 2);
         // ---- SiLU-gated activation -> int8 for down_proj
         {
@@ -1695,21 +1949,65 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
     load_o(layer_at(s, 0), true);
     load_gate_up(layer_at(s, 0), true);
 
+    // Reference order, a normalized phase (the input of q|k|v or gate|up, in
+    // LDS at x with its gamma): this wave's own quantization of it, and its
+    // dots (`dots(xc)`) taken on the speculative values, again only when the
+    // exact sum (sq[slot]) rejects them.  Sets sx, the per-token scale.
+    auto ref_quantize = [&](const float* x, const float* gamma, int phase, int slot, int L, float& sx,
+                            auto&& dots) {
+        SharedRef& r = static_cast<SharedRef&>(s);
+        if (!wait_flags(s, r.staged, phase)) return false;
+        // a fresh copy of the lane index keeps the per-lane LDS addresses
+        // here instead of hoisted into registers across the layer loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        v4u xc[kKCH];
+        WaveQuant st;
+        wave_speculate<kKCH>(r.xg, H, ln, xc, st);
+        dots(xc);
+        if (!wait_ready(s, phase)) return false;
+        stamp(P.trace, b, 64 * L + 8 + 2 * (phase % 4) + 8 * bw, kAT + kWave * bw);
+        asm volatile("" : "+v"(ln));
+        const float scale = rms_scale(r.sq[slot], H, P.epsilon);
+        if (!wave_confirm(x, gamma, r.xg, scale, st, ln, sx)) {
+            sx = wave_quantize<kKCH>(x, gamma, H, scale, ln, xc);
+            dots(xc);
+        }
+        if (bw == 0) capture_wave_input<CAP>(P, x, gamma, H, scale, xc, sx, L, phase % 4, ln);
+        return true;
+    };
+
     for (int L = 0; L < P.layers; ++L) {
         float* Kc = P.kv + (size_t)L * 2 * P.kv_heads * P.capacity * dim;
         float* Vc = Kc + (size_t)P.kv_heads * P.capacity * dim;
         const bool more = L + 1 < P.layers;
         const StepLayer& next = layer_at(s, more ? L + 1 : L);
         // ---- q|k|v, RoPE, KV append
-        if (!wait_ready(s, 4 * L + 0)) return false;
-        stamp(P.trace, b, 64 * L + 8 + 8 * bw, kAT + kWave * bw);
         {
-            const float sx = s.sx[0];
+            float sx;
+            int tot[kQP][2];
+            if constexpr (REF) {
+                auto dots = [&](const v4u (&xc)[kKCH]) {
+#pragma unroll
+                    for (int k = 0; k < kQP; ++k)
+#pragma unroll
+                        for (int r = 0; r < 2; ++r)
+                            tot[k][r] = has_q[k] ? dpp_sum_i32(row_part(w.q[k][r], xc, H / 16, lane)) : 0;
+                };
+                if (!ref_quantize(s.h_in, s.gamma_in, 4 * L + 0, 0, L, sx, dots)) return false;
+            } else {
+                if (!wait_ready(s, 4 * L + 0)) return false;
+                stamp(P.trace, b, 64 * L + 8 + 8 * bw, kAT + kWave * bw);
+                sx = s.sx[0];
+#pragma unroll
+                for (int k = 0; k < kQP; ++k)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) tot[k][r] = has_q[k] ? row_dot(w.q[k][r], s.xq[0], H / 16, lane) : 0;
+            }
 #pragma unroll
             for (int k = 0; k < kQP; ++k)
                 if (has_q[k]) {
-                    const int a0 = row_dot(w.q[k][0], s.xq[0], H / 16, lane);
-                    const int a1 = row_dot(w.q[k][1], s.xq[0], H / 16, lane);
+                    const int a0 = tot[k][0], a1 = tot[k][1];
                     if (lane == 0) {
                         const int r0 = qr[k][0], r1 = qr[k][1];
                         capture_acc<CAP>(P, L, 0, r0, a0);
@@ -1777,26 +2075,36 @@ __device__ __forceinline__ bool weight_role(const StepParams& P, Shared& s) {
         // 635 us per token with them here)
         load_down(layer_at(s, L), true);
         // ---- gate|up + SiLU gate
-        if (!wait_ready(s, 4 * L + 2)) return false;
-        stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
         {
             // Eight row dots against one read of the input, one transposed
             // reduction, then every pair's epilogue at once: lane 8 k (k < 4)
             // combines pair k's gate with its up (brought over from lane 8 k + 32).
             // Pairs this wave does not own are skipped (a wave-uniform test).
-            const float sx = s.sx[0];
             const int chunks = H / 16;
-            v4u xc[kKCH];
+            int total;
+            auto dots = [&](const v4u (&xc)[kKCH]) {
+                int part[2 * kGP];
 #pragma unroll
-            for (int j = 0; j < kKCH; ++j)
-                xc[j] = *reinterpret_cast<const v4u*>(s.xq[0] + 16 * min(lane + kWave * j, chunks - 1));
-            int part[2 * kGP];
+                for (int k = 0; k < kGP; ++k) {
+                    part[k] = has_g[k] ? row_part(w.g[k][0], xc, chunks, lane) : 0;
+                    part[kGP + k] = has_g[k] ? row_part(w.g[k][1], xc, chunks, lane) : 0;
+                }
+                total = sum8_transposed(part, lane);
+            };
+            float sx;
+            if constexpr (REF) {
+                if (!ref_quantize(s.h_mid, static_cast<SharedRef&>(s).gamma_mid, 4 * L + 2, 1, L, sx, dots))
+                    return false;
+            } else {
+                if (!wait_ready(s, 4 * L + 2)) return false;
+                stamp(P.trace, b, 64 * L + 12 + 8 * bw, kAT + kWave * bw);
+                sx = s.sx[0];
+                v4u xc[kKCH];
 #pragma unroll
-            for (int k = 0; k < kGP; ++k) {
-                part[k] = has_g[k] ? row_part(w.g[k][0], xc, chunks, lane) : 0;
-                part[kGP + k] = has_g[k] ? row_part(w.g[k][1], xc, chunks, lane) : 0;
+                for (int j = 0; j < kKCH; ++j)
+                    xc[j] = *reinterpret_cast<const v4u*>(s.xq[0] + 16 * min(lane + kWave * j, chunks - 1));
+                dots(xc);
             }
-            const int total = sum8_transposed(part, lane);
             if ((lane & 7) == 0 && g_live) capture_acc<CAP>(P, L, 2, g_row, total);
             const float mine = dequant(total, sx, w.gs.scale, w.gs.bias);
             const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
@@ -1856,8 +2164,10 @@ __global__ __launch_bounds__(kT, 1) void decode_step_kernel(StepParams P) {
         s.abort = 0;
         s.pair[0][0] = s.pair[0][1] = s.pair[1][0] = s.pair[1][1] = 0;
     }
-    if constexpr (REF)
+    if constexpr (REF) {
         if (t < 32) s.exp2[t] = kExp2Table32[t];
+        if (t == 0) s.staged[0] = s.staged[1] = -1;
+    }
     {
         const int words = P.layers * (int)(sizeof(StepLayer) / 16);
         const v4u* src = reinterpret_cast<const v4u*>(P.layer);

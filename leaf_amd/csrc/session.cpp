@@ -7,6 +7,7 @@
 #include <cstdlib>
 #include <limits>
 #include <string>
+#include <vector>
 
 #include "runtime.h"
 
@@ -418,8 +419,21 @@ void Session::step_prepare() {
     };
     for (const Layer& L : m.layers) {
         if (!L.stacked_qkv || !L.stacked_gate_up || !per_row_int8(L.qkv) || !per_row_int8(L.o) ||
-            !per_row_int8(L.gate_up) || !per_row_int8(L.down) || L.input_norm.beta || L.post_norm.beta)
+            !per_row_int8(L.gate_up) || !per_row_int8(L.down) || L.input_norm.beta || L.post_norm.beta ||
+            !L.input_norm.gamma || !L.post_norm.gamma)
             return;
+    }
+    if (reference_) {
+        // In reference order the step quantizes each layer's two normalized
+        // inputs speculatively from x * gamma and confirms against the exact
+        // norm; its error bound holds for |gamma| up to 1e20.
+        std::vector<float> g(c.hidden);
+        for (const Layer& L : m.layers)
+            for (const float* gamma : {L.input_norm.gamma, L.post_norm.gamma}) {
+                hip_check(hipMemcpy(g.data(), gamma, g.size() * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+                for (float v : g)
+                    if (!(std::fabs(v) <= 1e20f)) return;
+            }
     }
     const int blocks = decode_step_blocks(m.context.device);
     if (!decode_step_fits(int(c.hidden), int(c.intermediate), int(c.heads), int(c.kv_heads), int(c.head_dim),
