@@ -158,18 +158,20 @@ __global__ __launch_bounds__(kRoBlock) void ro_attention_kernel(AttentionCall p)
 }
 
 // The same arithmetic for head dim 64, one block per (query token, KV head)
-// with one wave per query head of the group: the lanes are the keys for the
-// scores (q in scalar registers; the group's K rows of 64 keys staged in LDS
-// once by coalesced loads, then each lane's row read back) and the output
+// with one wave per HPW query heads of the group: the lanes are the keys for
+// the scores (q in scalar registers; the group's K rows of 64 keys staged in
+// LDS once by coalesced loads, then each lane's row read back) and the output
 // elements for p.v, so no lane idles through a dependent sum and many rows
-// share each SIMD.  The denominator is the plain in-order chain, every lane
-// forming it alike.  Blocks run from the last token down: the longest rows
-// start first.
+// share each SIMD.  A wave's HPW heads run their dependent sums side by side
+// (independent chains interleaved; one K row read and one V load serve all
+// of them).  The denominator is the plain in-order chain, every lane forming
+// it alike.  Blocks run from the last token down: the longest rows start
+// first.
 constexpr int kRoWaveDim = 64;
 constexpr int kRoWaveKeys = 12;    // keys per chunk of the p.v chain (three float4 of p)
-constexpr int kRoWaveDepth = 4;    // chunks of V in flight
+constexpr int kRoWaveDepth = 2;    // chunks of V in flight
 constexpr int kRoKPitch = kRoWaveDim + 4;   // floats per staged K row: lanes' 16-byte reads meet distinct banks
-constexpr int kRoMaxGroup = 16;    // query heads per KV head (waves per block)
+constexpr int kRoMaxGroup = 16;    // query heads per KV head
 // Floats of a row's scores: its keys rounded up to whole groups of chunks,
 // plus the chunk the chain reads ahead.
 __host__ __device__ constexpr int ro_wave_row_floats(int keys) {
@@ -178,33 +180,40 @@ __host__ __device__ constexpr int ro_wave_row_floats(int keys) {
 }
 // PER: 16-byte K loads per thread per 64 keys (64 * 16 / blockDim.x, rounded up
 // to a power of two); the next keys' loads are in flight while these are scored.
-template <int PER>
-__global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(AttentionCall p, int row_floats) {
+// HPW: query heads per wave (it divides the group); head i of wave w is w + i * (group / HPW).
+template <int PER, int HPW>
+__global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_kernel(AttentionCall p, int row_floats) {
     extern __shared__ float lds[];
     constexpr int dim = kRoWaveDim;
     constexpr int kRowBytes = dim * (int)sizeof(float);
-    const int group = p.heads / p.kv_heads;
+    const int group = p.heads / p.kv_heads, waves = group / HPW;
     const int lane = threadIdx.x & (kWave - 1), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = p.tokens - 1 - (int)blockIdx.x / p.kv_heads, kvh = (int)blockIdx.x % p.kv_heads;
-    const int h = kvh * group + w;
     const int position = p.position_ptr ? *p.position_ptr : p.position;
     const int end = position + t + 1;
     const int begin = (p.window && end > p.window) ? end - p.window : 0;
     const int n = end - begin;
     float* kt = lds;                                       // [kWave][kRoKPitch]: 64 keys' rows
-    float* sc = lds + kWave * kRoKPitch + w * row_floats;  // this head's scores, then exp, then p
-    const float* q = p.q_heads + ((size_t)h * p.tokens + t) * dim;
+    float* sc[HPW];                                        // each head's scores, then exp, then p
+    float qs[HPW][dim];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        const int gh = w + i * waves, h = kvh * group + gh;
+        sc[i] = lds + kWave * kRoKPitch + gh * row_floats;
+        const float* q = p.q_heads + ((size_t)h * p.tokens + t) * dim;
+#pragma unroll
+        for (int d = 0; d < dim; ++d) qs[i][d] = q[d];
+    }
     float* K = const_cast<float*>(p.keys) + ((size_t)kvh * p.capacity + begin) * dim;
     float* V = const_cast<float*>(p.values) + ((size_t)kvh * p.capacity + begin) * dim;
     // bounds-checked views of the n visible rows: rows past them read as 0
     const __amdgpu_buffer_rsrc_t kbuf = __builtin_amdgcn_make_buffer_rsrc(K, (short)0, n * kRowBytes, kRawBufferWord3);
     const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(V, (short)0, n * kRowBytes, kRawBufferWord3);
-    float qs[dim];
-#pragma unroll
-    for (int d = 0; d < dim; ++d) qs[d] = q[d];
     // scores (s += q[d] * k[d] in column order, then * scale * scale) and
-    // their maximum (NaN scores never become it, as with std::max)
-    float m = -INFINITY;
+    // their maxima (NaN scores never become one, as with std::max)
+    float m[HPW];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) m[i] = -INFINITY;
     v4u pre[PER];
     auto fetch = [&](int k0) {
 #pragma unroll
@@ -224,68 +233,114 @@ __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(
         }
         __syncthreads();
         if (k0 + kWave < n) fetch(k0 + kWave);
-        v4f kr[dim / 4];
+        // the row in two halves: 32 registers for it instead of 64
+        float s[HPW];
 #pragma unroll
-        for (int j = 0; j < dim / 4; ++j) kr[j] = *reinterpret_cast<const v4f*>(kt + lane * kRoKPitch + 4 * j);
-        float s = 0.0f;
+        for (int i = 0; i < HPW; ++i) s[i] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < dim; ++d) s = s + qs[d] * kr[d / 4][d % 4];
-        s = s * p.scale * p.scale;
+        for (int half = 0; half < 2; ++half) {
+            v4f kr[dim / 8];
+#pragma unroll
+            for (int j = 0; j < dim / 8; ++j)
+                kr[j] = *reinterpret_cast<const v4f*>(kt + lane * kRoKPitch + 4 * (j + half * dim / 8));
+#pragma unroll
+            for (int d = 0; d < dim / 2; ++d)
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) s[i] = s[i] + qs[i][d + half * dim / 2] * kr[d / 4][d % 4];
+        }
         const int key = k0 + lane;
-        if (key < n) {
-            sc[key] = s;
-            m = m < s ? s : m;
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) {
+            s[i] = s[i] * p.scale * p.scale;
+            if (key < n) {
+                sc[i][key] = s[i];
+                m[i] = m[i] < s[i] ? s[i] : m[i];
+            }
         }
     }
     // from here on each wave works alone (no block barrier)
+    float maximum[HPW];
+    bool live[HPW];   // a fully masked (or infinite) row: the CPU leaves the zero-filled output
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float other = __shfl_xor(m, off, kWave);
-        m = m < other ? other : m;
-    }
-    const float maximum = m;
-    float* o = p.out + ((size_t)t * p.heads + h) * dim;
-    if (!isfinite(maximum)) {   // fully masked (or infinite) row: the CPU leaves the zero-filled output
-        o[lane] = 0.0f;
-        return;
+    for (int i = 0; i < HPW; ++i) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float other = __shfl_xor(m[i], off, kWave);
+            m[i] = m[i] < other ? other : m[i];
+        }
+        maximum[i] = m[i];
+        live[i] = isfinite(maximum[i]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // exp(s - max) with glibc's expf, eight per lane at a time
-    for (int k0 = 0; k0 < n; k0 += 8 * kWave) {
-        float e[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int k = k0 + i * kWave + lane;
-            e[i] = (k < n ? sc[k] : 0.0f) - maximum;
-        }
-        libm_expf_batch(e, [](uint32_t k) { return kExp2Table32[k]; });
+    for (int i = 0; i < HPW; ++i)
+        for (int k0 = 0; k0 < n; k0 += 8 * kWave) {
+            float e[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int k = k0 + i * kWave + lane;
-            if (k < n) sc[k] = e[i];
+            for (int u = 0; u < 8; ++u) {
+                const int k = k0 + u * kWave + lane;
+                e[u] = (k < n ? sc[i][k] : 0.0f) - maximum[i];
+            }
+            libm_expf_batch(e, [](uint32_t k) { return kExp2Table32[k]; });
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int k = k0 + u * kWave + lane;
+                if (k < n) sc[i][k] = e[u];
+            }
         }
-    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // the denominator in key order, every lane alike
-    float den = 0.0f;
+    // the denominators in key order, every lane alike; groups of eight terms
+    // are read kRoDenAhead groups ahead of their adds, so the chains do not
+    // wait for LDS (the scores' registers are free by now)
+    float den[HPW];
     {
-        int k = 0;
-        for (; k + 8 <= n; k += 8) {
-            const v4f a = *reinterpret_cast<const v4f*>(sc + k), b = *reinterpret_cast<const v4f*>(sc + k + 4);
-            den = den + a[0];
-            den = den + a[1];
-            den = den + a[2];
-            den = den + a[3];
-            den = den + b[0];
-            den = den + b[1];
-            den = den + b[2];
-            den = den + b[3];
+        constexpr int kRoDenAhead = 3;
+        const int groups8 = n / 8;
+        v4f ring[kRoDenAhead][HPW][2];
+        auto read8 = [&](v4f (&r)[HPW][2], int g) {
+            const int at = 8 * min(g, max(groups8 - 1, 0));   // past the last group: read again, unused
+#pragma unroll
+            for (int i = 0; i < HPW; ++i) {
+                r[i][0] = *reinterpret_cast<const v4f*>(sc[i] + at);
+                r[i][1] = *reinterpret_cast<const v4f*>(sc[i] + at + 4);
+            }
+        };
+        auto add8 = [&](const v4f (&r)[HPW][2]) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) den[i] = den[i] + r[i][j / 4][j % 4];
+        };
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) den[i] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kRoDenAhead; ++u) read8(ring[u], u);
+        int g = 0;
+        for (; g + kRoDenAhead <= groups8; g += kRoDenAhead) {
+#pragma unroll
+            for (int u = 0; u < kRoDenAhead; ++u) {
+                v4f cur[HPW][2];
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) {
+                    cur[i][0] = ring[u][i][0];
+                    cur[i][1] = ring[u][i][1];
+                }
+                read8(ring[u], g + u + kRoDenAhead);
+                add8(cur);
+            }
         }
-        for (; k < n; ++k) den = den + sc[k];
+        // the last groups (fewer than kRoDenAhead) are already in the ring
+#pragma unroll
+        for (int u = 0; u < kRoDenAhead; ++u)
+            if (g + u < groups8) add8(ring[u]);
+        for (int k = 8 * groups8; k < n; ++k)
+#pragma unroll
+            for (int i = 0; i < HPW; ++i) den[i] = den[i] + sc[i][k];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -293,12 +348,14 @@ __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(
     // p = e / den; the slots past n hold +0, so the chain's reads past the
     // keys add p * v = +0 * 0, which leaves a sum that started at +0 unchanged
     const int slots = ro_wave_row_floats(n);
-    for (int k = lane; k < slots; k += kWave) sc[k] = k < n ? sc[k] / den : 0.0f;
+#pragma unroll
+    for (int i = 0; i < HPW; ++i)
+        for (int k = lane; k < slots; k += kWave) sc[i][k] = k < n ? sc[i][k] / den[i] : 0.0f;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // output[d] += p * v[d] in key order, lane d; kRoWaveDepth chunks of V in
-    // flight, each chunk's p read one chunk ahead
+    // output[d] += p * v[d] in key order, lane d, one chain per head;
+    // kRoWaveDepth chunks of V in flight, each chunk's p read one chunk ahead
     const int chunks = (n + kRoWaveKeys - 1) / kRoWaveKeys;
     const int groups = (chunks + kRoWaveDepth - 1) / kRoWaveDepth;
     float ring[kRoWaveDepth][kRoWaveKeys];
@@ -308,15 +365,20 @@ __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(
         for (int j = 0; j < kRoWaveKeys; ++j)
             r[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vbuf, at + j * kRowBytes, 0, 0));
     };
-    v4f pp[2][kRoWaveKeys / 4];
-    auto read_p = [&](v4f (&pr)[kRoWaveKeys / 4], int c) {
+    v4f pp[2][HPW][kRoWaveKeys / 4];
+    auto read_p = [&](v4f (&pr)[HPW][kRoWaveKeys / 4], int c) {
 #pragma unroll
-        for (int j = 0; j < kRoWaveKeys / 4; ++j) pr[j] = *reinterpret_cast<const v4f*>(sc + c * kRoWaveKeys + 4 * j);
+        for (int i = 0; i < HPW; ++i)
+#pragma unroll
+            for (int j = 0; j < kRoWaveKeys / 4; ++j)
+                pr[i][j] = *reinterpret_cast<const v4f*>(sc[i] + c * kRoWaveKeys + 4 * j);
     };
 #pragma unroll
     for (int u = 0; u < kRoWaveDepth; ++u) load(ring[u], u);
     read_p(pp[0], 0);
-    float acc = 0.0f;
+    float acc[HPW];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) acc[i] = 0.0f;
     static_assert(kRoWaveDepth % 2 == 0 && kRoWaveKeys == 12, "p pairs alternate; the wait names twelve values");
     for (int g = 0; g < groups; ++g) {
 #pragma unroll
@@ -324,17 +386,23 @@ __global__ __launch_bounds__(kRoMaxGroup * kWave) void ro_attention_wave_kernel(
             const int c = g * kRoWaveDepth + u;
             read_p(pp[(u + 1) & 1], c + 1);
             float (&r)[kRoWaveKeys] = ring[u];
-            v4f (&pq)[kRoWaveKeys / 4] = pp[u & 1];
             // one wait for the whole chunk
             asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
-                              "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(pq[0]), "+v"(pq[1]),
-                              "+v"(pq[2]));
+                              "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]));
 #pragma unroll
-            for (int j = 0; j < kRoWaveKeys; ++j) acc = acc + pp[u & 1][j / 4][j % 4] * ring[u][j];
+            for (int i = 0; i < HPW; ++i) asm volatile("" : "+v"(pp[u & 1][i][0]), "+v"(pp[u & 1][i][1]), "+v"(pp[u & 1][i][2]));
+#pragma unroll
+            for (int j = 0; j < kRoWaveKeys; ++j)
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) acc[i] = acc[i] + pp[u & 1][i][j / 4][j % 4] * ring[u][j];
             load(ring[u], c + kRoWaveDepth);
         }
     }
-    o[lane] = acc;
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        const int h = kvh * group + w + i * waves;
+        p.out[((size_t)t * p.heads + h) * dim + lane] = live[i] ? acc[i] : 0.0f;
+    }
 }
 
 // Single-token attention at head dim 64 (decode): the same arithmetic as
@@ -812,7 +880,7 @@ bool allow_lds(K kernel, size_t bytes, int& allowed) {
     allowed = (int)bytes;
     return true;
 }
-int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds[4] = {};
+int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds[7] = {};
 
 }  // namespace
 
@@ -853,16 +921,24 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
     if (p.dim == kRoWaveDim && group <= kRoMaxGroup) {
         const int row_floats = ro_wave_row_floats(max_keys);
         const size_t lds = ((size_t)kWave * kRoKPitch + (size_t)group * row_floats) * sizeof(float);
-        const int threads = group * kWave, per = (kWave * kRoWaveDim / 4 + threads - 1) / threads;
+        // two heads per wave when the group pairs up (their chains interleave),
+        // with at least two waves per block
+        const int hpw = group % 2 == 0 && group >= 4 ? 2 : 1;
+        const int threads = group / hpw * kWave, per = (kWave * kRoWaveDim / 4 + threads - 1) / threads;
         auto run = [&](auto kernel, int& allowed) {
             if (!allow_lds(kernel, lds, allowed)) return launch_attention_rows(p, max_keys, stream);
             kernel<<<p.kv_heads * p.tokens, threads, lds, stream>>>(p, row_floats);
             return true;
         };
-        if (per <= 2) return run(ro_attention_wave_kernel<2>, g_attention_wave_lds[0]);
-        if (per <= 4) return run(ro_attention_wave_kernel<4>, g_attention_wave_lds[1]);
-        if (per <= 8) return run(ro_attention_wave_kernel<8>, g_attention_wave_lds[2]);
-        return run(ro_attention_wave_kernel<16>, g_attention_wave_lds[3]);
+        if (hpw == 2) {
+            if (per <= 2) return run(ro_attention_wave_kernel<2, 2>, g_attention_wave_lds[4]);
+            if (per <= 4) return run(ro_attention_wave_kernel<4, 2>, g_attention_wave_lds[5]);
+            return run(ro_attention_wave_kernel<8, 2>, g_attention_wave_lds[6]);   // 128 threads or more
+        }
+        if (per <= 2) return run(ro_attention_wave_kernel<2, 1>, g_attention_wave_lds[0]);
+        if (per <= 4) return run(ro_attention_wave_kernel<4, 1>, g_attention_wave_lds[1]);
+        if (per <= 8) return run(ro_attention_wave_kernel<8, 1>, g_attention_wave_lds[2]);
+        return run(ro_attention_wave_kernel<16, 1>, g_attention_wave_lds[3]);
     }
     return launch_attention_rows(p, max_keys, stream);
 }
