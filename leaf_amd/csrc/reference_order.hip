@@ -294,42 +294,35 @@ __global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_k
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // the denominators in key order, every lane alike; groups of eight terms
-    // are read kRoDenAhead groups ahead of their adds, so the chains do not
-    // wait for LDS (the scores' registers are free by now)
+    // the denominators in key order: one chain per wave (with two heads,
+    // lanes 0-31 form the first head's and lanes 32-63 the second's, each
+    // lane alike within its half); groups of eight terms are read
+    // kRoDenAhead groups ahead of their adds, so the chain does not wait for
+    // LDS (the scores' registers are free by now)
+    static_assert(HPW <= 2, "one denominator chain per half-wave");
     float den[HPW];
     {
         constexpr int kRoDenAhead = 3;
         const int groups8 = n / 8;
-        v4f ring[kRoDenAhead][HPW][2];
-        auto read8 = [&](v4f (&r)[HPW][2], int g) {
+        const float* src = HPW == 2 && lane >= 32 ? sc[HPW - 1] : sc[0];
+        v4f ring[kRoDenAhead][2];
+        auto read8 = [&](v4f (&r)[2], int g) {
             const int at = 8 * min(g, max(groups8 - 1, 0));   // past the last group: read again, unused
-#pragma unroll
-            for (int i = 0; i < HPW; ++i) {
-                r[i][0] = *reinterpret_cast<const v4f*>(sc[i] + at);
-                r[i][1] = *reinterpret_cast<const v4f*>(sc[i] + at + 4);
-            }
+            r[0] = *reinterpret_cast<const v4f*>(src + at);
+            r[1] = *reinterpret_cast<const v4f*>(src + at + 4);
         };
-        auto add8 = [&](const v4f (&r)[HPW][2]) {
+        float chain = 0.0f;
+        auto add8 = [&](const v4f (&r)[2]) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int i = 0; i < HPW; ++i) den[i] = den[i] + r[i][j / 4][j % 4];
+            for (int j = 0; j < 8; ++j) chain = chain + r[j / 4][j % 4];
         };
-#pragma unroll
-        for (int i = 0; i < HPW; ++i) den[i] = 0.0f;
 #pragma unroll
         for (int u = 0; u < kRoDenAhead; ++u) read8(ring[u], u);
         int g = 0;
         for (; g + kRoDenAhead <= groups8; g += kRoDenAhead) {
 #pragma unroll
             for (int u = 0; u < kRoDenAhead; ++u) {
-                v4f cur[HPW][2];
-#pragma unroll
-                for (int i = 0; i < HPW; ++i) {
-                    cur[i][0] = ring[u][i][0];
-                    cur[i][1] = ring[u][i][1];
-                }
+                const v4f cur[2] = {ring[u][0], ring[u][1]};
                 read8(ring[u], g + u + kRoDenAhead);
                 add8(cur);
             }
@@ -338,9 +331,10 @@ __global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_k
 #pragma unroll
         for (int u = 0; u < kRoDenAhead; ++u)
             if (g + u < groups8) add8(ring[u]);
-        for (int k = 8 * groups8; k < n; ++k)
+        for (int k = 8 * groups8; k < n; ++k) chain = chain + src[k];
 #pragma unroll
-            for (int i = 0; i < HPW; ++i) den[i] = den[i] + sc[i][k];
+        for (int i = 0; i < HPW; ++i)
+            den[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, chain), 32 * i));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
