@@ -195,6 +195,9 @@ __global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_k
     const int n = end - begin;
     float* kt = lds;                                       // [kWave][kRoKPitch]: 64 keys' rows
     float* sc[HPW];                                        // each head's scores, then exp, then p
+    // expf's table after the group's rows (stored here, read after the first barrier below)
+    uint64_t* exp2 = reinterpret_cast<uint64_t*>(lds + kWave * kRoKPitch + group * row_floats);
+    if (threadIdx.x < 32) exp2[threadIdx.x] = kExp2Table32[threadIdx.x];
     float qs[HPW][dim];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_k
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // exp(s - max) with glibc's expf, eight per lane at a time
+    // exp(s - max) with glibc's expf (its table in LDS), eight per lane at a time
 #pragma unroll
     for (int i = 0; i < HPW; ++i)
         for (int k0 = 0; k0 < n; k0 += 8 * kWave) {
@@ -284,7 +287,7 @@ __global__ __launch_bounds__(kRoMaxGroup / HPW * kWave) void ro_attention_wave_k
                 const int k = k0 + u * kWave + lane;
                 e[u] = (k < n ? sc[i][k] : 0.0f) - maximum[i];
             }
-            libm_expf_batch(e, [](uint32_t k) { return kExp2Table32[k]; });
+            libm_expf_batch(e, [exp2](uint32_t k) { return exp2[k]; });
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int k = k0 + u * kWave + lane;
@@ -914,7 +917,8 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
     const int group = p.heads / p.kv_heads;
     if (p.dim == kRoWaveDim && group <= kRoMaxGroup) {
         const int row_floats = ro_wave_row_floats(max_keys);
-        const size_t lds = ((size_t)kWave * kRoKPitch + (size_t)group * row_floats) * sizeof(float);
+        const size_t lds = ((size_t)kWave * kRoKPitch + (size_t)group * row_floats) * sizeof(float) +
+                           32 * sizeof(uint64_t);   // expf's table
         // two heads per wave when the group pairs up (their chains interleave),
         // with at least two waves per block
         const int hpw = group % 2 == 0 && group >= 4 ? 2 : 1;
