@@ -82,6 +82,42 @@ __global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int w
         out[c] = (row[c] - mean) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
 }
 
+// RMSNorm (mean 0, the non-accurate policy) with the column-order square sum
+// formed by the block's two waves in parallel (wave_pair_sequential_sum:
+// the chain's bits in a fraction of its time; the squares are never
+// negative), one block per row.  Rows up to kSeqSumMaxPerLane * 64 wide.
+__global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, int width, NormView norm, float* y,
+                                                               int rows_per_group, size_t group_stride) {
+    extern __shared__ float lds[];
+    float4* area0 = reinterpret_cast<float4*>(lds);
+    float4* area1 = area0 + kSeqSumArea;
+    float4* xchg = area1 + kSeqSumArea;
+    float4* comp = xchg + kSeqPairXchg;
+    float* v = reinterpret_cast<float*>(comp + 2 * kSeqPairComp);   // the squares, in SeqLayout
+    const SeqLayout lay(width);
+    float* row = v + kWave * lay.E;                                  // the values, natural order
+    const size_t at = rows_per_group > 0 ? (size_t)(blockIdx.x / rows_per_group) * group_stride +
+                                               (size_t)(blockIdx.x % rows_per_group) * width
+                                         : (size_t)blockIdx.x * width;
+    const float* in = x + at;
+    float* out = y + at;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        const float value = in[c];
+        const float d = value - 0.0f;
+        row[c] = value;
+        v[lay.at(c)] = d * d;
+    }
+    seq_zero_tail(v, width, threadIdx.x, blockDim.x);
+    __syncthreads();
+    const int w = threadIdx.x / kWave;
+    float square;
+    wave_pair_sequential_sum(v, width, area0, area1, xchg, comp + w * kSeqPairComp, w,
+                             [] { __syncthreads(); return true; }, square);
+    const float scale = 1.0f / sqrtf(square / (float)width + norm.epsilon);
+    for (int c = threadIdx.x; c < width; c += blockDim.x)
+        out[c] = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+}
+
 // ------------------------------------------------------------- attention ---
 // One block per (query head, query token).  LDS holds q and the scores of the
 // visible keys; thread 0 sums the denominator; thread d < dim accumulates
@@ -877,7 +913,7 @@ bool allow_lds(K kernel, size_t bytes, int& allowed) {
     allowed = (int)bytes;
     return true;
 }
-int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds[7] = {};
+int g_norm_lds = 0, g_rms_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention_wave_lds[7] = {};
 
 }  // namespace
 
@@ -885,6 +921,14 @@ int g_norm_lds = 0, g_attention_lds = 0, g_attention_decode_lds = 0, g_attention
 bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
                                  hipStream_t stream, int rows_per_group, size_t group_stride) {
     if (width > kReferenceOrderMaxWidth) return false;
+    if (norm.kind == 0 && !norm.accurate && width <= kSeqSumMaxPerLane * kWave) {
+        const size_t lds = (size_t)(2 * kSeqSumArea + kSeqPairXchg + 2 * kSeqPairComp) * sizeof(float4) +
+                           ((size_t)seq_per_lane_host(width) * kWave + width) * sizeof(float);
+        if (allow_lds(ro_rms_norm_kernel, lds, g_rms_norm_lds)) {
+            ro_rms_norm_kernel<<<rows, 2 * kWave, lds, stream>>>(x, width, norm, y, rows_per_group, group_stride);
+            return true;
+        }
+    }
     const size_t lds = 2 * (size_t)width * sizeof(float);
     if (!allow_lds(ro_norm_kernel, lds, g_norm_lds)) return false;
     ro_norm_kernel<<<rows, kRoBlock, lds, stream>>>(x, width, norm, y, rows_per_group, group_stride);
