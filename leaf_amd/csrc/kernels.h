@@ -199,6 +199,12 @@ constexpr int kReferenceOrderMaxWidth = 16384;   // norm rows staged in LDS
 // norm() with sequential sums; false when width exceeds kReferenceOrderMaxWidth.
 bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
                                  hipStream_t stream, int rows_per_group = 0, size_t group_stride = 0);
+// The same RMSNorm rows (kind 0, not accurate, width up to
+// kReferenceOrderQuantizeMaxWidth) quantized per row as quantize_rows does:
+// int8 values into q, the per-row scale into scales (no FP32 output).
+constexpr int kReferenceOrderQuantizeMaxWidth = 2048;
+bool launch_norm_quantize_reference_order(const float* x, int rows, int width, const NormView& norm, int8_t* q,
+                                          float* scales, hipStream_t stream);
 // Most visible keys one query of the reference-order attention can score (LDS).
 int reference_order_attention_keys();
 // attention_impl order; `max_keys` bounds the visible keys of every query

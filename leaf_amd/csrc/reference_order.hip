@@ -86,8 +86,12 @@ __global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int w
 // formed by the block's two waves in parallel (wave_pair_sequential_sum:
 // the chain's bits in a fraction of its time; the squares are never
 // negative), one block per row.  Rows up to kSeqSumMaxPerLane * 64 wide.
+// With q set, the normalized row is quantized as quantize_rows_kernel does
+// (its maximum, exact in any order; the scale and int8 values into q and
+// scales) instead of stored.
 __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, int width, NormView norm, float* y,
-                                                               int rows_per_group, size_t group_stride) {
+                                                               int rows_per_group, size_t group_stride,
+                                                               int8_t* q = nullptr, float* scales = nullptr) {
     extern __shared__ float lds[];
     float4* area0 = reinterpret_cast<float4*>(lds);
     float4* area1 = area0 + kSeqSumArea;
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, 
                                                (size_t)(blockIdx.x % rows_per_group) * width
                                          : (size_t)blockIdx.x * width;
     const float* in = x + at;
-    float* out = y + at;
+    float* out = y ? y + at : nullptr;
     for (int c = threadIdx.x; c < width; c += blockDim.x) {
         const float value = in[c];
         const float d = value - 0.0f;
@@ -114,8 +118,27 @@ __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, 
     wave_pair_sequential_sum(v, width, area0, area1, xchg, comp + w * kSeqPairComp, w,
                              [] { __syncthreads(); return true; }, square);
     const float scale = 1.0f / sqrtf(square / (float)width + norm.epsilon);
-    for (int c = threadIdx.x; c < width; c += blockDim.x)
-        out[c] = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+    if (!q) {
+        for (int c = threadIdx.x; c < width; c += blockDim.x)
+            out[c] = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+        return;
+    }
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        const float value = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
+        row[c] = value;   // this thread's own columns
+        m = fmaxf(m, fabsf(value));
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    __shared__ float wave_max[2];
+    if ((threadIdx.x & (kWave - 1)) == 0) wave_max[w] = m;
+    __syncthreads();
+    const float sx = fmaxf(fmaxf(wave_max[0], wave_max[1]) / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+    if (threadIdx.x == 0) scales[blockIdx.x] = sx;
+    int8_t* qr = q + (size_t)blockIdx.x * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) qr[c] = (int8_t)quantize_one(row[c], multiplier);
 }
 
 // ------------------------------------------------------------- attention ---
@@ -918,6 +941,18 @@ int g_norm_lds = 0, g_rms_norm_lds = 0, g_attention_lds = 0, g_attention_decode_
 }  // namespace
 
 // --------------------------------------------------------------- launchers ---
+bool launch_norm_quantize_reference_order(const float* x, int rows, int width, const NormView& norm, int8_t* q,
+                                          float* scales, hipStream_t stream) {
+    static_assert(kReferenceOrderQuantizeMaxWidth == kSeqSumMaxPerLane * kWave, "the pair sum's width");
+    if (norm.kind != 0 || norm.accurate || width < 1 || width > kReferenceOrderQuantizeMaxWidth || rows < 1)
+        return false;
+    const size_t lds = (size_t)(2 * kSeqSumArea + kSeqPairXchg + 2 * kSeqPairComp) * sizeof(float4) +
+                       ((size_t)seq_per_lane_host(width) * kWave + width) * sizeof(float);
+    if (!allow_lds(ro_rms_norm_kernel, lds, g_rms_norm_lds)) return false;
+    ro_rms_norm_kernel<<<rows, 2 * kWave, lds, stream>>>(x, width, norm, nullptr, 0, 0, q, scales);
+    return true;
+}
+
 bool launch_norm_reference_order(const float* x, int rows, int width, const NormView& norm, float* y,
                                  hipStream_t stream, int rows_per_group, size_t group_stride) {
     if (width > kReferenceOrderMaxWidth) return false;

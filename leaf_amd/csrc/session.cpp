@@ -227,6 +227,23 @@ bool Session::prequantizes(const Linear& l, int tokens) const {
     return fuse_quantize_ && !reference_ && tokens > 1 && model.integer_linear(l) && !l.input_scale;
 }
 
+// Reference order: an integer linear after an RMSNorm takes its input from
+// the column-order norm kernel's own quantization (one launch, no FP32 rows).
+bool Session::reference_prequantizes(const Linear& l, int tokens, const NormView& n, int width) const {
+    return fuse_quantize_ && reference_ && tokens > 1 && model.integer_linear(l) && !l.input_scale && n.kind == 0 &&
+           !n.accurate && width <= kReferenceOrderQuantizeMaxWidth;
+}
+
+void Session::norm_prequantize(const float* x, int rows, int width, const NormView& n) {
+    timed(Profiler::Other, 0, 0, [&] {
+        if (reference_)
+            check(launch_norm_quantize_reference_order(x, rows, width, n, xq_.as<int8_t>(), xs_.as<float>(), stream()),
+                  "reference-order norm rejected", LH_ERROR_UNSUPPORTED);
+        else
+            launch_norm_quantize(x, rows, width, n, xq_.as<int8_t>(), xs_.as<float>(), stream());
+    });
+}
+
 void Session::norm(const float* x, int rows, int width, const NormView& n, float* y, int rows_per_group,
                    size_t group_stride) {
     if (reference_) {
@@ -709,11 +726,10 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
             run_linear(L.qkv, hidden, M, qkv, kStore, &input_norm, &rope);
         } else if (fuse_in) {
             run_linear(L.qkv, hidden, M, qkv, kStore, &input_norm);
-        } else if (L.stacked_qkv && prequantizes(L.qkv, M)) {
+        } else if (L.stacked_qkv &&
+                   (prequantizes(L.qkv, M) || reference_prequantizes(L.qkv, M, L.input_norm, h))) {
             // norm + per-token quantization in one launch, then the GEMM
-            timed(Profiler::Other, 0, 0, [&] {
-                launch_norm_quantize(hidden, M, h, L.input_norm, xq_.as<int8_t>(), xs_.as<float>(), s);
-            });
+            norm_prequantize(hidden, M, h, L.input_norm);
             run_linear(L.qkv, nullptr, M, qkv, kStore, nullptr, nullptr, true);
         } else {
             norm(hidden, M, h, L.input_norm, normed);
@@ -830,10 +846,9 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                 run_linear(L.gate_up, hid, rows, gate_up, kStore, &post_norm, &gated);
             } else if (fuse_post) {
                 run_linear(L.gate_up, hid, rows, gate_up, kStore, &post_norm);
-            } else if (L.stacked_gate_up && prequantizes(L.gate_up, rows)) {
-                timed(Profiler::Other, 0, 0, [&] {
-                    launch_norm_quantize(hid, rows, h, L.post_norm, xq_.as<int8_t>(), xs_.as<float>(), s);
-                });
+            } else if (L.stacked_gate_up &&
+                       (prequantizes(L.gate_up, rows) || reference_prequantizes(L.gate_up, rows, L.post_norm, h))) {
+                norm_prequantize(hid, rows, h, L.post_norm);
                 run_linear(L.gate_up, nullptr, rows, gate_up, kStore, nullptr, nullptr, true);
             } else {
                 norm(hid, rows, h, L.post_norm, normed);
