@@ -213,6 +213,11 @@ bool launch_attention_reference_order(const AttentionCall& call, int max_keys, h
 // activate() with glibc's expf for SiLU (GELU codes use the device's erff / tanhf).
 void launch_activation_reference_order(const float* gate_up, int tokens, int width, int gated, int activation,
                                        float* act, hipStream_t stream);
+// launch_activation_reference_order's values quantized per row as
+// quantize_rows does (int8 values into q, scales per row), in one launch;
+// false past 8192 columns.
+bool launch_activation_quantize_reference_order(const float* gate_up, int tokens, int width, int gated,
+                                                int activation, int8_t* q, float* scales, hipStream_t stream);
 // y[i] = expf(x[i]) as glibc computes it.
 void launch_libm_expf(const float* x, size_t count, float* y, hipStream_t stream);
 // sums[i] = the column-order f32 sum of row i of x [count, n] (norm()'s and

@@ -663,6 +663,43 @@ __global__ void ro_activation_kernel(const float* gate_up, int tokens, int width
     }
 }
 
+// ro_activation_kernel's values quantized per row as quantize_rows_kernel
+// does (an exact maximum, then the int8 values), one block per row: the
+// activation and its quantization in one launch, no FP32 rows.  Thread t
+// owns columns t + k * blockDim.x (k < K).
+template <int K>
+__global__ __launch_bounds__(1024) void ro_activation_quantize_kernel(const float* gate_up, int width, int gated,
+                                                                      int activation, int8_t* q, float* scales) {
+    __shared__ float wave_max[1024 / kWave];
+    const float* in = gate_up + (size_t)blockIdx.x * width * (gated ? 2 : 1);
+    float a[K];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = threadIdx.x + k * (int)blockDim.x;
+        float v = 0.0f;
+        if (j < width) v = gated ? in[width + j] * ro_activate(activation, in[j]) : ro_activate(activation, in[j]);
+        a[k] = v;
+        m = fmaxf(m, fabsf(v));
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    const int waves = (int)blockDim.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) wave_max[threadIdx.x / kWave] = m;
+    __syncthreads();
+    m = 0.0f;
+    for (int i = 0; i < waves; ++i) m = fmaxf(m, wave_max[i]);
+    const float sx = fmaxf(m / 127.0f, 1e-12f);
+    const float multiplier = 1.0f / sx;
+    if (threadIdx.x == 0) scales[blockIdx.x] = sx;
+    int8_t* out = q + (size_t)blockIdx.x * width;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = threadIdx.x + k * (int)blockDim.x;
+        if (j < width) out[j] = (int8_t)quantize_one(a[k], multiplier);
+    }
+}
+
 // One block per vector: the vector staged in LDS in wave_sequential_sum's
 // layout, then its column-order sum by that function (method 0, one wave),
 // by the plain chain (method 1) or by wave_pair_sequential_sum (method 2, two
@@ -1018,6 +1055,17 @@ bool launch_attention_reference_order(const AttentionCall& p, int max_keys, hipS
         return run(ro_attention_wave_kernel<16, 1>, g_attention_wave_lds[3]);
     }
     return launch_attention_rows(p, max_keys, stream);
+}
+
+bool launch_activation_quantize_reference_order(const float* gate_up, int tokens, int width, int gated,
+                                                int activation, int8_t* q, float* scales, hipStream_t stream) {
+    if (tokens < 1 || width < 1 || width > 8 * 1024) return false;
+    const int k = (width + 1023) / 1024;
+    if (k <= 2) ro_activation_quantize_kernel<2><<<tokens, 1024, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    else if (k <= 4) ro_activation_quantize_kernel<4><<<tokens, 1024, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    else if (k <= 6) ro_activation_quantize_kernel<6><<<tokens, 1024, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    else ro_activation_quantize_kernel<8><<<tokens, 1024, 0, stream>>>(gate_up, width, gated, activation, q, scales);
+    return true;
 }
 
 void launch_activation_reference_order(const float* gate_up, int tokens, int width, int gated, int activation,

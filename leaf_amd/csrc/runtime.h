@@ -237,6 +237,7 @@ private:
     bool prequantizes(const Linear& l, int tokens) const;
     bool reference_prequantizes(const Linear& l, int tokens, const NormView& n, int width) const;
     void norm_prequantize(const float* x, int rows, int width, const NormView& n);
+    bool reference_prequantizes_down(const Layer& L, int rows) const;
     bool fuse_quantize_ = true;   // LEAF_PREFILL_FUSE=0 turns the fused norm / activation quantization off
     bool reference_ = false;      // reference-order numerics (LH_NUMERICS_REFERENCE)
     bool reference_vnni_ = false; // grouped INT8 sums as quant_vnni_tile (two roundings)

@@ -234,6 +234,14 @@ bool Session::reference_prequantizes(const Linear& l, int tokens, const NormView
            !n.accurate && width <= kReferenceOrderQuantizeMaxWidth;
 }
 
+// Reference order: the gated activation before an integer down projection
+// quantized in the same launch (reference-order activation, exact maximum).
+bool Session::reference_prequantizes_down(const Layer& L, int rows) const {
+    const Config& c = model.config;
+    return fuse_quantize_ && reference_ && rows > 1 && c.gated && model.integer_linear(L.down) &&
+           !L.down.input_scale && c.intermediate <= 8 * 1024;
+}
+
 void Session::norm_prequantize(const float* x, int rows, int width, const NormView& n) {
     timed(Profiler::Other, 0, 0, [&] {
         if (reference_)
@@ -865,7 +873,7 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
                               "up staging");
                 }
             }
-            if (!fuse_act && !prequantizes(L.down, rows))
+            if (!fuse_act && !prequantizes(L.down, rows) && !reference_prequantizes_down(L, rows))
                 timed(Profiler::Other, 0, 0, [&] { activation(gate_up, rows, f, 1, act); });
         } else {
             // ungated MLP: a single-token FP up projection normalizes its input
@@ -887,17 +895,24 @@ void Session::launch(int M, size_t position, bool all_logits, const int* positio
         }
         const bool down_q = c.gated && prequantizes(L.down, rows) &&
                             !(rows == 1 && model.integer_linear(L.gate_up) && L.stacked_gate_up);
+        const bool ref_down_q = reference_prequantizes_down(L, rows);
         if (down_q) {
             // the gated activation and its quantization in one launch
             timed(Profiler::Other, 0, 0, [&] {
                 launch_activation_quantize(gate_up, rows, f, 1, int(c.activation), xq_.as<int8_t>(), xs_.as<float>(), s);
             });
+        } else if (ref_down_q) {
+            timed(Profiler::Other, 0, 0, [&] {
+                check(launch_activation_quantize_reference_order(gate_up, rows, f, 1, int(c.activation),
+                                                                 xq_.as<int8_t>(), xs_.as<float>(), s),
+                      "reference-order activation rejected", LH_ERROR_UNSUPPORTED);
+            });
         }
         if (!c.parallel) {
-            run_linear(L.down, act, rows, hid, kAccumulate, nullptr, nullptr, down_q);   // hidden += down(act) + b
+            run_linear(L.down, act, rows, hid, kAccumulate, nullptr, nullptr, down_q || ref_down_q);   // hidden += down(act) + b
         } else {
             float* proj = proj_.as<float>();
-            run_linear(L.down, act, rows, proj, kStore, nullptr, nullptr, down_q);
+            run_linear(L.down, act, rows, proj, kStore, nullptr, nullptr, down_q || ref_down_q);
             launch_residual(hid, proj, attn_proj, rows * h, s);              // hidden += proj + attn_proj
         }
         if (trim) hidden = hid + size_t(rows - 1) * h;   // the final norm and head see only the last row
