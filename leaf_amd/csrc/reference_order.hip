@@ -92,6 +92,9 @@ __global__ __launch_bounds__(kRoBlock) void ro_norm_kernel(const float* x, int w
 __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, int width, NormView norm, float* y,
                                                                int rows_per_group, size_t group_stride,
                                                                int8_t* q = nullptr, float* scales = nullptr) {
+    // thread t owns columns t + 128 k; every load of the row and its gamma is
+    // issued before the first use
+    constexpr int kThreads = 2 * kWave, kPer = kSeqSumMaxPerLane * kWave / kThreads;
     extern __shared__ float lds[];
     float4* area0 = reinterpret_cast<float4*>(lds);
     float4* area1 = area0 + kSeqSumArea;
@@ -99,17 +102,23 @@ __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, 
     float4* comp = xchg + kSeqPairXchg;
     float* v = reinterpret_cast<float*>(comp + 2 * kSeqPairComp);   // the squares, in SeqLayout
     const SeqLayout lay(width);
-    float* row = v + kWave * lay.E;                                  // the values, natural order
     const size_t at = rows_per_group > 0 ? (size_t)(blockIdx.x / rows_per_group) * group_stride +
                                                (size_t)(blockIdx.x % rows_per_group) * width
                                          : (size_t)blockIdx.x * width;
     const float* in = x + at;
-    float* out = y ? y + at : nullptr;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) {
-        const float value = in[c];
-        const float d = value - 0.0f;
-        row[c] = value;
-        v[lay.at(c)] = d * d;
+    float value[kPer], gamma[kPer], beta[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kThreads;
+        value[k] = c < width ? in[c] : 0.0f;
+        gamma[k] = c < width ? norm.gamma[c] : 0.0f;
+        beta[k] = c < width && norm.beta ? norm.beta[c] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kThreads;
+        const float d = value[k] - 0.0f;
+        if (c < width) v[lay.at(c)] = d * d;
     }
     seq_zero_tail(v, width, threadIdx.x, blockDim.x);
     __syncthreads();
@@ -118,16 +127,20 @@ __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, 
     wave_pair_sequential_sum(v, width, area0, area1, xchg, comp + w * kSeqPairComp, w,
                              [] { __syncthreads(); return true; }, square);
     const float scale = 1.0f / sqrtf(square / (float)width + norm.epsilon);
-    if (!q) {
-        for (int c = threadIdx.x; c < width; c += blockDim.x)
-            out[c] = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
-        return;
-    }
     float m = 0.0f;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) {
-        const float value = (row[c] - 0.0f) * scale * norm.gamma[c] + (norm.beta ? norm.beta[c] : 0.0f);
-        row[c] = value;   // this thread's own columns
-        m = fmaxf(m, fabsf(value));
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        value[k] = (value[k] - 0.0f) * scale * gamma[k] + beta[k];
+        m = fmaxf(m, fabsf(value[k]));   // columns past the row hold 0
+    }
+    if (!q) {
+        float* out = y + at;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int c = threadIdx.x + k * kThreads;
+            if (c < width) out[c] = value[k];
+        }
+        return;
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
@@ -138,7 +151,11 @@ __global__ __launch_bounds__(2 * kWave) void ro_rms_norm_kernel(const float* x, 
     const float multiplier = 1.0f / sx;
     if (threadIdx.x == 0) scales[blockIdx.x] = sx;
     int8_t* qr = q + (size_t)blockIdx.x * width;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) qr[c] = (int8_t)quantize_one(row[c], multiplier);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kThreads;
+        if (c < width) qr[c] = (int8_t)quantize_one(value[k], multiplier);
+    }
 }
 
 // ------------------------------------------------------------- attention ---
@@ -984,7 +1001,7 @@ bool launch_norm_quantize_reference_order(const float* x, int rows, int width, c
     if (norm.kind != 0 || norm.accurate || width < 1 || width > kReferenceOrderQuantizeMaxWidth || rows < 1)
         return false;
     const size_t lds = (size_t)(2 * kSeqSumArea + kSeqPairXchg + 2 * kSeqPairComp) * sizeof(float4) +
-                       ((size_t)seq_per_lane_host(width) * kWave + width) * sizeof(float);
+                       (size_t)seq_per_lane_host(width) * kWave * sizeof(float);
     if (!allow_lds(ro_rms_norm_kernel, lds, g_rms_norm_lds)) return false;
     ro_rms_norm_kernel<<<rows, 2 * kWave, lds, stream>>>(x, width, norm, nullptr, 0, 0, q, scales);
     return true;
@@ -995,7 +1012,7 @@ bool launch_norm_reference_order(const float* x, int rows, int width, const Norm
     if (width > kReferenceOrderMaxWidth) return false;
     if (norm.kind == 0 && !norm.accurate && width <= kSeqSumMaxPerLane * kWave) {
         const size_t lds = (size_t)(2 * kSeqSumArea + kSeqPairXchg + 2 * kSeqPairComp) * sizeof(float4) +
-                           ((size_t)seq_per_lane_host(width) * kWave + width) * sizeof(float);
+                           (size_t)seq_per_lane_host(width) * kWave * sizeof(float);
         if (allow_lds(ro_rms_norm_kernel, lds, g_rms_norm_lds)) {
             ro_rms_norm_kernel<<<rows, 2 * kWave, lds, stream>>>(x, width, norm, y, rows_per_group, group_stride);
             return true;
