@@ -111,17 +111,20 @@ def test_configured_span_decode_matches_prefill(rt, full_artifacts, family, math
 
 
 
-def test_tinyllama_fused_prefill_quantization_is_bit_identical(rt, full_artifacts, monkeypatch):
+@pytest.mark.parametrize("numerics", ["fast", "reference"])
+def test_tinyllama_fused_prefill_quantization_is_bit_identical(rt, full_artifacts, monkeypatch, numerics):
     """At TinyLlama's shapes the 512-token prefill splits K in the q|k|v, o and
     down GEMMs.  The norm / activation fused into the per-token quantization
     (default) or run as separate kernels (LEAF_PREFILL_FUSE=0) must give the
-    same logits for every token, and again on a second, shorter prefill."""
+    same logits for every token, and again on a second, shorter prefill; in
+    reference order the fused launches are the column-order RMSNorm and the
+    glibc-expf SiLU with their quantizations."""
     path = full_artifacts("tinyllama")
     prompt = np.random.default_rng(6).integers(0, 32000, 512).astype(np.uint32)
     runs = []
     for fuse in ("1", "0"):
         monkeypatch.setenv("LEAF_PREFILL_FUSE", fuse)
-        dec = rt.Decoder(path, 8, "fast", max_context=600, max_prefill=512)
+        dec = rt.Decoder(path, 8, "fast", max_context=600, max_prefill=512, numerics=numerics)
         first = dec.forward(prompt, all_logits=True)
         dec.reset()
         second = dec.forward(prompt[:40], all_logits=True)
